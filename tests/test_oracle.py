@@ -1,0 +1,374 @@
+"""Pin the CPU oracle before it judges anything (CPU only).
+
+Each check is chosen so that a plausible mistake in the oracle -- a dropped
+term, a wrong lane index, a reversed tree, a wrong tie-break, a lost lineage --
+fails one of them:
+
+  * golden vectors written from the reference's own _refcpu.py and CPU-torch
+    build stages (tests/golden/make_golden.py);
+  * closed forms: integer-valued inputs make every summation order exact;
+  * hand-built cases whose value depends on the lane layout and the tree order;
+  * brute force: complete graph, exact top-k, exact merge.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import gaussian, golden, regen
+
+F32MAX = np.finfo(np.float32).max
+
+
+# -- distance ----------------------------------------------------------------
+def test_distance_matches_reference_vectors():
+    g = golden("refcpu_distance.npz")
+    for i in range(int(g["n"])):
+        d, metric, team = (int(v) for v in g[f"c{i}_meta"])
+        q, x, x16 = g[f"c{i}_q"], g[f"c{i}_x"], g[f"c{i}_x16"]
+        got32 = O.team_distance(q, x[None, :], 0, metric, team)
+        got16 = O.team_distance(q, x16[None, :], 0, metric, team)
+        assert got32.tobytes() == g[f"c{i}_d32"].tobytes(), (d, metric, team, "fp32")
+        assert got16.tobytes() == g[f"c{i}_d16"].tobytes(), (d, metric, team, "fp16")
+
+
+@pytest.mark.parametrize("team", [4, 8, 16, 32, 64])
+@pytest.mark.parametrize("metric", [O.METRIC_IP, O.METRIC_L2])
+def test_distance_integer_inputs_are_exact(team, metric):
+    """Small integers: every partial sum is exact, so any order gives the
+    true value -- a dropped, doubled or misindexed term cannot hide."""
+    rng = np.random.default_rng(5)
+    for d in (1, 5, 8, 64, 96, 130, 1536):
+        q = rng.integers(-3, 4, d).astype(np.float32)
+        x = rng.integers(-3, 4, (3, d)).astype(np.float32)
+        for r in range(3):
+            if metric == O.METRIC_IP:
+                want = np.float32(1.0 - float(np.dot(q.astype(np.int64), x[r].astype(np.int64))))
+            else:
+                want = np.float32(float(((q - x[r]).astype(np.int64) ** 2).sum()))
+            assert O.team_distance(q, x, r, metric, team) == want
+            assert O.team_distance(q, x.astype(np.float16), r, metric, team) == want
+
+
+def test_distance_lane_layout_fp32():
+    """team=2, vec=4: lane 0 owns elements 0-3 and 8-11, lane 1 owns 4-7 and
+    12-15.  2^24 and -2^24 both fall to lane 0, so the 1s in lane 1 survive:
+    the kernel's order gives 2; summing in element order would give 0."""
+    q = np.ones(16, np.float32)
+    x = np.zeros(16, np.float32)
+    x[0], x[4], x[5], x[8] = 2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)
+    assert O.team_distance(q, x[None], 0, O.METRIC_IP, 2) == np.float32(1 - 2)
+    # within lane 0 the order is sequential: 2^24 + 1 + 1 rounds back to 2^24
+    x2 = np.zeros(16, np.float32)
+    x2[0], x2[1], x2[2], x2[8] = 2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)
+    assert O.team_distance(q, x2[None], 0, O.METRIC_IP, 2) == np.float32(1 - 0)
+
+
+def test_distance_lane_layout_fp16():
+    """fp16 reads 8 elements per lane per step: with team=2 lane 0 owns 0-7
+    and 16-23, lane 1 owns 8-15.  Products 2^13*2048 = 2^24 at 0 and -2^24 at
+    16 cancel in lane 0 and the 1 at element 8 survives in lane 1: result 1.
+    With vec=4 element 8 would join lane 0 between them and be rounded away
+    (2^24 + 1 = 2^24), giving 0."""
+    q = np.ones(32, np.float32)
+    q[0] = q[16] = 2.0 ** 13
+    x = np.zeros(32, np.float16)
+    x[0], x[8], x[16] = 2048, 1, -2048
+    assert O.team_distance(q, x[None], 0, O.METRIC_IP, 2) == np.float32(1 - 1)
+
+
+def test_distance_tree_is_halving_from_the_top():
+    """team=4, one value per lane: [2^24, 1, -2^24, 1].  Folding off=2 then
+    off=1 gives (2^24 - 2^24) + (1 + 1) = 2; folding off=1 first would give 1."""
+    q = np.ones(16, np.float32)
+    x = np.zeros(16, np.float32)
+    x[0], x[4], x[8], x[12] = 2.0 ** 24, 1.0, -(2.0 ** 24), 1.0
+    assert O.team_distance(q, x[None], 0, O.METRIC_IP, 4) == np.float32(1 - 2)
+
+
+def test_distance_l2_is_rounded_square_then_sum():
+    """L2 terms are fl(fl(q-x)^2): q - x = 1 + 2^-12 squares to 1 + 2^-11 +
+    2^-24, whose last bit fp32 rounds away (ties to even)."""
+    q = np.array([1.0 + 2.0 ** -12, 0, 0, 0], np.float32)
+    x = np.zeros((1, 4), np.float32)
+    assert O.team_distance(q, x, 0, O.METRIC_L2, 4) == np.float32(1.0 + 2.0 ** -11)
+
+
+def test_half_conversion_is_exact():
+    h = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    L = O.lib()
+    got = np.array([L.so_half_to_float_export(int(v)) for v in h[::97]], np.float32)
+    want = f[::97]
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+# -- one branch -------------------------------------------------------------
+def _check_branch(br, g, key, L, what):
+    ids = g[f"{key}_ids"]; dist = g[f"{key}_dist"]; expd = g[f"{key}_expanded"]
+    lin = g[f"{key}_lineage"]; ctr = g[f"{key}_counters"]
+    n = int((ids >= 0).sum())
+    assert list(br.ids[:n]) == list(ids[:n]) and (br.ids[n:] == -1).all(), what
+    assert br.dist[:n].tobytes() == dist[:n].tobytes(), what
+    assert list(br.expanded[:n]) == list(expd[:n]), what
+    assert list(br.lineage[:n]) == list(lin[:n]), what
+    assert br.counters[0] == ctr[0] and br.counters[1] == ctr[1], what
+    assert int(br.counters[3]) == int(ctr[2]), what
+
+
+@pytest.mark.parametrize("tag,metric", [("ip", O.METRIC_IP), ("l2", O.METRIC_L2)])
+def test_branch_matches_refcpu_every_team(tag, metric):
+    g = golden("refcpu_branch.npz")
+    X = regen(2000, 64, 0, metric == O.METRIC_IP, g[f"{tag}_X_sha"])
+    G = g[f"{tag}_G"].astype(np.int32); Q = g[f"{tag}_Q"]; seeds = g[f"{tag}_seeds"]
+    for team in (4, 8, 16, 32):
+        for q in range(Q.shape[0]):
+            for j in range(seeds.shape[1]):
+                br = O.run(X, G, Q[q], int(seeds[q, j]), L=16, B=12, metric=metric, team=team)
+                sub = {k[len(f"{tag}_t{team}_"):]: v[q, j] for k, v in g.items()
+                       if k.startswith(f"{tag}_t{team}_")}
+                _check_branch(br, {f"x_{k}": v for k, v in sub.items()}, "x", 16,
+                              (tag, team, q, j))
+
+
+@pytest.mark.parametrize("pol", [O.POLICY_BEST, O.POLICY_ROUND_ROBIN])
+def test_multiseed_matches_refcpu(pol):
+    g = golden("refcpu_branch.npz")
+    X = regen(2000, 64, 53, True, g["ms_X_sha"])
+    G = g["ms_G"].astype(np.int32); Q = g["ms_Q"]; seeds = g["ms_seeds"]
+    for q in range(Q.shape[0]):
+        br = O.run(X, G, Q[q], list(seeds[q]), L=32, B=20, policy=pol)
+        _check_branch(br, {f"x_{n}": g[f"ms_p{pol}_{n}"][q] for n in
+                           ("ids", "dist", "expanded", "lineage", "counters")}, "x", 32, (pol, q))
+
+
+def test_early_stop_matches_refcpu():
+    g = golden("refcpu_branch.npz")
+    X = regen(2000, 64, 71, True, g["es_X_sha"])
+    G = g["es_G"].astype(np.int32); Q = g["es_Q"]; seeds = g["es_seeds"]
+    for e, eps in enumerate((0.0, 0.1, 0.25)):
+        for q in range(Q.shape[0]):
+            br = O.run(X, G, Q[q], list(seeds[q]), L=32, B=64, policy=O.POLICY_ROUND_ROBIN,
+                       stop_eps=eps, kstop=10)
+            _check_branch(br, {f"x_{n}": g[f"es_e{e}_{n}"][q] for n in
+                               ("ids", "dist", "expanded", "lineage", "counters")}, "x", 32,
+                          (eps, q))
+            assert br.counters[0] < 64
+
+
+def test_complete_graph_equals_brute_force():
+    """tests/test_engine.py:122-142: one expansion over a complete graph sees
+    every node, so the queue is the exact top-L."""
+    n, d, L = 96, 48, 16
+    rng = np.random.default_rng(17)
+    X = gaussian(n, d, 17, True)
+    G = np.stack([np.delete(np.arange(n), i) for i in range(n)]).astype(np.int32)[:, :95]
+    Q = gaussian(6, d, 18, True)
+    for qi in range(6):
+        br = O.run(X, G, Q[qi], 0, L=L, B=1)
+        exact = 1.0 - (Q[qi].astype(np.float64) @ X.astype(np.float64).T)
+        want = np.argsort(exact, kind="stable")[:L]
+        # node 0 is the seed and is never its own neighbour; it is in the
+        # queue only if it ranks, which the brute force also says
+        assert list(br.ids) == list(want)
+        assert np.allclose(br.dist, exact[want], atol=2e-6)
+    del rng
+
+
+def test_dead_branch_and_sink():
+    n, d = 64, 16
+    X = gaussian(n, d, 19, True)
+    G = np.full((n, 8), -1, np.int32)
+    q = gaussian(1, d, 20, True)[0]
+    br = O.run(X, G, q, 0, L=16, B=16)
+    assert br.counters[0] == 1 and br.counters[3] == 1
+    br = O.run(X, G, q, -1, L=16, B=16)
+    assert br.counters[0] == 0 and br.counters[3] == 1 and (br.ids == -1).all()
+
+
+def test_resume_equivalence():
+    X = gaussian(2000, 64, 3, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    Q = gaussian(4, 64, 4, True)
+    for qi in range(4):
+        one = O.init_branch(X, Q[qi], [qi * 7], L=32, B=24, D=32)
+        O.advance_branch(X, G, Q[qi], one, 24, 24)
+        for split in (1, 2, 7, 23):
+            two = O.init_branch(X, Q[qi], [qi * 7], L=32, B=24, D=32)
+            O.advance_branch(X, G, Q[qi], two, split, 24)
+            O.advance_branch(X, G, Q[qi], two, 24 - split, 24)
+            for f in ("ids", "dist", "expanded", "lineage", "visited", "counters"):
+                assert np.array_equal(getattr(one, f), getattr(two, f)), (qi, split, f)
+
+
+def test_budget_is_a_state_property():
+    X = gaussian(2000, 64, 5, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    q = gaussian(1, 64, 6, True)[0]
+    br = O.init_branch(X, q, [3, 99], L=16, B=10, D=32)
+    O.advance_branch(X, G, q, br, 100, 10)
+    assert br.counters[0] == 10
+
+
+def test_visited_overflow_is_counted():
+    X = gaussian(1000, 64, 23, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    q = gaussian(1, 64, 24, True)[0]
+    br = O.init_branch(X, q, [0], L=16, H=64, B=16, D=32)
+    O.advance_branch(X, G, q, br, 16, 16)
+    assert br.counters[2] > 0
+
+
+# -- several branches of one query --------------------------------------------
+def test_shared_cache_changes_work_not_results():
+    """tests/test_engine.py:213-239, in the serial schedule."""
+    X = gaussian(2000, 64, 79, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    Q = gaussian(6, 64, 80, True)
+    rng = np.random.default_rng(83)
+    for qi in range(6):
+        seeds = rng.integers(0, 2000, 24).astype(np.int32)
+        plain = O.search_query(X, G, Q[qi], seeds, L=32, B=12)
+        Hc = O.cache_size(24, 12, 32)
+        cached = O.search_query(X, G, Q[qi], seeds, L=32, B=12, Hc=Hc)
+        for f in ("ids", "dist", "expanded", "lineage"):
+            assert np.array_equal(plain[f], cached[f]), f
+        a = plain["counters"][:, 1].sum(); b = cached["counters"][:, 1].sum()
+        hits = cached["counters"][:, 4].sum()
+        assert b < a and a - b == hits
+
+
+def test_claims_keep_branches_disjoint():
+    """Exclusive claims with the visited table elided: a node scored by one
+    branch is never entered by another (seeds aside, which are not claimed)."""
+    X = gaussian(2000, 64, 81, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    q = gaussian(1, 64, 82, True)[0]
+    seeds = np.random.default_rng(84).integers(0, 2000, 16).astype(np.int32)
+    Hc = O.cache_size(16, 16, 32)
+    r = O.search_query(X, G, q, seeds, L=12, B=16, H=1, Hc=Hc, bound=True, exclusive=True,
+                       stop_eps=0.05)
+    owner = {}
+    for j in range(16):
+        for i in r["ids"][j]:
+            if i < 0 or i in set(seeds.tolist()):
+                continue
+            assert owner.setdefault(int(i), j) == j
+    # every cached distance is the exact team distance
+    for slot in np.nonzero(r["cache_id"])[0][:50]:
+        v = int(r["cache_id"][slot]) - 1
+        assert r["cache_d"][slot] == O.team_distance(q, X, v, O.METRIC_IP, 32)
+
+
+# -- merge ----------------------------------------------------------------------
+def test_merge_is_a_dedup_selection():
+    rng = np.random.default_rng(37)
+    Q, V, kk, k = 20, 5, 10, 10
+    ids = rng.integers(-1, 40, (Q, V, kk)).astype(np.int32)
+    base = rng.random(40).astype(np.float32)
+    dist = np.where(ids >= 0, base[np.clip(ids, 0, None)], F32MAX).astype(np.float32)
+    oi, od = O.merge(ids, dist, k)
+    for q in range(Q):
+        pool = {}
+        for j in range(V):
+            for t in range(kk):
+                if ids[q, j, t] >= 0:
+                    pool.setdefault(int(ids[q, j, t]), float(dist[q, j, t]))
+        want = sorted(pool.items(), key=lambda kv: (kv[1], kv[0]))[:k]
+        got = [(int(i), float(d)) for i, d in zip(oi[q], od[q]) if i >= 0]
+        assert got == [(i, float(np.float32(d))) for i, d in want]
+        assert (oi[q, len(want):] == -1).all() and np.isinf(od[q, len(want):]).all()
+
+
+# -- config C1 against the reference path ----------------------------------------
+def test_c1_branches_match_refcpu():
+    g = golden("refcpu_c1.npz")
+    X = regen(10000, 128, 0, True, g["X_sha"])
+    G = g["G"].astype(np.int32); Q = g["Q"]; seeds = g["seeds"].astype(np.int32)
+    for q in range(0, 200, 5):
+        for j in range(8):
+            br = O.run(X, G, Q[q], int(seeds[q, j]), L=12, B=64, metric=O.METRIC_IP, team=16,
+                       stop_eps=0.05, kstop=10)
+            n = int((g["ids"][q, j] >= 0).sum())
+            assert list(br.ids[:n]) == list(g["ids"][q, j, :n].astype(np.int32)), (q, j)
+            assert br.dist[:n].tobytes() == g["dist"][q, j, :n].tobytes(), (q, j)
+            assert br.counters[0] == g["counters"][q, j, 0]
+            assert br.counters[1] == g["counters"][q, j, 1]
+
+
+def test_c1_merged_answer_matches_reference():
+    g = golden("refcpu_c1.npz")
+    X = regen(10000, 128, 0, True, g["X_sha"])
+    G = g["G"].astype(np.int32); Q = g["Q"]; seeds = g["seeds"].astype(np.int32)
+    oi, od = O.search_batch(X, G, Q, seeds, k=10, L=12, B=64, metric=O.METRIC_IP, team=16,
+                            stop_eps=0.05, nthreads=4)
+    assert np.array_equal(oi, g["merged_ids"].astype(np.int32))
+    assert od.tobytes() == g["merged_dist"].astype(np.float32).tobytes()
+
+
+def test_c1_select_matches_reference():
+    """_select.py:93-128 in fp32: the E=8 nearest catalogue rows."""
+    g = golden("refcpu_c1.npz")
+    X = regen(10000, 128, 0, True, g["X_sha"])
+    cat = g["catalogue"].astype(np.int64)
+    want = np.random.default_rng(0).permutation(10000)[:4096]
+    assert np.array_equal(cat, np.sort(want))
+    idx, _ = O.select_nearest(g["Q"], X[cat], 8, O.METRIC_IP, nthreads=4)
+    got = cat[idx].astype(np.int32)
+    agree = (got == g["seeds"].astype(np.int32)).mean()
+    assert agree > 0.995, agree
+
+
+# -- build stages ---------------------------------------------------------------
+@pytest.mark.parametrize("tag,metric", [("ip", O.METRIC_IP), ("l2", O.METRIC_L2)])
+def test_sweep_matches_reference(tag, metric):
+    g = golden("refbuild_small.npz")
+    X = g[f"{tag}_X"]
+    cand, cdist = O.knn_candidates(X, 32, metric, nthreads=4)
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    assert (cand == rc).mean() > 0.99
+    assert np.allclose(cdist, rd, atol=2e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("tag,metric", [("ip", O.METRIC_IP), ("l2", O.METRIC_L2)])
+def test_prune_and_reverse_match_reference(tag, metric):
+    g = golden("refbuild_small.npz")
+    X = g[f"{tag}_X"]
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    Gp = O.robust_prune(X, rc, rd, 16, 1.2, metric, nthreads=4)
+    want_p = g[f"{tag}_Gp"].astype(np.int32)
+    rows_p = (Gp == want_p).all(1).mean()
+    assert rows_p > 0.98, rows_p
+    Gf = O.add_reverse(X, want_p, 16, 1.2, 64, metric, nthreads=4)
+    want_f = g[f"{tag}_Gf"].astype(np.int32)
+    same_sets = np.mean([set(a) == set(b) for a, b in zip(Gf, want_f)])
+    assert same_sets > 0.97, same_sets
+
+
+def test_prune_rule_invariants():
+    """DiskANN's rule, stated as invariants: every kept edge has no kept,
+    nearer neighbour that is alpha-closer to it; every dropped candidate
+    (before the row filled) has one."""
+    X = gaussian(400, 16, 31, False)
+    cand, cdist = O.knn_candidates(X, 24, O.METRIC_L2)
+    G = O.robust_prune(X, cand, cdist, 8, 1.2, O.METRIC_L2)
+    X64 = X.astype(np.float64)
+    for u in range(0, 400, 7):
+        kept = [c for c in G[u] if c >= 0]
+        pos = {int(c): i for i, c in enumerate(cand[u])}
+        assert [pos[c] for c in kept] == sorted(pos[c] for c in kept)
+        for i, c in enumerate(cand[u]):
+            if len([k for k in kept if pos[k] < i]) >= 8:
+                break
+            blockers = [w for w in kept if pos[w] < i and
+                        1.2 * ((X64[w] - X64[c]) ** 2).sum() <= cdist[u, i] + 1e-4]
+            if c in kept:
+                assert not [w for w in kept if pos[w] < i and
+                            1.2 * ((X64[w] - X64[c]) ** 2).sum() <= cdist[u, i] - 1e-4]
+            else:
+                assert blockers
