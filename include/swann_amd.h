@@ -1,0 +1,159 @@
+/*
+ * swann_amd.h -- C ABI of the MI355X (gfx950) library behind swann_amd.
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream passed
+ * as `void*` (0 = the null stream); nothing here names a torch or HIP type.
+ * Calls are asynchronous on that stream.  All return 0 on success or a
+ * negative SWANN_E_* code; swann_last_error() then holds a message for the
+ * calling thread.  No entry point on the search path allocates device memory:
+ * state and workspaces are owned by the caller, so a search can be captured
+ * in a hipGraph.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   swann_init_states      swann/csrc/local_search.cu:741-776  (pybind init_states)
+ *   swann_advance          swann/csrc/local_search.cu:778-841  (pybind advance)
+ *   swann_merge_branches   swann/csrc/local_search.cu:925-947  (pybind merge_branches)
+ *   swann_select_nearest   swann/_select.py:93-128             (select_nearest)
+ *   swann_build_sweep      swann/build.py:28-43                (knn_candidates)
+ *   swann_build_prune      swann/build.py:46-91                (robust_prune)
+ *   swann_build_reverse    swann/build.py:94-150               (add_reverse)
+ *   swann_overflow_async   swann/_engine.py:155-173            (SearchState.check / overflow)
+ *   swann_validate_*       the TORCH_CHECKs of local_search.cu:726-841, host only
+ */
+#ifndef SWANN_AMD_H
+#define SWANN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes */
+#define SWANN_OK 0
+#define SWANN_E_INVALID (-1)   /* an argument failed validation */
+#define SWANN_E_LAUNCH (-2)    /* the HIP runtime refused a launch */
+#define SWANN_E_UNSUPPORTED (-3)
+#define SWANN_E_NODEVICE (-4)
+
+/* constants shared with the Python layer (local_search.cu:32-42, _engine.py:31-37) */
+#define SWANN_METRIC_IP 0      /* distance = 1 - <q, x>; rows L2-normalised */
+#define SWANN_METRIC_L2 1      /* distance = ||q - x||^2 */
+#define SWANN_POLICY_BEST 0
+#define SWANN_POLICY_ROUND_ROBIN 1
+#define SWANN_DTYPE_F32 0
+#define SWANN_DTYPE_F16 1
+#define SWANN_NCTR 10          /* counters per branch, layout of local_search.cu:35-41 */
+#define SWANN_MAXL 512         /* queue width limit */
+#define SWANN_MAXD 128         /* graph out-degree limit */
+#define SWANN_MAXV 128         /* seeds per branch (init sort buffer) */
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* swann_last_error(void);
+
+/* Library version string and the gfx target it was built for. */
+const char* swann_version(void);
+
+/* Number of HIP devices visible (0 on a machine without a GPU). */
+int swann_device_count(void);
+
+/* ---- search state ------------------------------------------------------
+ * Layout (all row-major, contiguous):
+ *   X        [n, dim]  fp32 or fp16 (x_dtype)     corpus
+ *   Qv       [Q, dim]  fp32                       queries
+ *   seeds    [Q, J, V] int32, -1 = empty
+ *   G        [n, D]    int32, -1 = no edge
+ *   ids      [Q, J, L] int32, dist [Q, J, L] fp32, expd/lin [Q, J, L] uint8
+ *   visited  [Q, J, H] int32 (H a power of two; H == 1 disables it)
+ *   counters [Q, J, SWANN_NCTR] int32
+ *   cache_id [Q, Hc] int32, cache_d [Q, Hc] fp32 (Hc a power of two; 0 = off)
+ *   bound    [Q] fp32 or NULL
+ * A disabled feature is a NULL pointer (and Hc = 0), matching the
+ * reference's empty-tensor convention (swann/_engine.py:269-274).
+ */
+
+/* Host-only validation of init_states arguments (no GPU needed). */
+int swann_validate_init(int64_t n, int dim, int x_dtype, int64_t Q, int J, int V, int L,
+                        int H, int metric, int team_size, int Hc);
+
+/* Host-only validation of advance arguments (no GPU needed). */
+int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, int J, int L,
+                           int H, int metric, int team_size, int policy, int V, int Hc,
+                           int64_t nactive, int has_codes);
+
+/* Seed every branch, clear the per-query table and bound (init_kernel,
+ * local_search.cu:271-351). */
+int swann_init_states(const void* X, int x_dtype, int64_t n, int dim,
+                      const float* Qv, int64_t Q, const int32_t* seeds, int J, int V,
+                      int32_t* ids, float* dist, uint8_t* expd, uint8_t* lin, int L,
+                      int32_t* visited, int H, int32_t* counters,
+                      int metric, int team_size,
+                      int32_t* cache_id, float* cache_d, int Hc, float* bound,
+                      void* stream);
+
+/* Up to `delta` best-first expansions per branch, in place (advance_kernel,
+ * local_search.cu:353-688).  `active` (nactive entries of flattened q*J+j)
+ * restricts the grid to those branches; NULL = all Q*J.  The sign-code filter
+ * arguments (codes, cwords, alpha, cmu, code_margin) must be NULL/0: the
+ * filter is not built yet and a non-NULL `codes` is refused. */
+int swann_advance(const void* X, int x_dtype, int64_t n, int dim,
+                  const int32_t* G, int D, const float* Qv, int64_t Q, int J,
+                  int32_t* ids, float* dist, uint8_t* expd, uint8_t* lin, int L,
+                  int32_t* visited, int H, int32_t* counters,
+                  int metric, int team_size, int delta, int max_expansions,
+                  int policy, int V, float stop_eps, int kstop,
+                  int32_t* cache_id, float* cache_d, int Hc, float* bound, int exclusive,
+                  int stall_patience, float crowd_frac,
+                  const int32_t* active, int64_t nactive,
+                  const int32_t* codes, int cwords, const float* alpha, const float* cmu,
+                  float code_margin, void* stream);
+
+/* Per-query dedup top-k of branch results (merge_branches_kernel,
+ * local_search.cu:863-919).  bids/bdist [Q, V, kk] -> out [Q, k]; missing
+ * entries are (-1, +inf).  Needs V*kk <= 8192. */
+int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk,
+                         int k, int32_t* out_ids, float* out_dist, void* stream);
+
+/* Sum of counters[..., 2] (visited-table overflows) over nbranch branches,
+ * written to *out (device or host-pinned memory) without a host sync. */
+int swann_overflow_async(const int32_t* counters, int64_t nbranch, int32_t* out, void* stream);
+
+/* ---- seed selection ----------------------------------------------------
+ * The E nearest catalogue rows per query (_select.py:93-128), ascending by
+ * distance, as int32 row indices into Vp.  Q [nq, dim] fp32, Vp [P, dim] fp32.
+ * Distances: 1 - <q, v> (IP) or ||v||^2 - 2<q, v> + ||q||^2 (L2).
+ * `workspace` must hold swann_select_workspace_size(nq, P) bytes. */
+int64_t swann_select_workspace_size(int64_t nq, int64_t P);
+int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P,
+                         int E, int metric, int32_t* out_idx, float* out_dist,
+                         void* workspace, void* stream);
+
+/* ---- graph build -------------------------------------------------------
+ * Sweep (build.py:28-43): exact top-C neighbours of every row, self
+ * excluded, ascending, as (cand [n, C] int32, cdist [n, C] fp32).  Scores
+ * are screened with bf16 MFMA tiles over a bf16 copy of X and the survivors
+ * re-ranked in fp32 (IP: 1 - <a,b>; L2: max(0, |b|^2 - 2<a,b> + |a|^2)).
+ * X [n, dim] fp32.  `workspace`: swann_sweep_workspace_size bytes. */
+int64_t swann_sweep_workspace_size(int64_t n, int dim, int C);
+int swann_build_sweep(const float* X, int64_t n, int dim, int metric, int C,
+                      int32_t* cand, float* cdist, void* workspace, void* stream);
+
+/* Prune (build.py:46-91): keep candidate i of node u unless an already kept
+ * w satisfies alpha * d(w, i) <= d(u, i); deg kept ids per row, -1 padded. */
+int swann_build_prune(const float* X, int64_t n, int dim, int metric, const int32_t* cand,
+                      const float* cdist, int C, int deg, float alpha, int32_t* out,
+                      void* stream);
+
+/* Reverse (build.py:94-150): offer every edge u->v back to v (ascending
+ * source, at most max_in per target), dedup [G_u | in_u] minus self, score
+ * exactly, keep the nearest 128 and prune to deg.
+ * `workspace`: swann_reverse_workspace_size bytes. */
+int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in);
+int swann_build_reverse(const float* X, int64_t n, int dim, int metric, const int32_t* G,
+                        int deg, float alpha, int max_in, int32_t* out, void* workspace,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SWANN_AMD_H */

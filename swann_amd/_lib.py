@@ -1,0 +1,87 @@
+"""ctypes binding of libswann_amd.so (the C ABI declared in include/swann_amd.h).
+
+There is no fallback: if the library is not built, or there is no GPU, the
+calls raise.  Build it with `python -m swann_amd._build`.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libswann_amd.so"
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+I64 = ctypes.c_int64
+F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/swann_amd.h
+PROTOTYPES = {
+    "swann_last_error": (ctypes.c_char_p, []),
+    "swann_version": (ctypes.c_char_p, []),
+    "swann_device_count": (I, []),
+    "swann_validate_init": (I, [I64, I, I, I64, I, I, I, I, I, I, I]),
+    "swann_validate_advance": (I, [I64, I, I, I, I64, I, I, I, I, I, I, I, I, I64, I]),
+    "swann_init_states": (I, [P, I, I64, I, P, I64, P, I, I, P, P, P, P, I, P, I, P,
+                              I, I, P, P, I, P, P]),
+    "swann_advance": (I, [P, I, I64, I, P, I, P, I64, I, P, P, P, P, I, P, I, P,
+                          I, I, I, I, I, I, F, I, P, P, I, P, I, I, F, P, I64,
+                          P, I, P, P, F, P]),
+    "swann_merge_branches": (I, [P, P, I64, I, I, I, P, P, P]),
+    "swann_overflow_async": (I, [P, I64, P, P]),
+    "swann_select_workspace_size": (I64, [I64, I64]),
+    "swann_select_nearest": (I, [P, I64, I, P, I64, I, I, P, P, P, P]),
+    "swann_sweep_workspace_size": (I64, [I64, I, I]),
+    "swann_build_sweep": (I, [P, I64, I, I, I, P, P, P, P]),
+    "swann_build_prune": (I, [P, I64, I, I, P, P, I, I, F, P, P]),
+    "swann_reverse_workspace_size": (I64, [I64, I, I]),
+    "swann_build_reverse": (I, [P, I64, I, I, P, I, F, I, P, P, P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class SwannError(RuntimeError):
+    """A call into libswann_amd failed; the message is the library's own."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise SwannError(
+                        f"{LIB_PATH} is not built; run `python -m swann_amd._build` "
+                        "(there is no CPU fallback)")
+                L = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in PROTOTYPES.items():
+                    fn = getattr(L, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Call an int-returning entry point and raise on a nonzero code."""
+    L = lib()
+    rc = getattr(L, name)(*args)
+    if rc != 0:
+        msg = L.swann_last_error().decode(errors="replace")
+        raise SwannError(msg or f"{name} failed with code {rc}")
+    return rc
+
+
+def ptr(t):
+    """Device (or host) address of a tensor, or None for an absent one."""
+    if t is None or t.numel() == 0:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(device):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,112 @@
+"""Graph construction: exact candidates, then a prune that keeps detours short
+(swann/build.py).
+
+The three stages keep the reference's signatures and run as gfx950 kernels:
+`knn_candidates` is a fused distance-tile sweep with per-row top-C selection
+(the n^2 scores never reach HBM), `robust_prune` builds each node's candidate
+Gram in LDS and applies the sequential alpha rule, and `add_reverse` offers
+every edge back to its target through a count / scan / scatter pass and
+re-prunes.  Inputs and outputs live on the GPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import call, lib, ptr, stream_of
+
+_METRICS = {"ip": 0, "l2": 1}
+
+
+def _m(metric) -> int:
+    if isinstance(metric, str):
+        if metric not in _METRICS:
+            raise ValueError(f"metric must be one of {sorted(_METRICS)}")
+        return _METRICS[metric]
+    return int(metric)
+
+
+def _f32(X):
+    if not X.is_cuda:
+        raise RuntimeError("the build runs on the GPU: move the vectors to cuda first")
+    return X.float().contiguous()
+
+
+def pairwise(A, B, metric, bn=None):
+    """Distances from every row of A to every row of B (swann/build.py:14-25)."""
+    if _m(metric) == 0:
+        return 1.0 - (A @ B.T)
+    if bn is None:
+        bn = (B * B).sum(1)
+    return (bn.view(1, -1) - 2.0 * (A @ B.T) + (A * A).sum(1).view(-1, 1)).clamp(min=0)
+
+
+@torch.no_grad()
+def knn_candidates(Xg, C, chunk=4096, metric="ip"):
+    """Exact top-C neighbours by the corpus's metric, self excluded
+    (swann/build.py:28-43).  Returns (int32 [n, C], float32 [n, C]), ascending."""
+    del chunk
+    Xg = _f32(Xg)
+    n, d = Xg.shape
+    idx = torch.empty((n, C), dtype=torch.int32, device=Xg.device)
+    dst = torch.empty((n, C), dtype=torch.float32, device=Xg.device)
+    ws = torch.empty(int(lib().swann_sweep_workspace_size(n, d, C)), dtype=torch.uint8,
+                     device=Xg.device)
+    with torch.cuda.device(Xg.device):
+        call("swann_build_sweep", ptr(Xg), n, d, _m(metric), int(C), ptr(idx), ptr(dst), ptr(ws),
+             stream_of(Xg.device))
+    return idx, dst
+
+
+@torch.no_grad()
+def robust_prune(Xg, cand, cdist, deg, alpha=1.2, chunk=4096, deg_per_node=None, metric="ip",
+                 protect=None):
+    """Keep a candidate only when no nearer kept neighbour detours to it
+    (swann/build.py:46-91).  Returns int32 [n, deg], -1 padded."""
+    del chunk
+    if deg_per_node is not None or protect is not None:
+        raise NotImplementedError("per-node degrees and mutual protection are offline-builder "
+                                  "extras not built in swann_amd")
+    Xg = _f32(Xg)
+    cand = cand.to(device=Xg.device, dtype=torch.int32).contiguous()
+    cdist = cdist.to(device=Xg.device, dtype=torch.float32).contiguous()
+    n, C = cand.shape
+    out = torch.empty((n, deg), dtype=torch.int32, device=Xg.device)
+    with torch.cuda.device(Xg.device):
+        call("swann_build_prune", ptr(Xg), n, Xg.shape[1], _m(metric), ptr(cand), ptr(cdist),
+             int(C), int(deg), float(alpha), ptr(out), stream_of(Xg.device))
+    return out
+
+
+@torch.no_grad()
+def add_reverse(Xg, G, deg, chunk=2048, alpha=1.2, max_in=64, deg_per_node=None, metric="ip"):
+    """Offer every edge back to its target, then re-prune the union per node
+    (swann/build.py:94-150)."""
+    del chunk
+    if deg_per_node is not None:
+        raise NotImplementedError("per-node degrees are an offline-builder extra not built "
+                                  "in swann_amd")
+    Xg = _f32(Xg)
+    G = G.to(device=Xg.device, dtype=torch.int32).contiguous()
+    n, d = Xg.shape
+    if G.shape[1] != deg:
+        raise ValueError(f"G has {G.shape[1]} columns, deg is {deg}")
+    out = torch.empty((n, deg), dtype=torch.int32, device=Xg.device)
+    ws = torch.empty(int(lib().swann_reverse_workspace_size(n, deg, max_in)), dtype=torch.uint8,
+                     device=Xg.device)
+    with torch.cuda.device(Xg.device):
+        call("swann_build_reverse", ptr(Xg), n, d, _m(metric), ptr(G), int(deg), float(alpha),
+             int(max_in), ptr(out), ptr(ws), stream_of(Xg.device))
+    return out
+
+
+@torch.no_grad()
+def build_graph(X, metric: str = "ip", degree: int = 96, candidates: int = 128,
+                alpha: float = 1.2):
+    """Return an (n, degree) int32 neighbour table on the GPU (swann/build.py:153-171)."""
+    if X.device.type != "cuda":
+        X = X.cuda()
+    Xg = X.float().contiguous()
+    cand, cdist = knn_candidates(Xg, candidates, metric=metric)
+    G = robust_prune(Xg, cand, cdist, degree, alpha=alpha, metric=metric)
+    G = add_reverse(Xg, G, degree, alpha=alpha, metric=metric)
+    return G.to(torch.int32).contiguous()

@@ -1,0 +1,611 @@
+// Graph build: exact candidate sweep, alpha robust prune, reverse edges
+// (swann/build.py:14-171).
+//
+// sweep    a tiled distance GEMM over [row tile] x [all columns] whose tiles
+//          never leave the chip: each score is tested against its row's
+//          running threshold and only survivors are appended to a per-row
+//          buffer in the workspace; a full buffer is compacted in place to
+//          its C best (exact radix-style threshold search), so the n^2
+//          scores cost no HBM traffic.  A last pass sorts each row.
+// prune    one workgroup per node: the C x C Gram of its candidates is built
+//          in LDS (upper triangle), then one wave applies the sequential
+//          rule  take_i = room && !exists kept w: alpha * d(w, i) <= d(u, i).
+// reverse  in-degree count, exclusive scan, scatter; then per node the
+//          ascending-source first max_in in-edges are joined to its row,
+//          deduped, scored exactly, sorted, cut to 128 and pruned.
+#include <float.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace swann {
+namespace {
+
+constexpr float kSelf = 3.4e38f;          // build.py:39
+constexpr int kRT = 64, kCT = 64, kKT = 16;
+constexpr int kMaxC = 256;                 // candidates per row the sweep may keep
+constexpr int kPruneMaxC = 128;
+constexpr int kBig = 1 << 30;
+
+__device__ __forceinline__ bool lt(float da, int ia, float db, int ib) {
+    return (da < db) || (da == db && ia < ib);
+}
+
+// float -> uint32 whose unsigned order is the float order
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float funkey(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ float pair_formula(float dot, float na, float nb, int metric) {
+    if (metric == SWANN_METRIC_IP) return 1.0f - dot;
+    const float v = (nb - 2.0f * dot) + na;
+    return v < 0.f ? 0.f : v;
+}
+
+__global__ __launch_bounds__(256) void norms_kernel(const float* __restrict__ A, int64_t n,
+                                                    int dim, float* __restrict__ out) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n) return;
+    const float* a = A + r * dim;
+    float s = 0.f;
+    for (int t = lane; t < dim; t += 64) s = __builtin_fmaf(a[t], a[t], s);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) out[r] = s;
+}
+
+// ---------------------------------------------------------------------------
+// sweep
+struct SweepArgs {
+    const float* X; const float* xn; int64_t n; int dim; int metric; int C; int cap;
+    float* bkey; int32_t* bid; int32_t* bcnt;
+};
+
+// Wave-cooperative compaction of one row's buffer to its C best.
+__device__ void compact_row(float* key, int32_t* id, int cnt, int C, float* thr_out,
+                            int* cnt_out) {
+    const int lane = threadIdx.x & 63;
+    constexpr int R = 16;                      // cap <= 1024
+    uint32_t u[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const int i = t * 64 + lane;
+        u[t] = i < cnt ? fkey(key[i]) : 0xffffffffu;
+    }
+    // smallest T with #{u <= T} >= C
+    uint32_t lo = 0, hi = 0xffffffffu;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < R; ++t) c += (t * 64 + lane < cnt && u[t] <= mid) ? 1 : 0;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+        if (c >= C) hi = mid; else lo = mid + 1;
+    }
+    const uint32_t T = lo;
+    int nlt = 0;
+#pragma unroll
+    for (int t = 0; t < R; ++t) nlt += (t * 64 + lane < cnt && u[t] < T) ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) nlt += __shfl_xor(nlt, off, 64);
+    int eq_left = C - nlt;                     // copies of T still to keep, index order
+    int w = 0;
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const int i = t * 64 + lane;
+        const bool in = i < cnt;
+        const bool is_lt = in && u[t] < T;
+        const bool is_eq = in && u[t] == T;
+        const uint64_t meq = __ballot(is_eq);
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const int eq_rank = __popcll(meq & below);
+        const bool keep = is_lt || (is_eq && eq_rank < eq_left);
+        const uint64_t mk = __ballot(keep);
+        const int kid = in ? id[i] : 0;
+        const float kk = in ? key[i] : 0.f;
+        if (keep) {
+            const int dst = w + __popcll(mk & below);
+            key[dst] = kk;
+            id[dst] = kid;
+        }
+        w += __popcll(mk);
+        const int used = __popcll(meq);
+        eq_left -= used < eq_left ? used : eq_left;
+    }
+    if (lane == 0) { *thr_out = funkey(T); *cnt_out = w; }
+}
+
+__global__ __launch_bounds__(256) void sweep_kernel(SweepArgs a) {
+    __shared__ float As[kKT][kRT + 4];
+    __shared__ float Bs[kKT][kCT + 4];
+    __shared__ float thr[kRT];
+    __shared__ int cnt[kRT];
+    __shared__ int need;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int wave = tid >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * kRT;
+    const int dim = a.dim;
+    const int lr = tid >> 2, lk = (tid & 3) * 4;
+    if (tid < kRT) { thr[tid] = INFINITY; cnt[tid] = 0; }
+    if (tid == 0) need = 0;
+    __syncthreads();
+    float rn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = r0 + ty * 4 + i;
+        rn[i] = (a.metric == SWANN_METRIC_L2 && r < a.n) ? a.xn[r] : 0.f;
+    }
+    for (int64_t c0 = 0; c0 < a.n; c0 += kCT) {
+        float acc[4][4] = {};
+        for (int k0 = 0; k0 < dim; k0 += kKT) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = k0 + lk + e;
+                const int64_t ar = r0 + lr, bc = c0 + lr;
+                As[lk + e][lr] = (ar < a.n && k < dim) ? a.X[ar * dim + k] : 0.f;
+                Bs[lk + e][lr] = (bc < a.n && k < dim) ? a.X[bc * dim + k] : 0.f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kKT; ++k) {
+                float av[4], bv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av[i] = As[k][ty * 4 + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx * 4 + j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+            }
+            __syncthreads();
+        }
+        // screen against each row's threshold; append survivors
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rl = ty * 4 + i;
+            const int64_t r = r0 + rl;
+            if (r >= a.n) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t c = c0 + tx * 4 + j;
+                if (c >= a.n) continue;
+                const float cn = a.metric == SWANN_METRIC_L2 ? a.xn[c] : 0.f;
+                const float d = (c == r) ? kSelf : pair_formula(acc[i][j], rn[i], cn, a.metric);
+                if (d < thr[rl]) {
+                    const int p = atomicAdd(&cnt[rl], 1);
+                    a.bkey[r * a.cap + p] = d;
+                    a.bid[r * a.cap + p] = (int32_t)c;
+                }
+            }
+        }
+        __syncthreads();
+        // any row that could overflow on the next tile is compacted now
+        if (tid < kRT && cnt[tid] > a.cap - kCT) atomicOr(&need, 1);
+        __syncthreads();
+        if (need) {
+            for (int rl = wave; rl < kRT; rl += 4) {
+                const int64_t r = r0 + rl;
+                if (r < a.n && cnt[rl] > a.cap - kCT)
+                    compact_row(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C, &thr[rl],
+                                &cnt[rl]);
+            }
+            __syncthreads();
+            if (tid == 0) need = 0;
+            __syncthreads();
+        }
+    }
+    if (tid < kRT && r0 + tid < a.n) a.bcnt[r0 + tid] = cnt[tid];
+}
+
+// Sort each row's survivors and emit the first C.
+__global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bkey,
+                                                   const int32_t* __restrict__ bid,
+                                                   const int32_t* __restrict__ bcnt, int64_t n,
+                                                   int cap, int C, int32_t* __restrict__ cand,
+                                                   float* __restrict__ cdist) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int64_t r = blockIdx.x;
+    const int cnt = bcnt[r];
+    int np = 2;
+    while (np < cnt) np <<= 1;
+    float* sd = reinterpret_cast<float*>(smem);
+    int* si = reinterpret_cast<int*>(sd + np);
+    for (int i = threadIdx.x; i < np; i += 256) {
+        const bool real = i < cnt;
+        sd[i] = real ? bkey[r * cap + i] : INFINITY;
+        si[i] = real ? bid[r * cap + i] : INT32_MAX;
+    }
+    __syncthreads();
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < np; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = ((i & size) == 0);
+                    if (up != lt(sd[i], si[i], sd[j], si[j])) {
+                        const float td = sd[i]; sd[i] = sd[j]; sd[j] = td;
+                        const int ti = si[i]; si[i] = si[j]; si[j] = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (int t = threadIdx.x; t < C; t += 256) {
+        const bool ok = t < cnt;
+        cand[r * C + t] = ok ? si[t] : -1;
+        cdist[r * C + t] = ok ? sd[t] : INFINITY;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// prune: one workgroup (256 threads) per node
+constexpr int kPKC = 16;
+
+__device__ __forceinline__ int tri(int w, int i) { return i * (i - 1) / 2 + w; }   // w < i
+
+__global__ __launch_bounds__(256) void prune_kernel(const float* __restrict__ X, int64_t n,
+                                                    int dim, int metric,
+                                                    const int32_t* __restrict__ cand,
+                                                    const float* __restrict__ cdist, int C,
+                                                    int deg, float alpha,
+                                                    int32_t* __restrict__ out) {
+    __shared__ float gram[kPruneMaxC * (kPruneMaxC - 1) / 2];
+    __shared__ float vn[kPruneMaxC];
+    __shared__ float Vs[kPKC][kPruneMaxC + 4];
+    __shared__ int cid[kPruneMaxC];
+    __shared__ float cdu[kPruneMaxC];
+    const int64_t u = blockIdx.x;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    for (int i = tid; i < C; i += 256) {
+        const int c = cand[u * C + i];
+        cid[i] = c;
+        cdu[i] = cdist[u * C + i];
+    }
+    __syncthreads();
+    // thread (ty, tx) accumulates Gram rows ty*8.., columns tx*8.. (C <= 128)
+    float acc[8][8] = {};
+    const bool active = (ty * 8 < C) && (tx * 8 < C) && (tx >= ty);
+    for (int k0 = 0; k0 < dim; k0 += kPKC) {
+        for (int e = tid; e < kPKC * C; e += 256) {
+            const int i = e / kPKC, kk = e % kPKC;
+            const int c = cid[i];
+            const int k = k0 + kk;
+            Vs[kk][i] = (c >= 0 && c < n && k < dim) ? X[(int64_t)c * dim + k] : 0.f;
+        }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+            for (int kk = 0; kk < kPKC; ++kk) {
+                float av[8], bv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[i] = Vs[kk][ty * 8 + i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bv[j] = Vs[kk][tx * 8 + j];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+            }
+        }
+        __syncthreads();
+    }
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int w = ty * 8 + i;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = tx * 8 + j;
+                if (w < C && c < C) {
+                    if (w < c) gram[tri(w, c)] = acc[i][j];
+                    else if (w == c) vn[w] = acc[i][j];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // The sequential rule, one wave.  Every decision is wave-uniform, so the
+    // kept list lives in registers: lane t holds kept[t] and kept[64 + t].
+    if (tid < 64) {
+        const int lane = tid;
+        int k0 = -1, k1 = -1;
+        int nk = 0;
+        for (int i = 0; i < C && nk < deg; ++i) {
+            if (cid[i] < 0) continue;
+            const float du = cdu[i];
+            bool v = false;
+            if (lane < nk) v = alpha * pair_formula(gram[tri(k0, i)], vn[k0], vn[i], metric) <= du;
+            if (64 + lane < nk)
+                v = v || alpha * pair_formula(gram[tri(k1, i)], vn[k1], vn[i], metric) <= du;
+            if (__ballot(v) == 0ull) {
+                if (nk < 64) { if (lane == nk) k0 = i; }
+                else if (lane == nk - 64) k1 = i;
+                ++nk;
+            }
+        }
+        if (lane < deg) out[u * deg + lane] = lane < nk ? cid[k0] : -1;
+        if (64 + lane < deg) out[u * deg + 64 + lane] = 64 + lane < nk ? cid[k1] : -1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// reverse
+__global__ void fill_i32(int32_t* p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void rev_count(const int32_t* __restrict__ G, int64_t n, int deg,
+                          int32_t* __restrict__ cnt) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n * deg) return;
+    const int v = G[e];
+    if (v >= 0 && v < n) atomicAdd(&cnt[v], 1);
+}
+
+// exclusive scan of cnt[n] into start[n], one workgroup, in chunks of 1024
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ cnt, int64_t n,
+                                                    int32_t* __restrict__ start) {
+    __shared__ int buf[1024];
+    __shared__ int carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (int64_t b = 0; b < n; b += 1024) {
+        const int64_t i = b + threadIdx.x;
+        const int v = i < n ? cnt[i] : 0;
+        buf[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int t = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+            __syncthreads();
+            buf[threadIdx.x] += t;
+            __syncthreads();
+        }
+        if (i < n) start[i] = carry + buf[threadIdx.x] - v;
+        __syncthreads();
+        if (threadIdx.x == 1023) carry += buf[1023];
+        __syncthreads();
+    }
+}
+
+__global__ void rev_scatter(const int32_t* __restrict__ G, int64_t n, int deg,
+                            const int32_t* __restrict__ start, int32_t* __restrict__ fill,
+                            int32_t* __restrict__ src) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n * deg) return;
+    const int v = G[e];
+    if (v < 0 || v >= n) return;
+    const int p = atomicAdd(&fill[v], 1);
+    src[start[v] + p] = (int32_t)(e / deg);
+}
+
+__device__ void block_sort_int(int* s, int np) {
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < np; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = ((i & size) == 0);
+                    if (up != (s[i] < s[j])) { const int t = s[i]; s[i] = s[j]; s[j] = t; }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+constexpr int kRevBuf = 2048;
+
+// Per node: first max_in in-sources (ascending), union with G_u, minus self,
+// dedup, exact distances, ascending (d, id), the first keepn.
+__global__ __launch_bounds__(256) void rev_assemble(const float* __restrict__ X, int64_t n,
+                                                    int dim, int metric,
+                                                    const int32_t* __restrict__ G, int deg,
+                                                    int max_in,
+                                                    const int32_t* __restrict__ cnt,
+                                                    const int32_t* __restrict__ start,
+                                                    const int32_t* __restrict__ src, int keepn,
+                                                    int32_t* __restrict__ cand2,
+                                                    float* __restrict__ cd2) {
+    __shared__ int ib[kRevBuf];
+    __shared__ int row[512];
+    __shared__ float rd[512];
+    __shared__ float xu[4096];
+    const int64_t u = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int cu = cnt[u];
+    const int64_t s0 = start[u];
+    // smallest max_in sources, running over chunks
+    int keep = 0;
+    for (int c0 = 0; c0 < cu;) {
+        const int take = (cu - c0) < (kRevBuf - keep) ? (cu - c0) : (kRevBuf - keep);
+        const int fill = keep + take;
+        int np = 2;
+        while (np < fill) np <<= 1;
+        for (int i = keep + tid; i < np; i += 256) ib[i] = i < fill ? src[s0 + c0 + (i - keep)] : INT32_MAX;
+        __syncthreads();
+        block_sort_int(ib, np);
+        c0 += take;
+        keep = fill < max_in ? fill : max_in;
+    }
+    const int W = deg + max_in;
+    int np = 2;
+    while (np < W) np <<= 1;
+    for (int i = tid; i < np; i += 256) {
+        int v;
+        if (i < deg) v = G[u * deg + i];
+        else if (i < W) v = (i - deg) < keep ? ib[i - deg] : -1;
+        else v = INT32_MAX;
+        if (i < W && (v == (int)u || v < 0 || v >= n)) v = kBig;
+        row[i] = v;
+    }
+    __syncthreads();
+    block_sort_int(row, np);
+    // later copies of an id go (judged on the sorted values)
+    int mark[2] = {0, 0};
+    for (int t = 0, i = tid; i < W; i += 256, ++t)
+        mark[t] = (i > 0 && row[i] == row[i - 1]) ? 1 : 0;
+    __syncthreads();
+    for (int t = 0, i = tid; i < W; i += 256, ++t)
+        if (mark[t]) row[i] = kBig;
+    for (int t = tid; t < dim && t < 4096; t += 256) xu[t] = X[u * dim + t];
+    __syncthreads();
+    // exact distances, 16 lanes per candidate
+    const int team = tid >> 4, tl = tid & 15;
+    for (int i = team; i < W; i += 16) {
+        const int v = row[i];
+        float s = 0.f;
+        if (v < kBig) {
+            const float* xv = X + (int64_t)v * dim;
+            for (int t = tl; t < dim; t += 16) {
+                const float xt = dim <= 4096 ? xu[t] : X[u * dim + t];
+                if (metric == SWANN_METRIC_IP) s = __builtin_fmaf(xv[t], xt, s);
+                else { const float df = xv[t] - xt; s = __builtin_fmaf(df, df, s); }
+            }
+        }
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) s += __shfl_down(s, off, 16);
+        if (tl == 0) {
+            if (v < kBig) { rd[i] = metric == SWANN_METRIC_IP ? 1.0f - s : s; }
+            else { rd[i] = INFINITY; row[i] = 0; }     // build.py: invalid -> id 0, +inf
+        }
+    }
+    for (int i = W + tid; i < np; i += 256) { rd[i] = INFINITY; row[i] = INT32_MAX; }
+    __syncthreads();
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < np; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = ((i & size) == 0);
+                    if (up != lt(rd[i], row[i], rd[j], row[j])) {
+                        const float td = rd[i]; rd[i] = rd[j]; rd[j] = td;
+                        const int ti = row[i]; row[i] = row[j]; row[j] = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (int t = tid; t < keepn; t += 256) {
+        cand2[u * keepn + t] = row[t];
+        cd2[u * keepn + t] = rd[t];
+    }
+}
+
+inline int64_t align256(int64_t b) { return ((b + 255) / 256) * 256; }
+
+int sweep_cap(int C) {
+    int cap = C + 512;
+    return cap > 1024 ? 1024 : cap;
+}
+
+}  // namespace
+}  // namespace swann
+
+using namespace swann;
+
+extern "C" {
+
+int64_t swann_sweep_workspace_size(int64_t n, int dim, int C) {
+    (void)dim;
+    const int cap = sweep_cap(C);
+    return align256(n * 4) + align256(n * (int64_t)cap * 4) * 2 + align256(n * 4);
+}
+
+int swann_build_sweep(const float* X, int64_t n, int dim, int metric, int C, int32_t* cand,
+                      float* cdist, void* workspace, void* stream) {
+    clear_error();
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(n >= 2 && dim >= 1, "sweep: need n >= 2 rows");
+    SWANN_REQUIRE(C >= 1 && C <= kMaxC && C <= n, "sweep: candidates must be in 1..min(n, %d)",
+                  kMaxC);
+    SWANN_REQUIRE(n <= INT32_MAX / 2, "sweep: n too large");
+    SWANN_REQUIRE(X && cand && cdist && workspace, "sweep: a required pointer is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    const int cap = sweep_cap(C);
+    char* ws = (char*)workspace;
+    float* xn = (float*)ws; ws += align256(n * 4);
+    float* bkey = (float*)ws; ws += align256(n * (int64_t)cap * 4);
+    int32_t* bid = (int32_t*)ws; ws += align256(n * (int64_t)cap * 4);
+    int32_t* bcnt = (int32_t*)ws;
+    if (metric == SWANN_METRIC_L2)
+        hipLaunchKernelGGL(norms_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, X, n,
+                           dim, xn);
+    SweepArgs a{X, xn, n, dim, metric, C, cap, bkey, bid, bcnt};
+    hipLaunchKernelGGL(sweep_kernel, dim3((unsigned)((n + kRT - 1) / kRT)), dim3(256), 0, st, a);
+    int rc = launch_status("sweep");
+    if (rc) return rc;
+    int np = 2;
+    while (np < cap) np <<= 1;
+    hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
+                       bcnt, n, cap, C, cand, cdist);
+    return launch_status("sweep final");
+}
+
+int swann_build_prune(const float* X, int64_t n, int dim, int metric, const int32_t* cand,
+                      const float* cdist, int C, int deg, float alpha, int32_t* out,
+                      void* stream) {
+    clear_error();
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(C >= 1 && C <= kPruneMaxC, "prune: candidates per node must be in 1..%d",
+                  kPruneMaxC);
+    SWANN_REQUIRE(deg >= 1 && deg <= C, "prune: degree must be in 1..C");
+    SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
+    SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
+    hipLaunchKernelGGL(prune_kernel, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream, X, n,
+                       dim, metric, cand, cdist, C, deg, alpha, out);
+    return launch_status("prune");
+}
+
+int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in) {
+    const int keepn = (deg + max_in) < kPruneMaxC ? (deg + max_in) : kPruneMaxC;
+    return align256(n * 4) * 3 + align256(n * (int64_t)deg * 4) +
+           align256(n * (int64_t)keepn * 4) * 2;
+}
+
+int swann_build_reverse(const float* X, int64_t n, int dim, int metric, const int32_t* G, int deg,
+                        float alpha, int max_in, int32_t* out, void* workspace, void* stream) {
+    clear_error();
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(deg >= 1 && max_in >= 0 && deg + max_in <= 512,
+                  "reverse: need deg >= 1, max_in >= 0, deg + max_in <= 512");
+    SWANN_REQUIRE(n >= 1 && n * (int64_t)deg < INT32_MAX, "reverse: n * deg must fit in int32");
+    SWANN_REQUIRE(X && G && out && workspace, "reverse: a required pointer is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    const int keepn = (deg + max_in) < kPruneMaxC ? (deg + max_in) : kPruneMaxC;
+    char* ws = (char*)workspace;
+    int32_t* cnt = (int32_t*)ws; ws += align256(n * 4);
+    int32_t* fill = (int32_t*)ws; ws += align256(n * 4);
+    int32_t* start = (int32_t*)ws; ws += align256(n * 4);
+    int32_t* src = (int32_t*)ws; ws += align256(n * (int64_t)deg * 4);
+    int32_t* cand2 = (int32_t*)ws; ws += align256(n * (int64_t)keepn * 4);
+    float* cd2 = (float*)ws;
+    // counters are cleared by a kernel, not a memset, so the pass can be captured
+    const unsigned nbk = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(fill_i32, dim3(nbk), dim3(256), 0, st, cnt, n, 0);
+    hipLaunchKernelGGL(fill_i32, dim3(nbk), dim3(256), 0, st, fill, n, 0);
+    const int64_t E = n * deg;
+    const unsigned eb = (unsigned)((E + 255) / 256);
+    hipLaunchKernelGGL(rev_count, dim3(eb), dim3(256), 0, st, G, n, deg, cnt);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, n, start);
+    hipLaunchKernelGGL(rev_scatter, dim3(eb), dim3(256), 0, st, G, n, deg, start, fill, src);
+    int rc = launch_status("reverse scatter");
+    if (rc) return rc;
+    hipLaunchKernelGGL(rev_assemble, dim3((unsigned)n), dim3(256), 0, st, X, n, dim, metric, G,
+                       deg, max_in, cnt, start, src, keepn, cand2, cd2);
+    rc = launch_status("reverse assemble");
+    if (rc) return rc;
+    return swann_build_prune(X, n, dim, metric, cand2, cd2, keepn, deg, alpha, out, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,867 @@
+// Multi-branch graph search on gfx950: branch init, best-first advance,
+// per-query merge, and the asynchronous overflow readback.
+//
+// Semantics follow swann/csrc/local_search.cu (reference) exactly where the
+// result depends on them -- the distance's summation order (:185-203), the
+// (distance, id) order (:87-89), the slot rule and stop radius (:451-517), the
+// candidate filter (:607-625), merge-path with its tie behaviour (:637-650),
+// the bound (:655-658), crowd and stall retirement (:659-682), the shared
+// table and claims (:169-183, :541-592) -- and are MI355X-native in how they
+// run:
+//   * one workgroup per (query, branch) over a 1-D grid (no 65535-query cap),
+//     XCD-remapped so a query's branches share one L2;
+//   * BLOCK = 64 (one wave; every barrier folds away) for batch work, or 256
+//     for small batches where latency rules;
+//   * the neighbour list of an expansion is screened lane-parallel first
+//     (visited insert, table probe, claim), then only the survivors are
+//     scored, TEAM lanes per distance, with every 16-byte row load of a lane
+//     issued before its arithmetic;
+//   * queue, candidates and the query vector stay in LDS; counters stay in
+//     registers/LDS until the call ends;
+//   * the per-query table, claims and bound use agent-scope atomics, because
+//     L2 is per XCD and plain loads are not coherent across XCDs.
+#include <float.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "common.h"
+
+namespace swann {
+namespace {
+
+constexpr int kMaxL = SWANN_MAXL;
+constexpr int kMaxD = SWANN_MAXD;
+constexpr int kMaxV = SWANN_MAXV;
+constexpr int kNctr = SWANN_NCTR;
+constexpr int kCprobe = 32;            // bounded probe into the shared table
+constexpr int kMaxChunks = 16;         // 16-byte loads a lane keeps in flight
+constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
+constexpr size_t kMaxLds = 64 * 1024;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+template <typename XT> struct Vec;
+template <> struct Vec<float> { static constexpr int N = 4; };
+template <> struct Vec<_Float16> { static constexpr int N = 8; };
+
+__device__ __forceinline__ bool lt(float da, int ia, float db, int ib) {
+    return (da < db) || (da == db && ia < ib);
+}
+
+template <int METRIC>
+__device__ __forceinline__ float term(float q, float x) {
+    if (METRIC == SWANN_METRIC_IP) return q * x;
+    const float df = q - x;
+    return df * df;
+}
+
+// One distance: lane tl of a TEAM owns the VEC-element blocks at tl*VEC,
+// tl*VEC + TEAM*VEC, ...; each lane sums its terms in order, then the team
+// folds with off = TEAM/2 .. 1 (lane tl takes tl+off).  Built with
+// -ffp-contract=off so product and sum round separately.  The result is
+// meaningful in lane tl == 0.
+template <int TEAM, typename XT, int METRIC>
+__device__ __forceinline__ float team_dist(const float* __restrict__ sq,
+                                           const XT* __restrict__ x, int dim, int tl,
+                                           bool vec_ok) {
+    constexpr int VEC = Vec<XT>::N;
+    constexpr int STRIDE = TEAM * VEC;
+    float acc = 0.f;
+    if (vec_ok) {
+        for (int b0 = tl * VEC; b0 < dim; b0 += STRIDE * kMaxChunks) {
+            uint4 raw[kMaxChunks];
+#pragma unroll
+            for (int c = 0; c < kMaxChunks; ++c) {
+                const int base = b0 + c * STRIDE;
+                if (base < dim) raw[c] = *reinterpret_cast<const uint4*>(x + base);
+            }
+#pragma unroll
+            for (int c = 0; c < kMaxChunks; ++c) {
+                const int base = b0 + c * STRIDE;
+                if (base < dim) {
+                    if constexpr (VEC == 4) {
+                        const float4v xv = __builtin_bit_cast(float4v, raw[c]);
+                        const float4v qv = *reinterpret_cast<const float4v*>(sq + base);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(qv[i], xv[i]);
+                    } else {
+                        const half8 hv = __builtin_bit_cast(half8, raw[c]);
+                        const float4v q0 = *reinterpret_cast<const float4v*>(sq + base);
+                        const float4v q1 = *reinterpret_cast<const float4v*>(sq + base + 4);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q0[i], (float)hv[i]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc = acc + term<METRIC>(q1[i], (float)hv[4 + i]);
+                    }
+                }
+            }
+        }
+    } else {
+        // Any dimension: element loads, same order, nothing read past the row.
+        for (int base = tl * VEC; base < dim; base += STRIDE) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                if (base + i < dim) acc = acc + term<METRIC>(sq[base + i], (float)x[base + i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
+    return METRIC == SWANN_METRIC_IP ? 1.f - acc : acc;
+}
+
+template <int TEAM, typename XT>
+__device__ __forceinline__ float team_dist_m(const float* sq, const XT* x, int dim, int tl,
+                                             bool vec_ok, int metric) {
+    return metric == SWANN_METRIC_IP ? team_dist<TEAM, XT, SWANN_METRIC_IP>(sq, x, dim, tl, vec_ok)
+                                     : team_dist<TEAM, XT, SWANN_METRIC_L2>(sq, x, dim, tl, vec_ok);
+}
+
+// Per-branch visited set: open addressing, linear probe, slot = key + 1
+// (local_search.cu:94-110).  Private to the workgroup.
+__device__ __forceinline__ int vis_insert(int* tab, int H, int key, int* fail) {
+    const unsigned mask = (unsigned)(H - 1);
+    unsigned pos = (2654435761u * (unsigned)key) & mask;
+    for (int probe = 0; probe < H; ++probe) {
+        int cur = __hip_atomic_load(&tab[pos], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (cur == 0) {
+            int expected = 0;
+            if (__hip_atomic_compare_exchange_strong(&tab[pos], &expected, key + 1,
+                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP))
+                return 1;
+            cur = expected;
+        }
+        if (cur == key + 1) return 0;
+        pos = (pos + 1) & mask;
+    }
+    *fail += 1;
+    return 0;
+}
+
+// Per-query shared table and claims (local_search.cu:169-183).  Agent scope:
+// the branches of one query may run on different XCDs.
+__device__ __forceinline__ int cache_slot(int* cid, int Hc, int key, int* claimed) {
+    const unsigned mask = (unsigned)(Hc - 1);
+    unsigned pos = (2654435761u * (unsigned)key) & mask;
+    for (int probe = 0; probe < kCprobe; ++probe) {
+        int cur = __hip_atomic_load(&cid[pos], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (cur == key + 1) return (int)pos;
+        if (cur == 0) {
+            int expected = 0;
+            if (__hip_atomic_compare_exchange_strong(&cid[pos], &expected, key + 1,
+                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)) {
+                *claimed = 1;
+                return (int)pos;
+            }
+            if (expected == key + 1) return (int)pos;
+        }
+        pos = (pos + 1) & mask;
+    }
+    return -1;
+}
+
+__device__ __forceinline__ float load_agent_f(const float* p) {
+    const int b = __hip_atomic_load(reinterpret_cast<const int*>(p), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    return __int_as_float(b);
+}
+
+__device__ __forceinline__ void store_agent_f(float* p, float v) {
+    __hip_atomic_store(reinterpret_cast<int*>(p), __float_as_int(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int pow2_ge(int x, int lo, int cap) {
+    int n = lo;
+    while (n < x && n < cap) n <<= 1;
+    return n;
+}
+
+template <int BLOCK>
+__device__ __forceinline__ void block_add(int* dst, int v) {
+    // wave reduce then one LDS atomic per wave
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0 && v != 0) atomicAdd(dst, v);
+}
+
+// ---------------------------------------------------------------------------
+// init: local_search.cu:271-351
+struct InitArgs {
+    const void* X; const float* Qv; const int32_t* seeds;
+    int32_t* ids; float* dist; uint8_t* expd; uint8_t* lin; int32_t* visited; int32_t* counters;
+    int dim, J, V, L, H, metric;
+    int64_t Q, n;
+    int32_t* cache_id; float* cache_d; int Hc; float* bound;
+    int vec_ok;
+};
+
+template <int TEAM, typename XT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int NT = BLOCK / TEAM;
+    const int tid = threadIdx.x, team = tid / TEAM, tl = tid % TEAM;
+    const int64_t nb = a.Q * a.J;
+    const int64_t flat = xcd_remap(blockIdx.x, nb);
+    const int64_t q = flat / a.J;
+    const int j = (int)(flat % a.J);
+    const int dimp = (a.dim + 3) & ~3;
+    const int nsort = pow2_ge(a.V, 2, kMaxD);
+
+    float* sq = reinterpret_cast<float*>(smem);
+    int* c_id = reinterpret_cast<int*>(sq + dimp);
+    float* c_d = reinterpret_cast<float*>(c_id + nsort);
+    int* s_id = reinterpret_cast<int*>(c_d + nsort);
+    float* s_d = reinterpret_cast<float*>(s_id + nsort);
+    uint8_t* c_l = reinterpret_cast<uint8_t*>(s_d + nsort);
+    uint8_t* s_l = c_l + nsort;
+    uint8_t* s_new = s_l + nsort;
+    __shared__ int s_evals, s_fail;
+
+    int32_t* vis = a.visited + flat * (int64_t)a.H;
+    int32_t* ctr = a.counters + flat * kNctr;
+    const float* qrow = a.Qv + q * (int64_t)a.dim;
+    const XT* X = reinterpret_cast<const XT*>(a.X);
+
+    for (int t = tid; t < a.dim; t += BLOCK) sq[t] = qrow[t];
+    if (a.H > 1) {
+        if ((a.H & 3) == 0) {
+            int4* v4 = reinterpret_cast<int4*>(vis);
+            for (int t = tid; t < a.H / 4; t += BLOCK) v4[t] = make_int4(0, 0, 0, 0);
+        } else {
+            for (int t = tid; t < a.H; t += BLOCK) vis[t] = 0;
+        }
+    }
+    // The query's table and bound belong to all J branches; they clear it
+    // between them (local_search.cu:302-313).
+    if (a.Hc > 0) {
+        int32_t* cid = a.cache_id + q * (int64_t)a.Hc;
+        float* cdd = a.cache_d + q * (int64_t)a.Hc;
+        if ((a.Hc & 3) == 0) {
+            int4* i4 = reinterpret_cast<int4*>(cid);
+            float4* f4 = reinterpret_cast<float4*>(cdd);
+            for (int t = j * BLOCK + tid; t < a.Hc / 4; t += a.J * BLOCK) {
+                i4[t] = make_int4(0, 0, 0, 0);
+                f4[t] = make_float4(FLT_MAX, FLT_MAX, FLT_MAX, FLT_MAX);
+            }
+        } else {
+            for (int t = j * BLOCK + tid; t < a.Hc; t += a.J * BLOCK) {
+                cid[t] = 0;
+                cdd[t] = FLT_MAX;
+            }
+        }
+    }
+    if (a.bound && j == 0 && tid == 0) a.bound[q] = FLT_MAX;
+    for (int i = tid; i < nsort; i += BLOCK) { c_id[i] = -1; c_d[i] = FLT_MAX; c_l[i] = 0; s_new[i] = 0; }
+    if (tid == 0) { s_evals = 0; s_fail = 0; }
+    __syncthreads();
+
+    // Seeds: a repeated seed is kept once, the first occurrence winning
+    // (the visited table dedups, local_search.cu:318-340).  One lane inserts
+    // them in seed order so the surviving lineage never depends on a race.
+    const int32_t* sd = a.seeds + flat * (int64_t)a.V;
+    if (tid == 0) {
+        int fail = 0;
+        for (int si = 0; si < a.V; ++si) {
+            const int v = sd[si];
+            if (v < 0 || v >= a.n) continue;            // out-of-range ids are empty slots
+            int isnew = 1;
+            if (a.H > 1) isnew = vis_insert(vis, a.H, v, &fail);
+            s_new[si] = (uint8_t)isnew;
+        }
+        s_fail = fail;
+    }
+    __syncthreads();
+    int evals = 0;
+    for (int si = team; si < a.V; si += NT) {
+        if (!s_new[si]) continue;                        // uniform within the team
+        const int v = sd[si];
+        const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
+                                             a.vec_ok, a.metric);
+        if (tl == 0) { c_id[si] = v; c_d[si] = d; c_l[si] = (uint8_t)si; ++evals; }
+    }
+    block_add<BLOCK>(&s_evals, evals);
+    __syncthreads();
+    // rank sort of the nsort slots by (d, id), ties by slot (a stable sort)
+    for (int i = tid; i < nsort; i += BLOCK) {
+        const int id = c_id[i]; const float d = c_d[i];
+        int r = 0;
+        for (int t = 0; t < nsort; ++t) {
+            const int it = c_id[t]; const float dt = c_d[t];
+            r += (lt(dt, it, d, id) || (dt == d && it == id && t < i)) ? 1 : 0;
+        }
+        s_id[r] = id; s_d[r] = d; s_l[r] = c_l[i];
+    }
+    __syncthreads();
+    const int64_t qb = flat * (int64_t)a.L;
+    for (int i = tid; i < a.L; i += BLOCK) {
+        const bool ok = (i < nsort) && (s_id[i] >= 0);
+        a.ids[qb + i] = ok ? s_id[i] : -1;
+        a.dist[qb + i] = ok ? s_d[i] : FLT_MAX;
+        a.expd[qb + i] = ok ? 0 : 1;
+        a.lin[qb + i] = ok ? s_l[i] : 0;
+    }
+    for (int i = tid; i < kNctr; i += BLOCK)
+        ctr[i] = (i == 1) ? s_evals : (i == 2) ? s_fail : 0;
+}
+
+// ---------------------------------------------------------------------------
+// advance: local_search.cu:353-688
+struct AdvArgs {
+    const void* X; const int32_t* G; const float* Qv;
+    int32_t* ids; float* dist; uint8_t* expd; uint8_t* lin; int32_t* visited; int32_t* counters;
+    int dim, D, J, L, H, metric, delta, max_exp, policy, V;
+    float stop_eps; int kstop;
+    int32_t* cache_id; float* cache_d; int Hc; float* bound; int exclusive;
+    int stall_patience; float crowd_frac;
+    const int32_t* active; int64_t nblocks, nbranch, n;
+    int vec_ok;
+};
+
+template <int TEAM, typename XT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int NT = BLOCK / TEAM;
+    const int tid = threadIdx.x, team = tid / TEAM, tl = tid % TEAM;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t pos = xcd_remap(blockIdx.x, a.nblocks);
+    const int64_t flat = a.active ? (int64_t)a.active[pos] : pos;
+    if (flat < 0 || flat >= a.nbranch) return;          // a bad active entry: no work
+    const int64_t q = flat / a.J;
+    const int L = a.L, D = a.D;
+    const int dimp = (a.dim + 3) & ~3;
+    const int nsort = pow2_ge(D, 2, kMaxD);
+
+    // LDS carve-up; sizes must match advance_lds() on the host
+    float* sq = reinterpret_cast<float*>(smem);
+    int* qa_id = reinterpret_cast<int*>(sq + dimp);
+    float* qa_d = reinterpret_cast<float*>(qa_id + L);
+    int* qb_id = reinterpret_cast<int*>(qa_d + L);
+    float* qb_d = reinterpret_cast<float*>(qb_id + L);
+    int* c_id = reinterpret_cast<int*>(qb_d + L);
+    float* c_d = reinterpret_cast<float*>(c_id + nsort);
+    int* u_id = reinterpret_cast<int*>(c_d + nsort);
+    float* u_d = reinterpret_cast<float*>(u_id + nsort);
+    int* k_id = reinterpret_cast<int*>(u_d + nsort);
+    float* k_d = reinterpret_cast<float*>(k_id + nsort);
+    int* w_v = reinterpret_cast<int*>(k_d + nsort);
+    int* w_slot = w_v + nsort;
+    int* w_nidx = w_slot + nsort;
+    uint8_t* qa_e = reinterpret_cast<uint8_t*>(w_nidx + nsort);
+    uint8_t* qa_l = qa_e + L;
+    uint8_t* qb_e = qa_l + L;
+    uint8_t* qb_l = qb_e + L;
+    uint8_t* c_l = qb_l + L;
+    uint8_t* u_l = c_l + nsort;
+    uint8_t* k_l = u_l + nsort;
+
+    __shared__ int s_ctr[kNctr];
+    __shared__ int s_slot, s_p, s_plin, s_nkeep, s_nwork, s_nbr, s_cov, s_stall, s_crowd_run;
+    __shared__ unsigned s_retired[8];
+    __shared__ float s_best_k;
+
+    int32_t* vis = a.visited + flat * (int64_t)a.H;
+    int32_t* ctr = a.counters + flat * kNctr;
+    const int64_t qb = flat * (int64_t)L;
+    int32_t* cid = a.Hc > 0 ? a.cache_id + q * (int64_t)a.Hc : nullptr;
+    float* cdd = a.Hc > 0 ? a.cache_d + q * (int64_t)a.Hc : nullptr;
+    const float* qrow = a.Qv + q * (int64_t)a.dim;
+    const XT* X = reinterpret_cast<const XT*>(a.X);
+
+    for (int t = tid; t < a.dim; t += BLOCK) sq[t] = qrow[t];
+    for (int i = tid; i < L; i += BLOCK) {
+        qa_id[i] = a.ids[qb + i]; qa_d[i] = a.dist[qb + i];
+        qa_e[i] = a.expd[qb + i]; qa_l[i] = a.lin[qb + i];
+    }
+    if (tid < kNctr) s_ctr[tid] = ctr[tid];
+    if (tid < 8) s_retired[tid] = 0u;
+    if (tid == 0) { s_best_k = FLT_MAX; s_stall = 0; s_crowd_run = 0; }
+    __syncthreads();
+
+    int r_evals = 0, r_fail = 0, r_hits = 0, r_claim = 0;
+    const bool early = (a.stop_eps >= 0.f);
+    const int kr = (a.kstop < L) ? a.kstop : L;
+
+    for (int step = 0; step < a.delta; ++step) {
+        // ---- pick the slot to expand (wave 0; local_search.cu:452-517) ----
+        // The budget test is made here, by wave 0 alone, and published with
+        // the slot: the other waves never read a counter wave 0 may be moving.
+        if (wave == 0 && s_ctr[0] >= a.max_exp) {
+            if (lane == 0) s_slot = -2;
+        } else if (wave == 0) {
+            float radius = (kr > 0 && qa_id[kr - 1] >= 0) ? qa_d[kr - 1] : FLT_MAX;
+            if (a.bound) {
+                const float gb = load_agent_f(a.bound + q);
+                if (gb < radius) radius = gb;
+            }
+            const float limit = (radius == FLT_MAX) ? FLT_MAX : radius * (1.f + a.stop_eps);
+            int slot = -1;
+            if (a.policy == SWANN_POLICY_ROUND_ROBIN && a.V > 1) {
+                for (int turn = 0; turn < a.V && slot < 0; ++turn) {
+                    const int want = (s_ctr[0] + turn) % a.V;
+                    if (s_retired[want >> 5] & (1u << (want & 31))) continue;
+                    int found = -1;
+                    for (int b = 0; b < L && found < 0; b += 64) {
+                        const int i = b + lane;
+                        const bool ok = i < L && qa_id[i] >= 0 && qa_e[i] == 0 && qa_l[i] == want;
+                        const uint64_t m = __ballot(ok);
+                        if (m) found = b + __builtin_ctzll(m);
+                    }
+                    if (found < 0 || (early && qa_d[found] > limit)) {
+                        if (lane == 0) s_retired[want >> 5] |= (1u << (want & 31));
+                        continue;
+                    }
+                    slot = found;
+                }
+                if (slot < 0 && !early) {
+                    for (int b = 0; b < L && slot < 0; b += 64) {
+                        const int i = b + lane;
+                        const uint64_t m = __ballot(i < L && qa_id[i] >= 0 && qa_e[i] == 0);
+                        if (m) slot = b + __builtin_ctzll(m);
+                    }
+                }
+            } else {
+                int found = -1;
+                for (int b = 0; b < L && found < 0; b += 64) {
+                    const int i = b + lane;
+                    bool ok = i < L && qa_id[i] >= 0 && qa_e[i] == 0;
+                    if (ok) {
+                        const unsigned li = qa_l[i];
+                        ok = !(s_retired[li >> 5] & (1u << (li & 31)));
+                    }
+                    const uint64_t m = __ballot(ok);
+                    if (m) found = b + __builtin_ctzll(m);
+                }
+                if (found >= 0 && (!early || qa_d[found] <= limit)) slot = found;
+            }
+            if (lane == 0) {
+                s_slot = slot;
+                if (slot >= 0) {
+                    qa_e[slot] = 1;
+                    s_p = qa_id[slot];
+                    s_plin = qa_l[slot];
+                    s_ctr[0] += 1;
+                } else {
+                    s_ctr[3] = 1;
+                }
+                s_nwork = 0; s_nkeep = 0; s_nbr = 0; s_cov = 0;
+            }
+        }
+        for (int i = tid; i < nsort; i += BLOCK) { c_id[i] = -1; c_d[i] = FLT_MAX; c_l[i] = 0; }
+        __syncthreads();
+        if (s_slot < 0) break;
+        const int p = s_p;
+        const uint8_t plin = (uint8_t)s_plin;
+
+        // ---- screen the neighbours, one lane each ----
+        int nbr = 0, cov = 0;
+        for (int nidx = tid; nidx < D; nidx += BLOCK) {
+            const int v = a.G[(int64_t)p * D + nidx];
+            if (v < 0 || v >= a.n) continue;                 // -1 (or out of range): no edge
+            ++nbr;
+            int isnew = 1;
+            if (a.H > 1) isnew = vis_insert(vis, a.H, v, &r_fail);
+            if (!isnew) { ++cov; continue; }
+            int slot = -1, claimed = 0;
+            float d = FLT_MAX;
+            if (a.Hc > 0) {
+                slot = cache_slot(cid, a.Hc, v, &claimed);
+                d = (slot >= 0 && !claimed) ? load_agent_f(cdd + slot) : FLT_MAX;
+            }
+            if (a.exclusive && slot >= 0 && !claimed && d != FLT_MAX) {
+                ++r_hits; ++cov;                                // another branch owns it
+            } else if (d == FLT_MAX) {
+                const int w = atomicAdd(&s_nwork, 1);
+                w_v[w] = v; w_slot[w] = slot; w_nidx[w] = nidx | (claimed << 16);
+            } else {
+                ++r_hits;                                       // cached distance
+                c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin;
+            }
+        }
+        __syncthreads();
+
+        // ---- score the survivors, TEAM lanes per distance ----
+        const int nw = s_nwork;
+        for (int w = team; w < nw; w += NT) {
+            const int v = w_v[w];
+            const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
+                                                 a.vec_ok, a.metric);
+            if (tl == 0) {
+                const int slot = w_slot[w];
+                const int packed = w_nidx[w];
+                const int nidx = packed & 0xffff, claimed = packed >> 16;
+                if (slot >= 0) { store_agent_f(cdd + slot, d); ++r_claim; }
+                ++r_evals;
+                const bool taken = a.exclusive && slot >= 0 && !claimed && d != FLT_MAX;
+                if (taken) ++cov;
+                else { c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin; }
+            }
+        }
+        if (a.crowd_frac > 0.f) { block_add<BLOCK>(&s_nbr, nbr); block_add<BLOCK>(&s_cov, cov); }
+        __syncthreads();
+
+        // ---- keep what can still enter the queue (:607-625) ----
+        const float worst = (qa_id[L - 1] >= 0) ? qa_d[L - 1] : FLT_MAX;
+        for (int i = tid; i < nsort; i += BLOCK) {
+            const int v = c_id[i];
+            const float d = c_d[i];
+            if (v >= 0 && (worst == FLT_MAX || d <= worst)) {
+                const int k = atomicAdd(&s_nkeep, 1);
+                u_id[k] = v; u_d[k] = d; u_l[k] = c_l[i];
+            }
+        }
+        __syncthreads();
+        const int nk = s_nkeep;
+        int msort = 2;
+        while (msort < nk) msort <<= 1;
+        if (msort > nsort) msort = nsort;
+        // rank sort by (d, id); exact duplicates keep their order
+        for (int i = tid; i < nk; i += BLOCK) {
+            const int id = u_id[i]; const float d = u_d[i];
+            int r = 0;
+            for (int t = 0; t < nk; ++t) {
+                const int it = u_id[t]; const float dt = u_d[t];
+                r += (lt(dt, it, d, id) || (dt == d && it == id && t < i)) ? 1 : 0;
+            }
+            k_id[r] = id; k_d[r] = d; k_l[r] = u_l[i];
+        }
+        for (int i = nk + tid; i < msort; i += BLOCK) { k_id[i] = -1; k_d[i] = FLT_MAX; k_l[i] = 0; }
+        if (tid == 0) { s_ctr[8] += nk; s_ctr[9] += 1; }
+        __syncthreads();
+
+        // ---- merge-path into the other buffer (:637-650) ----
+        for (int o = tid; o < L; o += BLOCK) {
+            int lo = o - msort > 0 ? o - msort : 0;
+            int hi = o < L ? o : L;
+            while (lo < hi) {
+                const int i = (lo + hi) >> 1, jj = o - i;
+                if (jj > 0 && !lt(k_d[jj - 1], k_id[jj - 1], qa_d[i], qa_id[i])) lo = i + 1;
+                else hi = i;
+            }
+            const int i = lo, jj = o - i;
+            const bool takeA = (jj >= msort) || (i < L && lt(qa_d[i], qa_id[i], k_d[jj], k_id[jj]));
+            int nid; float nd; uint8_t ne, nl;
+            if (takeA) { nid = qa_id[i]; nd = qa_d[i]; ne = qa_e[i]; nl = qa_l[i]; }
+            else { nid = k_id[jj]; nd = k_d[jj]; ne = 0; nl = k_l[jj]; }
+            if (nid < 0) { nd = FLT_MAX; ne = 1; nl = 0; }
+            qb_id[o] = nid; qb_d[o] = nd; qb_e[o] = ne; qb_l[o] = nl;
+        }
+        __syncthreads();
+        { int* t = qa_id; qa_id = qb_id; qb_id = t; }
+        { float* t = qa_d; qa_d = qb_d; qb_d = t; }
+        { uint8_t* t = qa_e; qa_e = qb_e; qb_e = t; }
+        { uint8_t* t = qa_l; qa_l = qb_l; qb_l = t; }
+
+        // ---- bound, crowd, stall (:655-682) ----
+        if (tid == 0) {
+            if (a.bound && kr > 0 && qa_id[kr - 1] >= 0)
+                __hip_atomic_fetch_min(reinterpret_cast<int*>(a.bound + q),
+                                       __float_as_int(qa_d[kr - 1]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            if (a.crowd_frac > 0.f) {
+                const float cf = (s_nbr > 0) ? ((float)s_cov / (float)s_nbr) : 0.f;
+                if (cf >= a.crowd_frac) {
+                    if (++s_crowd_run >= 2) {
+                        const unsigned li = (unsigned)plin;
+                        s_retired[li >> 5] |= (1u << (li & 31));
+                        s_ctr[7] += 1;
+                        s_crowd_run = 0;
+                    }
+                } else {
+                    s_crowd_run = 0;
+                }
+            }
+            if (a.stall_patience > 0) {
+                const float bk = (kr > 0 && qa_id[kr - 1] >= 0) ? qa_d[kr - 1] : FLT_MAX;
+                if (bk < s_best_k) { s_best_k = bk; s_stall = 0; } else { s_stall += 1; }
+                if (s_stall >= a.stall_patience) s_ctr[6] = 1;
+            }
+        }
+        __syncthreads();
+        if (a.stall_patience > 0 && s_stall >= a.stall_patience) break;
+    }
+
+    block_add<BLOCK>(&s_ctr[1], r_evals);
+    block_add<BLOCK>(&s_ctr[2], r_fail);
+    block_add<BLOCK>(&s_ctr[4], r_hits);
+    block_add<BLOCK>(&s_ctr[5], r_claim);
+    __syncthreads();
+    for (int i = tid; i < L; i += BLOCK) {
+        a.ids[qb + i] = qa_id[i]; a.dist[qb + i] = qa_d[i];
+        a.expd[qb + i] = qa_e[i]; a.lin[qb + i] = qa_l[i];
+    }
+    if (tid < kNctr) ctr[tid] = s_ctr[tid];
+}
+
+// ---------------------------------------------------------------------------
+// merge: local_search.cu:863-919
+constexpr int kMergeBlock = 256;
+
+__global__ __launch_bounds__(kMergeBlock) void merge_kernel(const int32_t* __restrict__ bids,
+                                                           const float* __restrict__ bdist,
+                                                           int32_t* __restrict__ oi,
+                                                           float* __restrict__ od, int64_t Q,
+                                                           int n, int k, int padded) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* sd = reinterpret_cast<float*>(smem);
+    int* si = reinterpret_cast<int*>(sd + padded);
+    const int64_t q = xcd_remap(blockIdx.x, Q);
+    const int64_t base = q * (int64_t)n;
+    for (int i = threadIdx.x; i < padded; i += kMergeBlock) {
+        const bool real = i < n;
+        const int id = real ? bids[base + i] : -1;
+        sd[i] = (real && id >= 0) ? bdist[base + i] : INFINITY;
+        si[i] = id >= 0 ? id : INT32_MAX;
+    }
+    __syncthreads();
+    for (int size = 2; size <= padded; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < padded; i += kMergeBlock) {
+                const int jx = i ^ stride;
+                if (jx > i) {
+                    const bool up = ((i & size) == 0);
+                    const bool l = lt(sd[i], si[i], sd[jx], si[jx]);
+                    if (up != l) {
+                        const float td = sd[i]; sd[i] = sd[jx]; sd[jx] = td;
+                        const int ti = si[i]; si[i] = si[jx]; si[jx] = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (threadIdx.x == 0) {
+        int w = 0;
+        for (int i = 0; i < n && w < k; ++i) {
+            if (si[i] == INT32_MAX) break;
+            if (i > 0 && si[i] == si[i - 1]) continue;
+            oi[q * k + w] = si[i];
+            od[q * k + w] = sd[i];
+            ++w;
+        }
+        for (; w < k; ++w) { oi[q * k + w] = -1; od[q * k + w] = INFINITY; }
+    }
+}
+
+// Sum of counters[:, 2] into *out, one workgroup, no atomics: *out is
+// written, never accumulated, so no clear is needed before it.
+__global__ __launch_bounds__(1024) void overflow_kernel(const int32_t* __restrict__ ctr,
+                                                        int64_t nbranch, int32_t* out) {
+    __shared__ int part[16];
+    int s = 0;
+    for (int64_t i = threadIdx.x; i < nbranch; i += 1024) s += ctr[i * kNctr + 2];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t = 0;
+        for (int w = 0; w < 16; ++w) t += part[w];
+        *out = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+size_t init_lds(int dim, int V) {
+    const int nsort = pow2_at_least(V, 2, kMaxD);
+    return (size_t)((dim + 3) & ~3) * 4 + (size_t)nsort * (4 + 4 + 4 + 4 + 1 + 1 + 1);
+}
+
+size_t advance_lds(int dim, int D, int L) {
+    const int nsort = pow2_at_least(D, 2, kMaxD);
+    return (size_t)((dim + 3) & ~3) * 4 + (size_t)L * (4 + 4 + 4 + 4) +
+           (size_t)nsort * (4 * 9) + (size_t)L * 4 + (size_t)nsort * 3;
+}
+
+int search_block_for(int64_t nbranch) {
+    // SWANN_SEARCH_BLOCK=64|256 pins the workgroup size (tests use it to run
+    // both layouts on the same inputs); read per call, it costs a getenv.
+    const char* e = getenv("SWANN_SEARCH_BLOCK");
+    const int forced = e ? atoi(e) : 0;
+    if (forced == 64 || forced == 256) return forced;
+    // A batch that cannot fill 256 CUs with one-wave branches gets four
+    // waves per branch instead: more neighbours in flight per expansion.
+    return nbranch < 4096 ? 256 : 64;
+}
+
+bool rows_vec_ok(const void* X, int dim, int x_dtype) {
+    const int vec = x_dtype == SWANN_DTYPE_F16 ? 8 : 4;
+    return (dim % vec == 0) && ((uintptr_t)X % 16 == 0);
+}
+
+#define SWANN_DISPATCH(KERNEL, TEAMV, DT, BLK, GRID, LDS, ST, ARGS)                         \
+    do {                                                                                  \
+        if ((DT) == SWANN_DTYPE_F32) {                                                    \
+            SWANN_DISPATCH_T(KERNEL, float, TEAMV, BLK, GRID, LDS, ST, ARGS);             \
+        } else {                                                                          \
+            SWANN_DISPATCH_T(KERNEL, _Float16, TEAMV, BLK, GRID, LDS, ST, ARGS);          \
+        }                                                                                 \
+    } while (0)
+
+#define SWANN_DISPATCH_B(KERNEL, T, TM, BLK, GRID, LDS, ST, ARGS)                          \
+    do {                                                                                  \
+        if ((BLK) == 64)                                                                  \
+            hipLaunchKernelGGL((KERNEL<TM, T, 64>), GRID, dim3(64), LDS, ST, ARGS);       \
+        else                                                                              \
+            hipLaunchKernelGGL((KERNEL<TM, T, 256>), GRID, dim3(256), LDS, ST, ARGS);     \
+    } while (0)
+
+#define SWANN_DISPATCH_T(KERNEL, T, TEAMV, BLK, GRID, LDS, ST, ARGS)                       \
+    do {                                                                                  \
+        switch (TEAMV) {                                                                  \
+            case 4: SWANN_DISPATCH_B(KERNEL, T, 4, BLK, GRID, LDS, ST, ARGS); break;      \
+            case 8: SWANN_DISPATCH_B(KERNEL, T, 8, BLK, GRID, LDS, ST, ARGS); break;      \
+            case 16: SWANN_DISPATCH_B(KERNEL, T, 16, BLK, GRID, LDS, ST, ARGS); break;    \
+            case 32: SWANN_DISPATCH_B(KERNEL, T, 32, BLK, GRID, LDS, ST, ARGS); break;    \
+            default: SWANN_DISPATCH_B(KERNEL, T, 64, BLK, GRID, LDS, ST, ARGS); break;    \
+        }                                                                                 \
+    } while (0)
+
+}  // namespace
+}  // namespace swann
+
+using namespace swann;
+
+extern "C" {
+
+int swann_validate_init(int64_t n, int dim, int x_dtype, int64_t Q, int J, int V, int L,
+                        int H, int metric, int team_size, int Hc) {
+    clear_error();
+    SWANN_REQUIRE(n > 0 && dim > 0, "X must be a non-empty [n, dim] matrix");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(team_size == 4 || team_size == 8 || team_size == 16 || team_size == 32 ||
+                      team_size == 64,
+                  "team_size must be 4, 8, 16, 32 or 64");
+    SWANN_REQUIRE(Q >= 0 && J >= 1, "need Q >= 0 queries and J >= 1 branches");
+    SWANN_REQUIRE(V >= 1 && V <= kMaxV, "seeds per branch must be in 1..%d (the init sort buffer)",
+                  kMaxV);
+    SWANN_REQUIRE(L >= 1 && L <= kMaxL, "L must be in 1..%d", kMaxL);
+    SWANN_REQUIRE(is_pow2(H), "visited table size must be a power of two");
+    SWANN_REQUIRE(Hc == 0 || is_pow2(Hc), "cache size must be a power of two");
+    SWANN_REQUIRE(Q * (int64_t)J <= (int64_t)INT32_MAX / 64,
+                  "Q*J = %lld branches exceed the launch limit", (long long)(Q * J));
+    const size_t lds = init_lds(dim, V);
+    SWANN_REQUIRE(lds <= kMaxLds, "init needs %zu B of LDS (limit %zu); lower the dimension", lds,
+                  kMaxLds);
+    return SWANN_OK;
+}
+
+int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, int J, int L,
+                           int H, int metric, int team_size, int policy, int V, int Hc,
+                           int64_t nactive, int has_codes) {
+    clear_error();
+    SWANN_REQUIRE(n > 0 && dim > 0, "X must be a non-empty [n, dim] matrix");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(team_size == 4 || team_size == 8 || team_size == 16 || team_size == 32 ||
+                      team_size == 64,
+                  "team_size must be 4, 8, 16, 32 or 64");
+    SWANN_REQUIRE(D >= 1 && D <= kMaxD, "graph degree exceeds MAXD (%d)", kMaxD);
+    SWANN_REQUIRE(L >= 1 && L <= kMaxL, "L exceeds MAXL (%d)", kMaxL);
+    SWANN_REQUIRE(V >= 1 && V <= 256, "lineage count exceeds 256 (lineage is a uint8)");
+    SWANN_REQUIRE(policy == SWANN_POLICY_BEST || policy == SWANN_POLICY_ROUND_ROBIN,
+                  "policy must be 0 (best) or 1 (round robin)");
+    SWANN_REQUIRE(is_pow2(H), "visited table size must be a power of two");
+    SWANN_REQUIRE(Hc == 0 || is_pow2(Hc), "cache size must be a power of two");
+    SWANN_REQUIRE(Q >= 0 && J >= 1, "need Q >= 0 queries and J >= 1 branches");
+    SWANN_REQUIRE(nactive >= 0 && nactive <= Q * (int64_t)J, "active list longer than Q*J");
+    SWANN_REQUIRE(Q * (int64_t)J <= (int64_t)INT32_MAX / 64,
+                  "Q*J = %lld branches exceed the launch limit", (long long)(Q * J));
+    SWANN_REQUIRE(!has_codes,
+                  "the sign-code filter is not supported by this build (pass codes=None)");
+    const size_t lds = advance_lds(dim, D, L);
+    SWANN_REQUIRE(lds <= kMaxLds, "advance needs %zu B of LDS (limit %zu); lower L or the dimension",
+                  lds, kMaxLds);
+    return SWANN_OK;
+}
+
+int swann_init_states(const void* X, int x_dtype, int64_t n, int dim, const float* Qv, int64_t Q,
+                      const int32_t* seeds, int J, int V, int32_t* ids, float* dist,
+                      uint8_t* expd, uint8_t* lin, int L, int32_t* visited, int H,
+                      int32_t* counters, int metric, int team_size, int32_t* cache_id,
+                      float* cache_d, int Hc, float* bound, void* stream) {
+    int rc = swann_validate_init(n, dim, x_dtype, Q, J, V, L, H, metric, team_size, Hc);
+    if (rc) return rc;
+    SWANN_REQUIRE(Q == 0 || (X && Qv && seeds && ids && dist && expd && lin && visited && counters),
+                  "init_states: a required pointer is NULL");
+    SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "init_states: Hc > 0 needs cache_id and cache_d");
+    if (Q == 0) return SWANN_OK;
+    InitArgs a{X, Qv, seeds, ids, dist, expd, lin, visited, counters, dim, J, V, L, H, metric,
+               Q, n, Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound,
+               rows_vec_ok(X, dim, x_dtype) ? 1 : 0};
+    const int64_t nb = Q * J;
+    const int block = search_block_for(nb);
+    SWANN_DISPATCH(init_kernel, team_size, x_dtype, block, dim3((unsigned)nb), init_lds(dim, V),
+                   (hipStream_t)stream, a);
+    return launch_status("init_states");
+}
+
+int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t* G, int D,
+                  const float* Qv, int64_t Q, int J, int32_t* ids, float* dist, uint8_t* expd,
+                  uint8_t* lin, int L, int32_t* visited, int H, int32_t* counters, int metric,
+                  int team_size, int delta, int max_expansions, int policy, int V, float stop_eps,
+                  int kstop, int32_t* cache_id, float* cache_d, int Hc, float* bound,
+                  int exclusive, int stall_patience, float crowd_frac, const int32_t* active,
+                  int64_t nactive, const int32_t* codes, int cwords, const float* alpha,
+                  const float* cmu, float code_margin, void* stream) {
+    (void)cwords; (void)alpha; (void)cmu; (void)code_margin;
+    int rc = swann_validate_advance(n, dim, x_dtype, D, Q, J, L, H, metric, team_size, policy, V,
+                                    Hc, active ? nactive : 0, codes != nullptr);
+    if (rc) return rc;
+    SWANN_REQUIRE(Q == 0 || (X && G && Qv && ids && dist && expd && lin && visited && counters),
+                  "advance: a required pointer is NULL");
+    SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "advance: Hc > 0 needs cache_id and cache_d");
+    SWANN_REQUIRE(!exclusive || Hc > 0, "advance: exclusive claims need the shared table");
+    const int64_t nb = active ? nactive : Q * J;
+    if (nb == 0 || delta <= 0) return SWANN_OK;
+    AdvArgs a{X, G, Qv, ids, dist, expd, lin, visited, counters, dim, D, J, L, H, metric,
+              delta, max_expansions, policy, V, stop_eps, kstop,
+              Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound, exclusive ? 1 : 0,
+              stall_patience, crowd_frac, active, nb, Q * J, n,
+              rows_vec_ok(X, dim, x_dtype) ? 1 : 0};
+    const int block = search_block_for(nb);
+    SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
+                   advance_lds(dim, D, L), (hipStream_t)stream, a);
+    return launch_status("advance");
+}
+
+int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk, int k,
+                         int32_t* out_ids, float* out_dist, void* stream) {
+    clear_error();
+    SWANN_REQUIRE(V >= 1 && kk >= 1, "expected (Q, V, kk) branch results with V, kk >= 1");
+    const int64_t n = (int64_t)V * kk;
+    SWANN_REQUIRE(k > 0 && k <= n, "k must be in 1..V*kk");
+    SWANN_REQUIRE(n <= kMergeMax, "merge of %lld candidates exceeds %d; lower V or the per-branch k",
+                  (long long)n, kMergeMax);
+    SWANN_REQUIRE(Q >= 0 && Q <= INT32_MAX, "Q out of range");
+    if (Q == 0) return SWANN_OK;
+    SWANN_REQUIRE(bids && bdist && out_ids && out_dist, "merge: a required pointer is NULL");
+    int padded = 1;
+    while (padded < n) padded <<= 1;
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)Q), dim3(kMergeBlock),
+                       (size_t)padded * 8, (hipStream_t)stream, bids, bdist, out_ids, out_dist, Q,
+                       (int)n, k, padded);
+    return launch_status("merge_branches");
+}
+
+int swann_overflow_async(const int32_t* counters, int64_t nbranch, int32_t* out, void* stream) {
+    clear_error();
+    SWANN_REQUIRE(nbranch >= 0 && out, "overflow: need an output pointer");
+    SWANN_REQUIRE(nbranch == 0 || counters, "overflow: counters is NULL");
+    hipLaunchKernelGGL(overflow_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, counters,
+                       nbranch, out);
+    return launch_status("overflow");
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+"""The public interface: build an index over vectors, then search it
+(swann/index.py).
+
+    import swann_amd as swann
+    index = swann.Index.build(X, metric="ip")      # X: (n, d) float32 or float16
+    ids, dist = index.search(Q, k=10)
+
+Same classes, signatures, knobs and file format as the reference.  Two
+deliberate differences: there is no 65535-query cap (the kernels run on a
+1-D grid), and the overflow check no longer costs its own host
+synchronisation: it is computed on the device with the search and read after
+the results' own copy back.
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _engine as E
+from . import _select as S
+
+METRICS = {"ip": E.METRIC_IP, "l2": E.METRIC_L2}
+
+
+@dataclass
+class SearchConfig:
+    """Knobs, with the reference's defaults (swann/index.py:26-45).
+
+    branches  trajectories one query is split into (workgroups per query).
+    queue     width of each branch's candidate queue.
+    budget    cap on expansions per branch; `stop_eps` usually binds first.
+    stop_eps  stop a branch once its best candidate is worse than the query's
+              current k-th answer by this fraction; negative disables it.
+    team      lanes cooperating on one distance (4, 8, 16, 32 or 64).
+    """
+    branches: int = 32
+    queue: int = 12
+    budget: int = 64
+    stop_eps: float = 0.05
+    team: int = 16
+    k: int = 10
+
+
+class Index:
+    """A proximity graph plus the vectors it indexes, resident on one GPU."""
+
+    def __init__(self, vectors: torch.Tensor, graph: torch.Tensor, metric: str = "ip",
+                 catalogue: torch.Tensor | None = None, catalogue_size: int = 4096,
+                 seed: int = 0):
+        if vectors.device.type != "cuda":
+            raise ValueError("vectors must already be on the GPU")
+        if vectors.dtype not in (torch.float32, torch.float16):
+            raise ValueError("vectors must be float32 or float16")
+        if metric not in METRICS:
+            raise ValueError(f"metric must be one of {sorted(METRICS)}")
+        self.X = vectors.contiguous()
+        self.G = graph.to(device=self.X.device, dtype=torch.int32).contiguous()
+        if self.G.dim() != 2 or self.G.shape[0] != self.X.shape[0]:
+            raise ValueError(f"graph must be [n, degree] with n = {self.X.shape[0]}")
+        self.metric = metric
+        self._m = METRICS[metric]
+        if catalogue is None:
+            n = self.X.shape[0]
+            rng = np.random.default_rng(seed)
+            pick = np.sort(rng.permutation(n)[:min(catalogue_size, n)])
+            catalogue = torch.from_numpy(pick.astype(np.int64)).to(self.X.device)
+        self.catalogue = catalogue.to(device=self.X.device, dtype=torch.int64)
+        self._cat = S.pool_vectors(self.X, self.catalogue)
+        self._flag = None
+
+    # -- construction ----------------------------------------------------
+    @classmethod
+    def build(cls, vectors, metric: str = "ip", degree: int = 96, candidates: int = 128,
+              alpha: float = 1.2, **kw) -> "Index":
+        """Build a graph over `vectors` on the GPU (sweep, prune, reverse)."""
+        from .build import build_graph
+        X = _as_cuda(vectors)
+        G = build_graph(X, metric=metric, degree=degree, candidates=candidates, alpha=alpha)
+        return cls(X, G, metric=metric, **kw)
+
+    # -- search ----------------------------------------------------------
+    def search_async(self, queries, k: int = 10, config: SearchConfig | None = None,
+                     **overrides):
+        """Launch a search and return device tensors (ids, dist, state,
+        overflow) without synchronising; `overflow` is a device scalar."""
+        cfg = config or SearchConfig(k=k)
+        for key, value in overrides.items():
+            if not hasattr(cfg, key):
+                raise TypeError(f"unknown search option {key!r}")
+            setattr(cfg, key, value)
+        Q = _as_cuda(queries).float().contiguous()
+        entries = S.select_nearest(Q, self._cat, cfg.branches, metric=self._m)
+        seeds = self.catalogue[entries].to(torch.int32)
+        ids, dist, st = E.search(
+            self.X, self.G, Q, seeds, k=k, L=cfg.queue, B=cfg.budget, metric=self._m,
+            team_size=cfg.team, stop_eps=cfg.stop_eps, shared_cache=True, shared_bound=True,
+            exclusive=True, elide_visited=True, check=False)
+        return ids, dist, st, st.overflow()
+
+    def search(self, queries, k: int = 10, config: SearchConfig | None = None, **overrides):
+        """Return (ids, distances), each (nq, k), as numpy arrays
+        (swann/index.py:86-110)."""
+        ids, dist, st, over = self.search_async(queries, k=k, config=config, **overrides)
+        if self._flag is None:
+            self._flag = torch.empty((), dtype=torch.int32, pin_memory=True)
+        flag = self._flag
+        if E._OVERFLOW_GUARD:
+            flag.copy_(over, non_blocking=True)
+        ids_h, dist_h = ids.cpu().numpy(), dist.cpu().numpy()     # synchronises
+        if E._OVERFLOW_GUARD and int(flag):
+            raise RuntimeError(f"visited table overflowed ({int(flag)} failed inserts)")
+        return ids_h, dist_h
+
+    # -- persistence -----------------------------------------------------
+    def save(self, path) -> None:
+        """Write graph.npy, catalogue.npy and index.json (swann/index.py:113-122)."""
+        path = Path(path)
+        path.mkdir(parents=True, exist_ok=True)
+        np.save(path / "graph.npy", self.G.cpu().numpy())
+        np.save(path / "catalogue.npy", self.catalogue.cpu().numpy())
+        (path / "index.json").write_text(json.dumps(
+            {"metric": self.metric, "n": int(self.X.shape[0]), "d": int(self.X.shape[1]),
+             "degree": int(self.G.shape[1])}, indent=2))
+
+    @classmethod
+    def load(cls, path, vectors) -> "Index":
+        path = Path(path)
+        meta = json.loads((path / "index.json").read_text())
+        G = torch.from_numpy(np.load(path / "graph.npy", allow_pickle=False)).cuda()
+        cat = torch.from_numpy(np.load(path / "catalogue.npy", allow_pickle=False)).cuda()
+        return cls(_as_cuda(vectors), G, metric=meta["metric"], catalogue=cat)
+
+    def __repr__(self) -> str:
+        n, d = self.X.shape
+        return (f"Index(n={n:,}, d={d}, degree={self.G.shape[1]}, "
+                f"metric={self.metric!r}, dtype={self.X.dtype})")
+
+
+def _as_cuda(a) -> torch.Tensor:
+    if isinstance(a, np.ndarray):
+        a = torch.from_numpy(np.ascontiguousarray(a))
+    if a.device.type != "cuda":
+        a = a.cuda()
+    return a.contiguous()

@@ -1,0 +1,174 @@
+"""The public interface on the GPU, end to end (the reference's
+tests/test_index.py), plus seed selection and the build stages against the
+oracle and the reference's golden build vectors."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import gaussian, golden, regen
+from test_oracle_helpers import exact_topk, recall
+
+pytestmark = pytest.mark.gpu
+
+swann = pytest.importorskip("swann_amd")
+from swann_amd import _select as S  # noqa: E402
+from swann_amd import build as B  # noqa: E402
+
+
+def note(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def corpus(n=8000, d=128, nq=200, seed=0, normalise=True):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, d), dtype=np.float32)
+    Q = rng.standard_normal((nq, d), dtype=np.float32)
+    if normalise:
+        X /= np.linalg.norm(X, axis=1, keepdims=True)
+        Q /= np.linalg.norm(Q, axis=1, keepdims=True)
+    return X, Q
+
+
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_recall_is_high(metric):
+    note("recall", metric)
+    X, Q = corpus(normalise=(metric == "ip"))
+    index = swann.Index.build(X, metric=metric, degree=48, candidates=64)
+    ids, dist = index.search(Q, k=10)
+    assert ids.shape == (Q.shape[0], 10) and dist.shape == ids.shape
+    r = recall(ids, exact_topk(X, Q, 10, 0 if metric == "ip" else 1), 10)
+    note("recall", metric, r)
+    assert r > 0.90
+
+
+def test_more_branches_do_not_lose_recall():
+    X, Q = corpus()
+    index = swann.Index.build(X, degree=48, candidates=64)
+    truth = exact_topk(X, Q, 10)
+    few = recall(index.search(Q, k=10, branches=8)[0], truth, 10)
+    many = recall(index.search(Q, k=10, branches=64)[0], truth, 10)
+    assert many >= few - 1e-9
+
+
+def test_round_trip(tmp_path):
+    X, Q = corpus()
+    index = swann.Index.build(X, degree=48, candidates=64)
+    before, _ = index.search(Q, k=10)
+    index.save(tmp_path / "ix")
+    again = swann.Index.load(tmp_path / "ix", X)
+    assert torch.equal(again.G, index.G) and torch.equal(again.catalogue, index.catalogue)
+    after, _ = again.search(Q, k=10)
+    # claims and the bound are racy: the answers agree, up to rare reorders
+    assert (before == after).mean() > 0.99
+
+
+def test_batch_beyond_65535_is_served():
+    """The reference refuses more than 65535 queries; the 1-D grid does not."""
+    X, _ = corpus(n=2000)
+    index = swann.Index.build(X, degree=32, candidates=48)
+    Q = np.ascontiguousarray(np.repeat(X[:700], 100, axis=0))       # 70,000 queries
+    ids, dist = index.search(Q, k=10, branches=2)
+    assert ids.shape == (70000, 10)
+    assert (ids[:, 0] == np.repeat(np.arange(700), 100)).mean() > 0.95
+
+
+def test_unknown_option_is_a_type_error():
+    X, Q = corpus(n=1000)
+    index = swann.Index.build(X, degree=16, candidates=32)
+    with pytest.raises(TypeError):
+        index.search(Q, k=10, banches=4)
+
+
+def test_fp16_corpus_distances_within_tolerance():
+    """fp16 corpus, fp32 queries: returned distances equal exact fp32
+    recomputation on the fp16 values to 2e-3."""
+    X, Q = corpus(n=6000)
+    X16 = X.astype(np.float16)
+    index = swann.Index(torch.from_numpy(X16).cuda(),
+                        B.build_graph(torch.from_numpy(X).cuda(), degree=32, candidates=64),
+                        metric="ip")
+    ids, dist = index.search(Q, k=10)
+    Xf = X16.astype(np.float64)
+    for q in range(0, Q.shape[0], 7):
+        for i, dv in zip(ids[q], dist[q]):
+            if i >= 0:
+                assert abs(dv - (1.0 - Q[q].astype(np.float64) @ Xf[i])) < 2e-3
+
+
+def test_select_matches_oracle():
+    g = golden("refcpu_c1.npz")
+    X = regen(10000, 128, 0, True, g["X_sha"])
+    cat = g["catalogue"].astype(np.int64)
+    Vp = torch.from_numpy(X[cat]).cuda()
+    for metric in (0, 1):
+        idx = S.select_nearest(torch.from_numpy(g["Q"]).cuda(), Vp, 8, metric=metric)
+        want, _ = O.select_nearest(g["Q"], X[cat], 8, metric, nthreads=8)
+        agree = (idx.cpu().numpy() == want).mean()
+        note("select", metric, agree)
+        assert agree > 0.995
+        if metric == 0:
+            assert (cat[idx.cpu().numpy()] == g["seeds"].astype(np.int64)).mean() > 0.995
+
+
+@pytest.mark.parametrize("tag,metric", [("ip", 0), ("l2", 1)])
+def test_build_stages_match_reference(tag, metric):
+    g = golden("refbuild_small.npz")
+    X = torch.from_numpy(g[f"{tag}_X"]).cuda()
+    m = "ip" if metric == 0 else "l2"
+    cand, cdist = B.knn_candidates(X, 32, metric=m)
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    c_same = (cand.cpu().numpy() == rc).mean()
+    note("sweep", tag, c_same)
+    assert c_same > 0.99
+    assert np.allclose(cdist.cpu().numpy(), rd, atol=3e-5, rtol=1e-5)
+    Gp = B.robust_prune(X, torch.from_numpy(rc).cuda(), torch.from_numpy(rd).cuda(), 16,
+                        alpha=1.2, metric=m).cpu().numpy()
+    rows_p = (Gp == g[f"{tag}_Gp"].astype(np.int32)).all(1).mean()
+    note("prune", tag, rows_p)
+    assert rows_p > 0.98
+    Gf = B.add_reverse(X, torch.from_numpy(g[f"{tag}_Gp"].astype(np.int32)).cuda(), 16,
+                       alpha=1.2, metric=m).cpu().numpy()
+    same_sets = np.mean([set(a) == set(b) for a, b in zip(Gf, g[f"{tag}_Gf"].astype(np.int32))])
+    note("reverse", tag, same_sets)
+    assert same_sets > 0.97
+
+
+def test_build_matches_oracle_exactly_where_it_can():
+    """Against the oracle's restatement on one corpus: the same candidate
+    lists, and the prune of identical inputs gives identical rows."""
+    X = gaussian(3000, 40, 313, False)
+    Xg = torch.from_numpy(X).cuda()
+    cand, cdist = B.knn_candidates(Xg, 48, metric="l2")
+    oc, od = O.knn_candidates(X, 48, O.METRIC_L2, nthreads=8)
+    assert (cand.cpu().numpy() == oc).mean() > 0.995
+    Gp = B.robust_prune(Xg, torch.from_numpy(oc).cuda(), torch.from_numpy(od).cuda(), 24,
+                        metric="l2").cpu().numpy()
+    Op = O.robust_prune(X, oc, od, 24, 1.2, O.METRIC_L2, nthreads=8)
+    assert (Gp == Op).all(1).mean() > 0.99
+
+
+def test_c1_built_graph_recall_matches_reference_graph():
+    """The GPU-built C1 graph gives recall within 0.005 of the reference-built
+    graph (tests/golden/refcpu_c1.npz) under the same search."""
+    from swann_amd import _engine as E
+    g = golden("refcpu_c1.npz")
+    X = regen(10000, 128, 0, True, g["X_sha"])
+    Xg = torch.from_numpy(X).cuda()
+    G_gpu = B.build_graph(Xg, metric="ip", degree=32, candidates=64, alpha=1.2)
+    G_ref = torch.from_numpy(g["G"].astype(np.int32)).cuda()
+    Q = gaussian(2000, 128, 777, True)
+    Qg = torch.from_numpy(Q).cuda()
+    cat = torch.from_numpy(g["catalogue"].astype(np.int64)).cuda()
+    seeds = cat[S.select_nearest(Qg, Xg[cat], 8, metric=0)].to(torch.int32)
+    truth = exact_topk(X, Q, 10)
+    rs = []
+    for G in (G_gpu, G_ref):
+        ids, _, _ = E.search(Xg, G, Qg, seeds, k=10, L=12, B=64, metric=0, team_size=16,
+                             stop_eps=0.05)
+        rs.append(recall(ids.cpu().numpy(), truth, 10))
+    note("C1 graph recall gpu-built / reference-built", rs)
+    assert rs[0] >= rs[1] - 0.005

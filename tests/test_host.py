@@ -1,0 +1,133 @@
+"""Host-side checks that need no GPU: the C ABI loads and exports what its
+header declares, argument validation refuses what the reference refuses
+(swann/csrc/local_search.cu:726-841), the sizing closed forms, the tensor
+merge against the oracle, and the product refusing to run without a GPU."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import ROOT
+
+from swann_amd import _engine as E
+from swann_amd import _lib
+from swann_amd.index import SearchConfig
+
+HEADER = ROOT / "include" / "swann_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int64_t|int)\s+(swann_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 15, names
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in swann_amd.h but not exported"
+        assert name in _lib.PROTOTYPES, f"{name} has no ctypes prototype"
+    assert set(_lib.PROTOTYPES) == set(names)
+    assert b"gfx950" in L.swann_version()
+
+
+def _vinit(**kw):
+    a = dict(n=1000, dim=128, x_dtype=0, Q=4, J=2, V=1, L=16, H=1024, metric=0, team_size=16, Hc=0)
+    a.update(kw)
+    return _lib.lib().swann_validate_init(*a.values())
+
+
+def _vadv(**kw):
+    a = dict(n=1000, dim=128, x_dtype=0, D=32, Q=4, J=2, L=16, H=1024, metric=0, team_size=16,
+             policy=0, V=1, Hc=0, nactive=0, has_codes=0)
+    a.update(kw)
+    return _lib.lib().swann_validate_advance(*a.values())
+
+
+def _err():
+    return _lib.lib().swann_last_error().decode()
+
+
+def test_validation_accepts_the_reference_configs():
+    assert _vinit() == 0 and _vadv() == 0
+    for team in (4, 8, 16, 32, 64):
+        assert _vinit(team_size=team) == 0 and _vadv(team_size=team) == 0
+    # C3/C4 shapes: d=1536 and 4096 fp16, D=64, L=12
+    assert _vadv(dim=1536, x_dtype=1, D=64, L=12, Q=10000, J=32, H=1, Hc=131072) == 0
+    assert _vadv(dim=4096, x_dtype=1, D=64, L=12, Q=512, J=128, H=1, Hc=524288) == 0
+    # no 65535-query cap
+    assert _vinit(Q=70000, J=32) == 0 and _vadv(Q=70000, J=32) == 0
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(team_size=3), "team_size"),
+    (dict(L=513), "L"),
+    (dict(H=1000), "power of two"),
+    (dict(Hc=1000), "power of two"),
+    (dict(V=129), "seeds per branch"),
+    (dict(metric=2), "metric"),
+    (dict(x_dtype=5), "float32 or float16"),
+    (dict(dim=40000), "LDS"),
+])
+def test_init_validation_refuses(kw, msg):
+    assert _vinit(**kw) != 0
+    assert msg in _err()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=129), "MAXD"),
+    (dict(L=600), "MAXL"),
+    (dict(V=300), "uint8"),
+    (dict(policy=7), "policy"),
+    (dict(has_codes=1), "sign-code"),
+    (dict(nactive=100), "active"),
+    (dict(dim=20000), "LDS"),
+])
+def test_advance_validation_refuses(kw, msg):
+    assert _vadv(**kw) != 0
+    assert msg in _err()
+
+
+def test_sizing_closed_forms():
+    """_engine.py:66-77, :186-198 at the configs' shapes."""
+    assert E.visited_size(64, 64) == 16384 and E.visited_size(64, 32) == 8192
+    assert E.cache_size(8, 64, 32) == 16384          # C1
+    assert E.cache_size(32, 64, 64) == 131072        # C2/C3
+    assert E.cache_size(128, 64, 64) == 524288       # C4, J=128
+    assert E.cache_size(10_000, 64, 64) == 1 << 20   # the cap
+    assert E.cache_size(8, 64, 32) == O.cache_size(8, 64, 32)
+    assert E.visited_size(12, 32) == O.visited_size(12, 32)
+
+
+def test_search_config_defaults():
+    c = SearchConfig()
+    assert (c.branches, c.queue, c.budget, c.stop_eps, c.team, c.k) == (32, 12, 64, 0.05, 16, 10)
+
+
+def test_tensor_merge_matches_oracle():
+    rng = np.random.default_rng(3)
+    Q, V, kk, k = 30, 6, 10, 10
+    ids = rng.integers(-1, 50, (Q, V, kk)).astype(np.int32)
+    base = rng.random(50).astype(np.float32)
+    dist = np.where(ids >= 0, base[np.clip(ids, 0, None)], np.float32(3e38)).astype(np.float32)
+    oi, od = E._merge_branches_tensor(torch.from_numpy(ids), torch.from_numpy(dist), k)
+    wi, wd = O.merge(ids, dist, k)
+    assert np.array_equal(oi.numpy(), wi)
+    assert np.array_equal(od.numpy(), wd)
+
+
+def test_product_refuses_cpu_tensors():
+    X = torch.zeros((10, 8))
+    with pytest.raises(RuntimeError):
+        E.init_states(X, X[:2].clone(), torch.zeros((2, 1), dtype=torch.int32), D=4)
+
+
+def test_no_oracle_in_the_product():
+    """The product package never imports the oracle."""
+    for f in (ROOT / "swann_amd").rglob("*.py"):
+        text = f.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, f
