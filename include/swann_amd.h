@@ -129,29 +129,34 @@ int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, i
                          void* workspace, void* stream);
 
 /* ---- graph build -------------------------------------------------------
+ * X [n, dim] is fp32 or fp16 (x_dtype); an fp16 corpus is read as fp16 and
+ * upcast exactly, which equals the reference's X.float() (build.py:167).
+ *
  * Sweep (build.py:28-43): exact top-C neighbours of every row, self
- * excluded, ascending, as (cand [n, C] int32, cdist [n, C] fp32).  Scores
- * are screened with bf16 MFMA tiles over a bf16 copy of X and the survivors
- * re-ranked in fp32 (IP: 1 - <a,b>; L2: max(0, |b|^2 - 2<a,b> + |a|^2)).
- * X [n, dim] fp32.  `workspace`: swann_sweep_workspace_size bytes. */
-int64_t swann_sweep_workspace_size(int64_t n, int dim, int C);
-int swann_build_sweep(const float* X, int64_t n, int dim, int metric, int C,
+ * excluded (3.4e38), ascending, as (cand [n, C] int32, cdist [n, C] fp32) with
+ * IP: 1 - <a,b>; L2: max(0, |b|^2 - 2<a,b> + |a|^2).  When dim % 8 == 0 the
+ * scores come from fp16 MFMA tiles (fp16 corpus: exact products; fp32 corpus:
+ * a three-term hi/lo split, ~22 significant bits); otherwise from fp32 SIMT
+ * tiles.  `workspace`: swann_sweep_workspace_size bytes. */
+int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C);
+int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric, int C,
                       int32_t* cand, float* cdist, void* workspace, void* stream);
 
 /* Prune (build.py:46-91): keep candidate i of node u unless an already kept
- * w satisfies alpha * d(w, i) <= d(u, i); deg kept ids per row, -1 padded. */
-int swann_build_prune(const float* X, int64_t n, int dim, int metric, const int32_t* cand,
-                      const float* cdist, int C, int deg, float alpha, int32_t* out,
-                      void* stream);
+ * w satisfies alpha * d(w, i) <= d(u, i); deg kept ids per row, -1 padded.
+ * C <= 128. */
+int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                      const int32_t* cand, const float* cdist, int C, int deg, float alpha,
+                      int32_t* out, void* stream);
 
 /* Reverse (build.py:94-150): offer every edge u->v back to v (ascending
  * source, at most max_in per target), dedup [G_u | in_u] minus self, score
  * exactly, keep the nearest 128 and prune to deg.
  * `workspace`: swann_reverse_workspace_size bytes. */
 int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in);
-int swann_build_reverse(const float* X, int64_t n, int dim, int metric, const int32_t* G,
-                        int deg, float alpha, int max_in, int32_t* out, void* workspace,
-                        void* stream);
+int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                        const int32_t* G, int deg, float alpha, int max_in, int32_t* out,
+                        void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

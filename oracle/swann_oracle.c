@@ -77,8 +77,20 @@ static float so_half_to_float(uint16_t h) {
 
 float so_half_to_float_export(uint16_t h) { return so_half_to_float(h); }
 
+/* The same conversion through a 64K-entry table, filled once (thread-safe:
+ * every writer stores identical values). */
+static float so_h2f_table[65536];
+static volatile int so_h2f_ready = 0;
+
+static void so_h2f_init(void) {
+    if (so_h2f_ready) return;
+    for (uint32_t h = 0; h < 65536u; ++h) so_h2f_table[h] = so_half_to_float((uint16_t)h);
+    __sync_synchronize();
+    so_h2f_ready = 1;
+}
+
 static inline float so_elem(const void* X, int dt, int64_t i) {
-    return dt == SO_F16 ? so_half_to_float(((const uint16_t*)X)[i]) : ((const float*)X)[i];
+    return dt == SO_F16 ? so_h2f_table[((const uint16_t*)X)[i]] : ((const float*)X)[i];
 }
 
 /* One distance in the kernel's order: lane l owns the blocks of `vec`
@@ -86,6 +98,7 @@ static inline float so_elem(const void* X, int dt, int64_t i) {
  * the halving tree off = team/2 .. 1.  IP returns 1 - dot. */
 float so_team_distance(const float* q, const void* X, int dt, int64_t row, int dim,
                        int metric, int team) {
+    if (dt == SO_F16) so_h2f_init();
     float lanes[64];
     const int vec = (dt == SO_F16) ? 8 : 4;
     const int64_t off0 = row * (int64_t)dim;

@@ -25,10 +25,17 @@ def _m(metric) -> int:
     return int(metric)
 
 
-def _f32(X):
+_DT = {torch.float32: 0, torch.float16: 1}
+
+
+def _rows(X):
+    """The corpus as the kernels read it: fp16 stays fp16 (its exact upcast is
+    the reference's X.float()), anything else becomes fp32."""
     if not X.is_cuda:
         raise RuntimeError("the build runs on the GPU: move the vectors to cuda first")
-    return X.float().contiguous()
+    if X.dtype not in _DT:
+        X = X.float()
+    return X.contiguous()
 
 
 def pairwise(A, B, metric, bn=None):
@@ -45,15 +52,15 @@ def knn_candidates(Xg, C, chunk=4096, metric="ip"):
     """Exact top-C neighbours by the corpus's metric, self excluded
     (swann/build.py:28-43).  Returns (int32 [n, C], float32 [n, C]), ascending."""
     del chunk
-    Xg = _f32(Xg)
+    Xg = _rows(Xg)
     n, d = Xg.shape
     idx = torch.empty((n, C), dtype=torch.int32, device=Xg.device)
     dst = torch.empty((n, C), dtype=torch.float32, device=Xg.device)
-    ws = torch.empty(int(lib().swann_sweep_workspace_size(n, d, C)), dtype=torch.uint8,
-                     device=Xg.device)
+    ws = torch.empty(int(lib().swann_sweep_workspace_size(n, d, _DT[Xg.dtype], C)),
+                     dtype=torch.uint8, device=Xg.device)
     with torch.cuda.device(Xg.device):
-        call("swann_build_sweep", ptr(Xg), n, d, _m(metric), int(C), ptr(idx), ptr(dst), ptr(ws),
-             stream_of(Xg.device))
+        call("swann_build_sweep", ptr(Xg), _DT[Xg.dtype], n, d, _m(metric), int(C), ptr(idx),
+             ptr(dst), ptr(ws), stream_of(Xg.device))
     return idx, dst
 
 
@@ -66,14 +73,14 @@ def robust_prune(Xg, cand, cdist, deg, alpha=1.2, chunk=4096, deg_per_node=None,
     if deg_per_node is not None or protect is not None:
         raise NotImplementedError("per-node degrees and mutual protection are offline-builder "
                                   "extras not built in swann_amd")
-    Xg = _f32(Xg)
+    Xg = _rows(Xg)
     cand = cand.to(device=Xg.device, dtype=torch.int32).contiguous()
     cdist = cdist.to(device=Xg.device, dtype=torch.float32).contiguous()
     n, C = cand.shape
     out = torch.empty((n, deg), dtype=torch.int32, device=Xg.device)
     with torch.cuda.device(Xg.device):
-        call("swann_build_prune", ptr(Xg), n, Xg.shape[1], _m(metric), ptr(cand), ptr(cdist),
-             int(C), int(deg), float(alpha), ptr(out), stream_of(Xg.device))
+        call("swann_build_prune", ptr(Xg), _DT[Xg.dtype], n, Xg.shape[1], _m(metric), ptr(cand),
+             ptr(cdist), int(C), int(deg), float(alpha), ptr(out), stream_of(Xg.device))
     return out
 
 
@@ -85,7 +92,7 @@ def add_reverse(Xg, G, deg, chunk=2048, alpha=1.2, max_in=64, deg_per_node=None,
     if deg_per_node is not None:
         raise NotImplementedError("per-node degrees are an offline-builder extra not built "
                                   "in swann_amd")
-    Xg = _f32(Xg)
+    Xg = _rows(Xg)
     G = G.to(device=Xg.device, dtype=torch.int32).contiguous()
     n, d = Xg.shape
     if G.shape[1] != deg:
@@ -94,8 +101,8 @@ def add_reverse(Xg, G, deg, chunk=2048, alpha=1.2, max_in=64, deg_per_node=None,
     ws = torch.empty(int(lib().swann_reverse_workspace_size(n, deg, max_in)), dtype=torch.uint8,
                      device=Xg.device)
     with torch.cuda.device(Xg.device):
-        call("swann_build_reverse", ptr(Xg), n, d, _m(metric), ptr(G), int(deg), float(alpha),
-             int(max_in), ptr(out), ptr(ws), stream_of(Xg.device))
+        call("swann_build_reverse", ptr(Xg), _DT[Xg.dtype], n, d, _m(metric), ptr(G), int(deg),
+             float(alpha), int(max_in), ptr(out), ptr(ws), stream_of(Xg.device))
     return out
 
 
@@ -105,7 +112,7 @@ def build_graph(X, metric: str = "ip", degree: int = 96, candidates: int = 128,
     """Return an (n, degree) int32 neighbour table on the GPU (swann/build.py:153-171)."""
     if X.device.type != "cuda":
         X = X.cuda()
-    Xg = X.float().contiguous()
+    Xg = _rows(X)
     cand, cdist = knn_candidates(Xg, candidates, metric=metric)
     G = robust_prune(Xg, cand, cdist, degree, alpha=alpha, metric=metric)
     G = add_reverse(Xg, G, degree, alpha=alpha, metric=metric)

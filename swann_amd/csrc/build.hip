@@ -20,7 +20,15 @@
 #include "common.h"
 
 namespace swann {
+
+int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype);
+int sweep_mfma_cap(int C);
+int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
+                   float* bkey, int32_t* bid, int32_t* bcnt, char* extra, hipStream_t st);
+
 namespace {
+
+template <typename XT> __device__ __forceinline__ float ld(const XT* p) { return (float)*p; }
 
 constexpr float kSelf = 3.4e38f;          // build.py:39
 constexpr int kRT = 64, kCT = 64, kKT = 16;
@@ -47,14 +55,15 @@ __device__ __forceinline__ float pair_formula(float dot, float na, float nb, int
     return v < 0.f ? 0.f : v;
 }
 
-__global__ __launch_bounds__(256) void norms_kernel(const float* __restrict__ A, int64_t n,
+template <typename XT>
+__global__ __launch_bounds__(256) void norms_kernel(const XT* __restrict__ A, int64_t n,
                                                     int dim, float* __restrict__ out) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= n) return;
-    const float* a = A + r * dim;
+    const XT* a = A + r * dim;
     float s = 0.f;
-    for (int t = lane; t < dim; t += 64) s = __builtin_fmaf(a[t], a[t], s);
+    for (int t = lane; t < dim; t += 64) { const float v = ld(a + t); s = __builtin_fmaf(v, v, s); }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if (lane == 0) out[r] = s;
@@ -63,7 +72,7 @@ __global__ __launch_bounds__(256) void norms_kernel(const float* __restrict__ A,
 // ---------------------------------------------------------------------------
 // sweep
 struct SweepArgs {
-    const float* X; const float* xn; int64_t n; int dim; int metric; int C; int cap;
+    const void* X; const float* xn; int64_t n; int dim; int metric; int C; int cap;
     float* bkey; int32_t* bid; int32_t* bcnt;
 };
 
@@ -122,7 +131,9 @@ __device__ void compact_row(float* key, int32_t* id, int cnt, int C, float* thr_
     if (lane == 0) { *thr_out = funkey(T); *cnt_out = w; }
 }
 
+template <typename XT>
 __global__ __launch_bounds__(256) void sweep_kernel(SweepArgs a) {
+    const XT* X = reinterpret_cast<const XT*>(a.X);
     __shared__ float As[kKT][kRT + 4];
     __shared__ float Bs[kKT][kCT + 4];
     __shared__ float thr[kRT];
@@ -149,8 +160,8 @@ __global__ __launch_bounds__(256) void sweep_kernel(SweepArgs a) {
             for (int e = 0; e < 4; ++e) {
                 const int k = k0 + lk + e;
                 const int64_t ar = r0 + lr, bc = c0 + lr;
-                As[lk + e][lr] = (ar < a.n && k < dim) ? a.X[ar * dim + k] : 0.f;
-                Bs[lk + e][lr] = (bc < a.n && k < dim) ? a.X[bc * dim + k] : 0.f;
+                As[lk + e][lr] = (ar < a.n && k < dim) ? ld(X + ar * dim + k) : 0.f;
+                Bs[lk + e][lr] = (bc < a.n && k < dim) ? ld(X + bc * dim + k) : 0.f;
             }
             __syncthreads();
 #pragma unroll
@@ -251,7 +262,8 @@ constexpr int kPKC = 16;
 
 __device__ __forceinline__ int tri(int w, int i) { return i * (i - 1) / 2 + w; }   // w < i
 
-__global__ __launch_bounds__(256) void prune_kernel(const float* __restrict__ X, int64_t n,
+template <typename XT>
+__global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
                                                     const int32_t* __restrict__ cand,
                                                     const float* __restrict__ cdist, int C,
@@ -278,7 +290,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const float* __restrict__ X,
             const int i = e / kPKC, kk = e % kPKC;
             const int c = cid[i];
             const int k = k0 + kk;
-            Vs[kk][i] = (c >= 0 && c < n && k < dim) ? X[(int64_t)c * dim + k] : 0.f;
+            Vs[kk][i] = (c >= 0 && c < n && k < dim) ? ld(X + (int64_t)c * dim + k) : 0.f;
         }
         __syncthreads();
         if (active) {
@@ -405,7 +417,8 @@ constexpr int kRevBuf = 2048;
 
 // Per node: first max_in in-sources (ascending), union with G_u, minus self,
 // dedup, exact distances, ascending (d, id), the first keepn.
-__global__ __launch_bounds__(256) void rev_assemble(const float* __restrict__ X, int64_t n,
+template <typename XT>
+__global__ __launch_bounds__(256) void rev_assemble(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
                                                     const int32_t* __restrict__ G, int deg,
                                                     int max_in,
@@ -455,7 +468,7 @@ __global__ __launch_bounds__(256) void rev_assemble(const float* __restrict__ X,
     __syncthreads();
     for (int t = 0, i = tid; i < W; i += 256, ++t)
         if (mark[t]) row[i] = kBig;
-    for (int t = tid; t < dim && t < 4096; t += 256) xu[t] = X[u * dim + t];
+    for (int t = tid; t < dim && t < 4096; t += 256) xu[t] = ld(X + u * dim + t);
     __syncthreads();
     // exact distances, 16 lanes per candidate
     const int team = tid >> 4, tl = tid & 15;
@@ -463,11 +476,12 @@ __global__ __launch_bounds__(256) void rev_assemble(const float* __restrict__ X,
         const int v = row[i];
         float s = 0.f;
         if (v < kBig) {
-            const float* xv = X + (int64_t)v * dim;
+            const XT* xv = X + (int64_t)v * dim;
             for (int t = tl; t < dim; t += 16) {
-                const float xt = dim <= 4096 ? xu[t] : X[u * dim + t];
-                if (metric == SWANN_METRIC_IP) s = __builtin_fmaf(xv[t], xt, s);
-                else { const float df = xv[t] - xt; s = __builtin_fmaf(df, df, s); }
+                const float xt = dim <= 4096 ? xu[t] : ld(X + u * dim + t);
+                const float xvt = ld(xv + t);
+                if (metric == SWANN_METRIC_IP) s = __builtin_fmaf(xvt, xt, s);
+                else { const float df = xvt - xt; s = __builtin_fmaf(df, df, s); }
             }
         }
 #pragma unroll
@@ -506,42 +520,61 @@ int sweep_cap(int C) {
     return cap > 1024 ? 1024 : cap;
 }
 
+bool use_mfma(int dim) { return dim % 8 == 0; }
+
 }  // namespace
 }  // namespace swann
 
 using namespace swann;
 
+#define SWANN_BY_DTYPE(DT, CALL_F32, CALL_F16) \
+    do { if ((DT) == SWANN_DTYPE_F16) { CALL_F16; } else { CALL_F32; } } while (0)
+
 extern "C" {
 
-int64_t swann_sweep_workspace_size(int64_t n, int dim, int C) {
-    (void)dim;
-    const int cap = sweep_cap(C);
-    return align256(n * 4) + align256(n * (int64_t)cap * 4) * 2 + align256(n * 4);
+int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C) {
+    const int cap = use_mfma(dim) ? sweep_mfma_cap(C) : sweep_cap(C);
+    int64_t b = align256(n * 4) + align256(n * (int64_t)cap * 4) * 2 + align256(n * 4);
+    if (use_mfma(dim)) b += sweep_mfma_extra_bytes(n, dim, x_dtype);
+    return b;
 }
 
-int swann_build_sweep(const float* X, int64_t n, int dim, int metric, int C, int32_t* cand,
-                      float* cdist, void* workspace, void* stream) {
+int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric, int C,
+                      int32_t* cand, float* cdist, void* workspace, void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
     SWANN_REQUIRE(n >= 2 && dim >= 1, "sweep: need n >= 2 rows");
     SWANN_REQUIRE(C >= 1 && C <= kMaxC && C <= n, "sweep: candidates must be in 1..min(n, %d)",
                   kMaxC);
     SWANN_REQUIRE(n <= INT32_MAX / 2, "sweep: n too large");
     SWANN_REQUIRE(X && cand && cdist && workspace, "sweep: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
-    const int cap = sweep_cap(C);
+    const bool mf = use_mfma(dim);
+    const int cap = mf ? sweep_mfma_cap(C) : sweep_cap(C);
     char* ws = (char*)workspace;
     float* xn = (float*)ws; ws += align256(n * 4);
     float* bkey = (float*)ws; ws += align256(n * (int64_t)cap * 4);
     int32_t* bid = (int32_t*)ws; ws += align256(n * (int64_t)cap * 4);
-    int32_t* bcnt = (int32_t*)ws;
-    if (metric == SWANN_METRIC_L2)
-        hipLaunchKernelGGL(norms_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, X, n,
-                           dim, xn);
-    SweepArgs a{X, xn, n, dim, metric, C, cap, bkey, bid, bcnt};
-    hipLaunchKernelGGL(sweep_kernel, dim3((unsigned)((n + kRT - 1) / kRT)), dim3(256), 0, st, a);
-    int rc = launch_status("sweep");
+    int32_t* bcnt = (int32_t*)ws; ws += align256(n * 4);
+    int rc;
+    if (mf) {
+        rc = sweep_mfma_run(X, x_dtype, n, dim, metric, C, cap, bkey, bid, bcnt, ws, st);
+    } else {
+        const unsigned nb = (unsigned)((n + 3) / 4);
+        if (metric == SWANN_METRIC_L2)
+            SWANN_BY_DTYPE(x_dtype,
+                hipLaunchKernelGGL(norms_kernel<float>, dim3(nb), dim3(256), 0, st, (const float*)X, n, dim, xn),
+                hipLaunchKernelGGL(norms_kernel<_Float16>, dim3(nb), dim3(256), 0, st, (const _Float16*)X, n, dim, xn));
+        SweepArgs a{X, xn, n, dim, metric, C, cap, bkey, bid, bcnt};
+        const unsigned grid = (unsigned)((n + kRT - 1) / kRT);
+        SWANN_BY_DTYPE(x_dtype,
+            hipLaunchKernelGGL(sweep_kernel<float>, dim3(grid), dim3(256), 0, st, a),
+            hipLaunchKernelGGL(sweep_kernel<_Float16>, dim3(grid), dim3(256), 0, st, a));
+        rc = launch_status("sweep");
+    }
     if (rc) return rc;
     int np = 2;
     while (np < cap) np <<= 1;
@@ -550,19 +583,25 @@ int swann_build_sweep(const float* X, int64_t n, int dim, int metric, int C, int
     return launch_status("sweep final");
 }
 
-int swann_build_prune(const float* X, int64_t n, int dim, int metric, const int32_t* cand,
-                      const float* cdist, int C, int deg, float alpha, int32_t* out,
-                      void* stream) {
+int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                      const int32_t* cand, const float* cdist, int C, int deg, float alpha,
+                      int32_t* out, void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
     SWANN_REQUIRE(C >= 1 && C <= kPruneMaxC, "prune: candidates per node must be in 1..%d",
                   kPruneMaxC);
     SWANN_REQUIRE(deg >= 1 && deg <= C, "prune: degree must be in 1..C");
     SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
     SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
-    hipLaunchKernelGGL(prune_kernel, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream, X, n,
-                       dim, metric, cand, cdist, C, deg, alpha, out);
+    hipStream_t st = (hipStream_t)stream;
+    SWANN_BY_DTYPE(x_dtype,
+        hipLaunchKernelGGL(prune_kernel<float>, dim3((unsigned)n), dim3(256), 0, st,
+                           (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha, out),
+        hipLaunchKernelGGL(prune_kernel<_Float16>, dim3((unsigned)n), dim3(256), 0, st,
+                           (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha, out));
     return launch_status("prune");
 }
 
@@ -572,11 +611,14 @@ int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in) {
            align256(n * (int64_t)keepn * 4) * 2;
 }
 
-int swann_build_reverse(const float* X, int64_t n, int dim, int metric, const int32_t* G, int deg,
-                        float alpha, int max_in, int32_t* out, void* workspace, void* stream) {
+int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                        const int32_t* G, int deg, float alpha, int max_in, int32_t* out,
+                        void* workspace, void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
     SWANN_REQUIRE(deg >= 1 && max_in >= 0 && deg + max_in <= 512,
                   "reverse: need deg >= 1, max_in >= 0, deg + max_in <= 512");
     SWANN_REQUIRE(n >= 1 && n * (int64_t)deg < INT32_MAX, "reverse: n * deg must fit in int32");
@@ -601,11 +643,17 @@ int swann_build_reverse(const float* X, int64_t n, int dim, int metric, const in
     hipLaunchKernelGGL(rev_scatter, dim3(eb), dim3(256), 0, st, G, n, deg, start, fill, src);
     int rc = launch_status("reverse scatter");
     if (rc) return rc;
-    hipLaunchKernelGGL(rev_assemble, dim3((unsigned)n), dim3(256), 0, st, X, n, dim, metric, G,
-                       deg, max_in, cnt, start, src, keepn, cand2, cd2);
+    SWANN_BY_DTYPE(x_dtype,
+        hipLaunchKernelGGL(rev_assemble<float>, dim3((unsigned)n), dim3(256), 0, st,
+                           (const float*)X, n, dim, metric, G, deg, max_in, cnt, start, src,
+                           keepn, cand2, cd2),
+        hipLaunchKernelGGL(rev_assemble<_Float16>, dim3((unsigned)n), dim3(256), 0, st,
+                           (const _Float16*)X, n, dim, metric, G, deg, max_in, cnt, start, src,
+                           keepn, cand2, cd2));
     rc = launch_status("reverse assemble");
     if (rc) return rc;
-    return swann_build_prune(X, n, dim, metric, cand2, cd2, keepn, deg, alpha, out, stream);
+    return swann_build_prune(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha, out,
+                             stream);
 }
 
 }  // extern "C"

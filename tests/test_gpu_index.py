@@ -172,3 +172,29 @@ def test_c1_built_graph_recall_matches_reference_graph():
         rs.append(recall(ids.cpu().numpy(), truth, 10))
     note("C1 graph recall gpu-built / reference-built", rs)
     assert rs[0] >= rs[1] - 0.005
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_mfma_sweep_matches_oracle(metric, dtype):
+    """The MFMA sweep (dim % 8 == 0): fp32 rows through the three-term fp16
+    split, fp16 rows as exact products; ragged n exercises the tile edges."""
+    n, d = 3001, 64
+    X = gaussian(n, d, 401 + metric, metric == 0)
+    if metric == 1:
+        X = X * 3.0 + 1.5                       # unnormalised, offset: exercises the row scales
+    if dtype == "f16":
+        X = X.astype(np.float16)
+    Xg = torch.from_numpy(X).cuda()
+    m = "ip" if metric == 0 else "l2"
+    note("mfma sweep", dtype, m)
+    cand, cdist = B.knn_candidates(Xg, 40, metric=m)
+    oc, od = O.knn_candidates(X.astype(np.float32), 40, metric, nthreads=8)
+    same = (cand.cpu().numpy() == oc).mean()
+    note("mfma sweep agreement", dtype, m, same)
+    assert same > 0.995
+    scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
+    # self is never a candidate, rows are ascending
+    assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
+    assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
