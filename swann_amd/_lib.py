@@ -6,10 +6,14 @@ calls raise.  Build it with `python -m swann_amd._build`.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libswann_amd.so"
+# The in-tree build; SWANN_AMD_LIB names another build of the same ABI (used to
+# compare kernel variants side by side).
+LIB_PATH = Path(os.environ.get("SWANN_AMD_LIB") or
+                Path(__file__).resolve().parent / "_lib" / "libswann_amd.so")
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -47,21 +51,26 @@ class SwannError(RuntimeError):
     """A call into libswann_amd failed; the message is the library's own."""
 
 
+def load(path):
+    """Open a build of the library at `path` and declare its prototypes."""
+    path = Path(path)
+    if not path.exists():
+        raise SwannError(f"{path} is not built; run `python -m swann_amd._build` "
+                         "(there is no CPU fallback)")
+    L = ctypes.CDLL(str(path))
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
 def lib():
     global _lib
     if _lib is None:
         with _lock:
             if _lib is None:
-                if not LIB_PATH.exists():
-                    raise SwannError(
-                        f"{LIB_PATH} is not built; run `python -m swann_amd._build` "
-                        "(there is no CPU fallback)")
-                L = ctypes.CDLL(str(LIB_PATH))
-                for name, (res, args) in PROTOTYPES.items():
-                    fn = getattr(L, name)
-                    fn.restype = res
-                    fn.argtypes = args
-                _lib = L
+                _lib = load(LIB_PATH)
     return _lib
 
 

@@ -35,7 +35,19 @@ constexpr int kMaxD = SWANN_MAXD;
 constexpr int kMaxV = SWANN_MAXV;
 constexpr int kNctr = SWANN_NCTR;
 constexpr int kCprobe = 32;            // bounded probe into the shared table
-constexpr int kMaxChunks = 16;         // 16-byte loads a lane keeps in flight
+#ifndef SWANN_MAX_CHUNKS
+#define SWANN_MAX_CHUNKS 16
+#endif
+constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in flight
+// Scope of the per-query table and bound operations.  A query's branches are
+// placed on one XCD (xcd_remap), whose L2 is the coherence point for all of
+// them; workgroup-scope accesses are served there, agent scope goes past it.
+#ifndef SWANN_TABLE_SCOPE
+#define SWANN_TABLE_SCOPE __HIP_MEMORY_SCOPE_AGENT
+#endif
+#ifndef SWANN_CAS_FIRST
+#define SWANN_CAS_FIRST 0
+#endif
 constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
 constexpr size_t kMaxLds = 64 * 1024;
 
@@ -148,18 +160,30 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int key, int* claime
     const unsigned mask = (unsigned)(Hc - 1);
     unsigned pos = (2654435761u * (unsigned)key) & mask;
     for (int probe = 0; probe < kCprobe; ++probe) {
-        int cur = __hip_atomic_load(&cid[pos], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#if SWANN_CAS_FIRST
+        // The compare-and-swap returns the slot's value: one round trip
+        // decides found / claimed / occupied.
+        int expected = 0;
+        if (__hip_atomic_compare_exchange_strong(&cid[pos], &expected, key + 1, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, SWANN_TABLE_SCOPE)) {
+            *claimed = 1;
+            return (int)pos;
+        }
+        if (expected == key + 1) return (int)pos;
+#else
+        int cur = __hip_atomic_load(&cid[pos], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
         if (cur == key + 1) return (int)pos;
         if (cur == 0) {
             int expected = 0;
             if (__hip_atomic_compare_exchange_strong(&cid[pos], &expected, key + 1,
                                                      __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT)) {
+                                                     SWANN_TABLE_SCOPE)) {
                 *claimed = 1;
                 return (int)pos;
             }
             if (expected == key + 1) return (int)pos;
         }
+#endif
         pos = (pos + 1) & mask;
     }
     return -1;
@@ -167,13 +191,13 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int key, int* claime
 
 __device__ __forceinline__ float load_agent_f(const float* p) {
     const int b = __hip_atomic_load(reinterpret_cast<const int*>(p), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+                                    SWANN_TABLE_SCOPE);
     return __int_as_float(b);
 }
 
 __device__ __forceinline__ void store_agent_f(float* p, float v) {
     __hip_atomic_store(reinterpret_cast<int*>(p), __float_as_int(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+                       SWANN_TABLE_SCOPE);
 }
 
 __device__ __forceinline__ int pow2_ge(int x, int lo, int cap) {
@@ -562,7 +586,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (a.bound && kr > 0 && qa_id[kr - 1] >= 0)
                 __hip_atomic_fetch_min(reinterpret_cast<int*>(a.bound + q),
                                        __float_as_int(qa_d[kr - 1]), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                                       SWANN_TABLE_SCOPE);
             if (a.crowd_frac > 0.f) {
                 const float cf = (s_nbr > 0) ? ((float)s_cov / (float)s_nbr) : 0.f;
                 if (cf >= a.crowd_frac) {

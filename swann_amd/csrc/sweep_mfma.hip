@@ -41,8 +41,9 @@ __device__ __forceinline__ float funkey(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-__device__ __forceinline__ float dist_formula(float dot, float na, float nb, int metric) {
-    if (metric == SWANN_METRIC_IP) return 1.0f - dot;
+template <int METRIC>
+__device__ __forceinline__ float dist_formula(float dot, float na, float nb) {
+    if (METRIC == SWANN_METRIC_IP) return 1.0f - dot;
     const float v = (nb - 2.0f * dot) + na;
     return v < 0.f ? 0.f : v;
 }
@@ -158,14 +159,63 @@ __device__ void compact_row_w(float* key, int32_t* id, int cnt, int C, float* th
     if (lane == 0) { *thr_out = funkey(T); *cnt_out = w; }
 }
 
-template <int NTERM>
+
+// Epilogue for one 32 x 32 accumulator block: lane holds column c and the 16
+// rows rbase + (e/4)*8 + (e%4).  Thresholds and row norms are read as four
+// 16-byte LDS vectors, all 16 distances are tested into a mask, and only a
+// wave with a survivor takes the append path.  Rows past n carry a -inf
+// threshold, so they never pass.
+template <int METRIC>
+__device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64_t r0, int64_t c,
+                                               bool cok, bool diag, float cn, float sc,
+                                               const float* rs, const float* thr,
+                                               const float* rnorm, int* cnt,
+                                               const MfmaSweepArgs& a, int nterm_scale,
+                                               const f32x16* vx) {
+    float4 th[4], rn[4], rsc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        th[g] = *reinterpret_cast<const float4*>(thr + rbase + g * 8);
+        if (METRIC == SWANN_METRIC_L2) rn[g] = *reinterpret_cast<const float4*>(rnorm + rbase + g * 8);
+        if (nterm_scale) rsc[g] = *reinterpret_cast<const float4*>(rs + rbase + g * 8);
+    }
+    unsigned mask = 0;
+    float dv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int g = e >> 2, q = e & 3;
+        float dot;
+        if (nterm_scale)
+            dot = rsc[g][q] * sc * (v[e] + (*vx)[e] * (1.0f / 2048.0f));
+        else
+            dot = v[e];
+        float d = dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? rn[g][q] : 0.f, cn);
+        if (diag && c == r0 + rbase + g * 8 + q) d = kSelf;
+        dv[e] = d;
+        mask |= (d < th[g][q]) ? (1u << e) : 0u;
+    }
+    if (!cok) mask = 0;
+    if (__ballot(mask != 0) == 0ull) return;
+    while (mask) {
+        const int e = __builtin_ctz(mask);
+        mask &= mask - 1;
+        const int rl = rbase + (e >> 2) * 8 + (e & 3);
+        const int p = atomicAdd(&cnt[rl], 1);
+        const int64_t o = (r0 + rl) * (int64_t)a.cap + p;
+        a.bkey[o] = dv[e];
+        a.bid[o] = (int32_t)c;
+    }
+}
+
+template <int NTERM, int METRIC>
 __global__ __launch_bounds__(256) void sweep_mfma_kernel(MfmaSweepArgs a) {
     constexpr int NT = (NTERM == 1) ? 1 : 2;          // operand planes: hi (and lo)
     __shared__ __align__(16) _Float16 sA[NT][kBM * kLdsRow];
     __shared__ __align__(16) _Float16 sB[NT][kBN * kLdsRow];
-    __shared__ float thr[kBM];
+    __shared__ __align__(16) float thr[kBM];
     __shared__ int cnt[kBM];
-    __shared__ float rnorm[kBM], rscale[kBM];
+    __shared__ __align__(16) float rnorm[kBM];
+    __shared__ __align__(16) float rscale[kBM];
     __shared__ int need;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -178,7 +228,7 @@ __global__ __launch_bounds__(256) void sweep_mfma_kernel(MfmaSweepArgs a) {
 
     if (tid < kBM) {
         const int64_t r = r0 + tid;
-        thr[tid] = INFINITY;
+        thr[tid] = r < n ? INFINITY : -INFINITY;
         cnt[tid] = 0;
         rnorm[tid] = r < n ? a.xn[r] : 0.f;
         rscale[tid] = r < n ? a.scale[r] : 1.f;
@@ -255,32 +305,20 @@ __global__ __launch_bounds__(256) void sweep_mfma_kernel(MfmaSweepArgs a) {
             __syncthreads();
         }
         // ---- epilogue: distances, threshold test, append ----
+        const bool diag = (cb == r0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int cl = wn * 64 + j * 32 + (lane & 31);
-            const int64_t c = cb + cl;
+            const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
             const bool cok = c < n;
             const float cn = cok ? a.xn[c] : 0.f;
             const float cs = cok ? a.scale[c] : 1.f;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int rl = wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-                    const int64_t r = r0 + rl;
-                    if (!cok || r >= n) continue;
-                    float dot;
-                    if constexpr (NTERM == 3)
-                        dot = rscale[rl] * cs * (acc[i][j][e] + accx[i][j][e] * (1.0f / 2048.0f));
-                    else
-                        dot = acc[i][j][e];
-                    const float d = (c == r) ? kSelf : dist_formula(dot, rnorm[rl], cn, a.metric);
-                    if (d < thr[rl]) {
-                        const int p = atomicAdd(&cnt[rl], 1);
-                        a.bkey[r * a.cap + p] = d;
-                        a.bid[r * a.cap + p] = (int32_t)c;
-                    }
-                }
+                int rbase = wm * 64 + i * 32 + (lane >> 5) * 4;
+                asm volatile("" : "+v"(rbase));
+                epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn, cs, rscale, thr,
+                                       rnorm, cnt, a, NTERM == 3, &accx[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         __syncthreads();
@@ -301,6 +339,173 @@ __global__ __launch_bounds__(256) void sweep_mfma_kernel(MfmaSweepArgs a) {
     if (tid < kBM && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
 }
 
+// ---------------------------------------------------------------------------
+// fp16 operands (NTERM = 1): workgroup tile 256 x 256 with eight waves of
+// 128 x 64 (4 x 2 blocks of 32 x 32; 128 accumulators each), so two waves share
+// a SIMD and one's epilogue or wait overlaps the other's MFMAs.  K tile 32.  The
+// workgroup's work is one stream of (column tile, K tile) steps: global loads
+// run two steps ahead in two register stages, LDS is double-buffered with one
+// barrier per step, and a column tile's epilogue overlaps the next tile's loads.
+constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;
+
+struct Stage { f16x8 a[2], b[2]; };
+
+template <int METRIC>
+__global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) {
+    __shared__ __align__(16) _Float16 sA[2][kBM2 * kLdsRow];
+    __shared__ __align__(16) _Float16 sB[2][kBN2 * kLdsRow];
+    __shared__ __align__(16) float thr[kBM2];
+    __shared__ int cnt[kBM2];
+    __shared__ __align__(16) float rnorm[kBM2];
+    __shared__ int need;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;           // rows wm*128.., cols wn*64..
+    const int64_t n = a.n;
+    const int dim = a.dim;
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    const int64_t r0 = xcd_remap(blockIdx.x, ntile) * kBM2;
+
+    if (tid < kBM2) {
+        thr[tid] = r0 + tid < n ? INFINITY : -INFINITY;
+        cnt[tid] = 0;
+        rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
+    }
+    if (tid == 0) need = 0;
+
+    // loader: 256 rows x 4 chunks of 16 B per operand = 2 chunks per thread each
+    int lrow[2], lpart[2];
+    int64_t aoff[2];
+    bool av[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const int c = tid + kT2 * m;
+        lrow[m] = c >> 2;
+        lpart[m] = (c & 3) * 8;
+        av[m] = r0 + lrow[m] < n;
+        aoff[m] = (av[m] ? r0 + lrow[m] : n - 1) * (int64_t)dim + lpart[m];
+    }
+    const int nk = (dim + kBK - 1) / kBK;
+    const int64_t nct = (n + kBN2 - 1) / kBN2;
+    const int64_t nsteps = nct * nk;
+
+    auto gload = [&](Stage& S, int64_t t) {
+        const f16x8 z = {};
+        if (t >= nsteps) return;
+        const int kt = (int)(t % nk);
+        const int64_t cb = (t / nk) * kBN2;
+        const int k0 = kt * kBK;
+        const bool kfull = k0 + kBK <= dim;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const int64_t rb = cb + lrow[m];
+            const bool bv = rb < n;
+            const bool kin = kfull || (k0 + lpart[m] < dim);
+            const int64_t boff = (bv ? rb : n - 1) * (int64_t)dim + lpart[m];
+            const int kk = kin ? k0 : 0;                // never read past a row
+            const f16x8 va = *reinterpret_cast<const f16x8*>(a.hi + aoff[m] + kk);
+            const f16x8 vb = *reinterpret_cast<const f16x8*>(a.hi + boff + kk);
+            S.a[m] = (av[m] && kin) ? va : z;
+            S.b[m] = (bv && kin) ? vb : z;
+        }
+    };
+    auto lstore = [&](const Stage& S, int buf) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            *reinterpret_cast<f16x8*>(&sA[buf][lrow[m] * kLdsRow + lpart[m]]) = S.a[m];
+            *reinterpret_cast<f16x8*>(&sB[buf][lrow[m] * kLdsRow + lpart[m]]) = S.b[m];
+        }
+    };
+
+    f32x16 acc[4][2];
+    Stage S0, S1;
+    gload(S0, 0);
+    gload(S1, 1);
+    lstore(S0, 0);
+    gload(S0, 2);
+    __syncthreads();
+
+    auto step = [&](int64_t t, Stage& Snext) {
+        const int kt = (int)(t % nk);
+        const int buf = (int)(t & 1);
+        if (kt == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
+        }
+        // column norms of this tile, loaded before the next steps' prefetch so
+        // the epilogue never waits on it
+        float cn[2] = {0.f, 0.f};
+        if (METRIC == SWANN_METRIC_L2 && kt == nk - 1) {
+            const int64_t cb = (t / nk) * kBN2;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
+                cn[j] = c < n ? a.xn[c] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < kBK; ks += 16) {
+            const int kof = ks + (lane >> 5) * 8;
+            f16x8 fa[4], fb[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[i] = *reinterpret_cast<const f16x8*>(
+                    &sA[buf][(wm * 128 + i * 32 + (lane & 31)) * kLdsRow + kof]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[j] = *reinterpret_cast<const f16x8*>(
+                    &sB[buf][(wn * 64 + j * 32 + (lane & 31)) * kLdsRow + kof]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j],
+                                                                      0, 0, 0);
+        }
+        if (t + 1 < nsteps) lstore(Snext, buf ^ 1);
+        gload(Snext, t + 3);
+        if (kt == nk - 1) {
+            // ---- epilogue of this column tile: distance, threshold, append ----
+            const int64_t cb = (t / nk) * kBN2;
+            const bool diag = (cb == r0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
+                const bool cok = c < n;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
+                    asm volatile("" : "+v"(rbase));
+                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], 1.f, nullptr,
+                                           thr, rnorm, cnt, a, 0, nullptr);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __syncthreads();
+            if (tid < kBM2 && cnt[tid] > a.cap - kBN2) atomicOr(&need, 1);
+            __syncthreads();
+            if (need) {
+                for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+                    const int64_t r = r0 + rl;
+                    if (r < n && cnt[rl] > a.cap - kBN2)
+                        compact_row_w(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C,
+                                      &thr[rl], &cnt[rl]);
+                }
+                __syncthreads();
+                if (tid == 0) need = 0;
+            }
+        }
+        __syncthreads();
+    };
+    for (int64_t t = 0; t < nsteps; t += 2) {
+        step(t, S1);
+        if (t + 1 < nsteps) step(t + 1, S0);
+    }
+    if (tid < kBM2 && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 }  // namespace
@@ -312,7 +517,8 @@ int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
 }
 
 int sweep_mfma_cap(int C) {
-    int cap = C + 640;
+    // room for one 256-column tile of appends above the C kept
+    int cap = C + 768;
     return cap > 1024 ? 1024 : cap;
 }
 
@@ -336,11 +542,16 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         lo = l;
     }
     MfmaSweepArgs a{hi, lo, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt};
-    const unsigned grid = (unsigned)((n + kBM - 1) / kBM);
-    if (x_dtype == SWANN_DTYPE_F16)
-        hipLaunchKernelGGL(sweep_mfma_kernel<1>, dim3(grid), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL(sweep_mfma_kernel<3>, dim3(grid), dim3(256), 0, st, a);
+    const bool ip = metric == SWANN_METRIC_IP;
+    if (x_dtype == SWANN_DTYPE_F16) {
+        const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
+        if (ip) hipLaunchKernelGGL(sweep_mfma256_kernel<SWANN_METRIC_IP>, dim3(grid), dim3(kT2), 0, st, a);
+        else hipLaunchKernelGGL(sweep_mfma256_kernel<SWANN_METRIC_L2>, dim3(grid), dim3(kT2), 0, st, a);
+    } else {
+        const unsigned grid = (unsigned)((n + kBM - 1) / kBM);
+        if (ip) hipLaunchKernelGGL((sweep_mfma_kernel<3, SWANN_METRIC_IP>), dim3(grid), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((sweep_mfma_kernel<3, SWANN_METRIC_L2>), dim3(grid), dim3(256), 0, st, a);
+    }
     return launch_status("sweep (mfma)");
 }
 
