@@ -136,8 +136,9 @@ int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, i
  * excluded (3.4e38), ascending, as (cand [n, C] int32, cdist [n, C] fp32) with
  * IP: 1 - <a,b>; L2: max(0, |b|^2 - 2<a,b> + |a|^2).  When dim % 8 == 0 the
  * scores come from fp16 MFMA tiles (fp16 corpus: exact products; fp32 corpus:
- * a three-term hi/lo split, ~22 significant bits); otherwise from fp32 SIMT
- * tiles.  `workspace`: swann_sweep_workspace_size bytes. */
+ * a power-of-two row-scaled fp16 screen keeps C+32 per row, which are then
+ * re-ranked with exact fp32 dot products); otherwise from fp32 SIMT tiles.
+ * `workspace`: swann_sweep_workspace_size bytes. */
 int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C);
 int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric, int C,
                       int32_t* cand, float* cdist, void* workspace, void* stream);

@@ -513,6 +513,75 @@ __global__ __launch_bounds__(256) void rev_assemble(const XT* __restrict__ X, in
     }
 }
 
+// ---------------------------------------------------------------------------
+// Exact re-rank of screened candidates (fp32 corpus): per row, the reference
+// formula on fp32 dot products with each of its Cs screened candidates, sorted
+// by (d, id), the first C kept.  One workgroup per row, 16 lanes per candidate.
+template <int METRIC>
+__global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ X, int64_t n, int dim,
+                                                     const float* __restrict__ xn,
+                                                     const int32_t* __restrict__ scand, int Cs,
+                                                     int C, int32_t* __restrict__ cand,
+                                                     float* __restrict__ cdist) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* xu = reinterpret_cast<float*>(smem);
+    __shared__ float sd[512];
+    __shared__ int si[512];
+    const int64_t u = blockIdx.x;
+    const int tid = threadIdx.x, team = tid >> 4, tl = tid & 15;
+    for (int t = tid; t < dim; t += 256) xu[t] = X[u * dim + t];
+    int np = 2;
+    while (np < Cs) np <<= 1;
+    for (int i = Cs + tid; i < np; i += 256) { sd[i] = INFINITY; si[i] = INT32_MAX; }
+    __syncthreads();
+    const float nu = METRIC == SWANN_METRIC_L2 ? xn[u] : 0.f;
+    const bool v4 = (dim & 3) == 0;
+    for (int i = team; i < Cs; i += 16) {
+        const int c = scand[u * Cs + i];
+        float s = 0.f;
+        if (c >= 0 && c < n) {
+            const float* xc = X + (int64_t)c * dim;
+            if (v4) {
+                for (int t = tl * 4; t < dim; t += 64) {
+                    const float4 a = *reinterpret_cast<const float4*>(xc + t);
+                    const float4 b = *reinterpret_cast<const float4*>(xu + t);
+                    s = __builtin_fmaf(a.x, b.x, s); s = __builtin_fmaf(a.y, b.y, s);
+                    s = __builtin_fmaf(a.z, b.z, s); s = __builtin_fmaf(a.w, b.w, s);
+                }
+            } else {
+                for (int t = tl; t < dim; t += 16) s = __builtin_fmaf(xc[t], xu[t], s);
+            }
+        }
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) s += __shfl_down(s, off, 16);
+        if (tl == 0) {
+            if (c < 0 || c >= n) { sd[i] = INFINITY; si[i] = INT32_MAX; }
+            else if (c == u) { sd[i] = kSelf; si[i] = c; }
+            else { sd[i] = pair_formula(s, nu, METRIC == SWANN_METRIC_L2 ? xn[c] : 0.f, METRIC); si[i] = c; }
+        }
+    }
+    __syncthreads();
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < np; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = ((i & size) == 0);
+                    if (up != lt(sd[i], si[i], sd[j], si[j])) {
+                        const float td = sd[i]; sd[i] = sd[j]; sd[j] = td;
+                        const int ti = si[i]; si[i] = si[j]; si[j] = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (int t = tid; t < C; t += 256) {
+        const bool ok = si[t] != INT32_MAX;
+        cand[u * C + t] = ok ? si[t] : -1;
+        cdist[u * C + t] = ok ? sd[t] : INFINITY;
+    }
+}
+
 inline int64_t align256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 int sweep_cap(int C) {
@@ -521,6 +590,15 @@ int sweep_cap(int C) {
 }
 
 bool use_mfma(int dim) { return dim % 8 == 0; }
+
+// Candidates the fp32 screen keeps per row before the exact re-rank.
+int screen_count(int C, int64_t n, int x_dtype, int dim) {
+    if (x_dtype == SWANN_DTYPE_F16 || !use_mfma(dim)) return C;
+    int64_t cs = C + 32;
+    if (cs > kMaxC) cs = kMaxC;
+    if (cs > n) cs = n;
+    return (int)(cs < C ? C : cs);
+}
 
 }  // namespace
 }  // namespace swann
@@ -533,8 +611,10 @@ using namespace swann;
 extern "C" {
 
 int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C) {
-    const int cap = use_mfma(dim) ? sweep_mfma_cap(C) : sweep_cap(C);
+    const int Cs = screen_count(C, n, x_dtype, dim);
+    const int cap = use_mfma(dim) ? sweep_mfma_cap(Cs) : sweep_cap(C);
     int64_t b = align256(n * 4) + align256(n * (int64_t)cap * 4) * 2 + align256(n * 4);
+    if (Cs != C) b += align256(n * (int64_t)Cs * 4) * 2;
     if (use_mfma(dim)) b += sweep_mfma_extra_bytes(n, dim, x_dtype);
     return b;
 }
@@ -553,15 +633,24 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     SWANN_REQUIRE(X && cand && cdist && workspace, "sweep: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
     const bool mf = use_mfma(dim);
-    const int cap = mf ? sweep_mfma_cap(C) : sweep_cap(C);
+    const int Cs = screen_count(C, n, x_dtype, dim);
+    SWANN_REQUIRE(Cs == C || dim * 4 <= 64 * 1024, "sweep: dimension too large for the re-rank");
+    const int cap = mf ? sweep_mfma_cap(Cs) : sweep_cap(C);
     char* ws = (char*)workspace;
     float* xn = (float*)ws; ws += align256(n * 4);
     float* bkey = (float*)ws; ws += align256(n * (int64_t)cap * 4);
     int32_t* bid = (int32_t*)ws; ws += align256(n * (int64_t)cap * 4);
     int32_t* bcnt = (int32_t*)ws; ws += align256(n * 4);
+    int32_t* scand = nullptr;
+    float* scd = nullptr;
+    if (Cs != C) {
+        scand = (int32_t*)ws; ws += align256(n * (int64_t)Cs * 4);
+        scd = (float*)ws; ws += align256(n * (int64_t)Cs * 4);
+    }
+    char* extra = ws;
     int rc;
     if (mf) {
-        rc = sweep_mfma_run(X, x_dtype, n, dim, metric, C, cap, bkey, bid, bcnt, ws, st);
+        rc = sweep_mfma_run(X, x_dtype, n, dim, metric, Cs, cap, bkey, bid, bcnt, extra, st);
     } else {
         const unsigned nb = (unsigned)((n + 3) / 4);
         if (metric == SWANN_METRIC_L2)
@@ -578,9 +667,26 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     if (rc) return rc;
     int np = 2;
     while (np < cap) np <<= 1;
+    if (Cs == C) {
+        hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
+                           bcnt, n, cap, C, cand, cdist);
+        return launch_status("sweep final");
+    }
     hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
-                       bcnt, n, cap, C, cand, cdist);
-    return launch_status("sweep final");
+                       bcnt, n, cap, Cs, scand, scd);
+    rc = launch_status("sweep final");
+    if (rc) return rc;
+    // exact fp32 re-rank of the screened lists; the norms are the sweep's
+    const float* xnorm = (const float*)extra;
+    if (metric == SWANN_METRIC_IP)
+        hipLaunchKernelGGL(rerank_kernel<SWANN_METRIC_IP>, dim3((unsigned)n), dim3(256),
+                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C, cand,
+                           cdist);
+    else
+        hipLaunchKernelGGL(rerank_kernel<SWANN_METRIC_L2>, dim3((unsigned)n), dim3(256),
+                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C, cand,
+                           cdist);
+    return launch_status("sweep re-rank");
 }
 
 int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,

@@ -6,13 +6,10 @@
 // S = X_rows . X_cols^T:
 //   * an fp16 corpus is used as is: fp16 x fp16 products are exact in fp32 and
 //     accumulate in fp32, so the scores are as good as an fp32 GEMM's;
-//   * an fp32 corpus is split per row into hi = fp16(x / s) and
-//     lo = fp16((x / s - hi) * 2^11) with s a power of two (exact scaling), and
-//     s_a s_b (hi.hi + 2^-11 (hi.lo + lo.hi)) carries ~22 significant bits --
-//     fp32-grade scores from three fp16 MFMA terms.
-// Workgroup: 256 threads = 4 waves in 2 x 2, tile 128 rows x 128 columns, each
-// wave 64 x 64 = 2 x 2 blocks of v_mfma_f32_32x32x16_f16, K step 32, the next
-// K tile prefetched into registers while the current one is consumed.
+//   * an fp32 corpus is screened: rows are scaled by a power of two s and
+//     rounded once to fp16, s_a s_b (h_a . h_b) ranks the candidates to within
+//     ~1e-4 relative, the sweep keeps C + 32 per row, and the caller re-ranks
+//     those in fp32 (one gather of C + 32 rows per row, not a second sweep).
 // Epilogue per tile: score -> distance by the reference formula, test against
 // the row's running threshold (LDS), append survivors to the row's buffer;
 // rows near capacity are compacted to their C best (wave-level exact select).
@@ -28,7 +25,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kBK = 32;
 constexpr int kPad = 8;                       // fp16 elements of padding per LDS row
 constexpr int kLdsRow = kBK + kPad;           // 40 halves = 80 bytes
 constexpr float kSelf = 3.4e38f;
@@ -79,7 +76,7 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ X, i
         const float v = x[t] * inv;
         const _Float16 h = (_Float16)v;
         hi[r * dim + t] = h;
-        lo[r * dim + t] = (_Float16)((v - (float)h) * 2048.0f);
+        if (lo) lo[r * dim + t] = (_Float16)((v - (float)h) * 2048.0f);
     }
     if (lane == 0) { scale[r] = s; norm[r] = s2; }
 }
@@ -102,6 +99,7 @@ struct MfmaSweepArgs {
     const _Float16* hi; const _Float16* lo; const float* scale; const float* xn;
     int64_t n; int dim; int metric; int C; int cap;
     float* bkey; int32_t* bid; int32_t* bcnt;
+    int scaled;                  // rows carry a power-of-two scale (fp32 corpus)
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -185,8 +183,10 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
     for (int e = 0; e < 16; ++e) {
         const int g = e >> 2, q = e & 3;
         float dot;
-        if (nterm_scale)
+        if (nterm_scale == 1)
             dot = rsc[g][q] * sc * (v[e] + (*vx)[e] * (1.0f / 2048.0f));
+        else if (nterm_scale == 2)
+            dot = rsc[g][q] * sc * v[e];
         else
             dot = v[e];
         float d = dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? rn[g][q] : 0.f, cn);
@@ -207,138 +207,6 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
     }
 }
 
-template <int NTERM, int METRIC>
-__global__ __launch_bounds__(256) void sweep_mfma_kernel(MfmaSweepArgs a) {
-    constexpr int NT = (NTERM == 1) ? 1 : 2;          // operand planes: hi (and lo)
-    __shared__ __align__(16) _Float16 sA[NT][kBM * kLdsRow];
-    __shared__ __align__(16) _Float16 sB[NT][kBN * kLdsRow];
-    __shared__ __align__(16) float thr[kBM];
-    __shared__ int cnt[kBM];
-    __shared__ __align__(16) float rnorm[kBM];
-    __shared__ __align__(16) float rscale[kBM];
-    __shared__ int need;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;          // wave's 64 x 64 quadrant
-    const int64_t n = a.n;
-    const int dim = a.dim;
-    // XCD-aware: consecutive row tiles share an XCD (and its L2 copy of the columns)
-    const int64_t ntile = (n + kBM - 1) / kBM;
-    const int64_t r0 = xcd_remap(blockIdx.x, ntile) * kBM;
-
-    if (tid < kBM) {
-        const int64_t r = r0 + tid;
-        thr[tid] = r < n ? INFINITY : -INFINITY;
-        cnt[tid] = 0;
-        rnorm[tid] = r < n ? a.xn[r] : 0.f;
-        rscale[tid] = r < n ? a.scale[r] : 1.f;
-    }
-    if (tid == 0) need = 0;
-    __syncthreads();
-
-    // loader: 128 rows x 64 bytes per plane = 512 chunks of 16 B, 2 per thread
-    const int c0i = tid, c1i = tid + 256;
-    const int lr0 = c0i >> 2, lp0 = (c0i & 3) * 8;
-    const int lr1 = c1i >> 2, lp1 = (c1i & 3) * 8;
-
-    for (int64_t cb = 0; cb < n; cb += kBN) {
-        f32x16 acc[2][2], accx[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                acc[i][j] = (f32x16){};
-                accx[i][j] = (f32x16){};
-            }
-        f16x8 ga[NT][2], gb[NT][2];
-        auto gload = [&](int k0) {
-#pragma unroll
-            for (int p = 0; p < NT; ++p) {
-                const _Float16* M = p == 0 ? a.hi : a.lo;
-                const int64_t ra0 = r0 + lr0, ra1 = r0 + lr1;
-                const int64_t rb0 = cb + lr0, rb1 = cb + lr1;
-                const f16x8 z = {};
-                ga[p][0] = (ra0 < n && k0 + lp0 < dim) ? *reinterpret_cast<const f16x8*>(M + ra0 * dim + k0 + lp0) : z;
-                ga[p][1] = (ra1 < n && k0 + lp1 < dim) ? *reinterpret_cast<const f16x8*>(M + ra1 * dim + k0 + lp1) : z;
-                gb[p][0] = (rb0 < n && k0 + lp0 < dim) ? *reinterpret_cast<const f16x8*>(M + rb0 * dim + k0 + lp0) : z;
-                gb[p][1] = (rb1 < n && k0 + lp1 < dim) ? *reinterpret_cast<const f16x8*>(M + rb1 * dim + k0 + lp1) : z;
-            }
-        };
-        gload(0);
-        for (int k0 = 0; k0 < dim; k0 += kBK) {
-#pragma unroll
-            for (int p = 0; p < NT; ++p) {
-                *reinterpret_cast<f16x8*>(&sA[p][lr0 * kLdsRow + lp0]) = ga[p][0];
-                *reinterpret_cast<f16x8*>(&sA[p][lr1 * kLdsRow + lp1]) = ga[p][1];
-                *reinterpret_cast<f16x8*>(&sB[p][lr0 * kLdsRow + lp0]) = gb[p][0];
-                *reinterpret_cast<f16x8*>(&sB[p][lr1 * kLdsRow + lp1]) = gb[p][1];
-            }
-            __syncthreads();
-            if (k0 + kBK < dim) gload(k0 + kBK);       // next tile in flight during the MFMAs
-#pragma unroll
-            for (int ks = 0; ks < kBK; ks += 16) {
-                f16x8 fa[NT][2], fb[NT][2];
-                const int kof = ks + (lane >> 5) * 8;
-#pragma unroll
-                for (int p = 0; p < NT; ++p)
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const int ar = wm * 64 + i * 32 + (lane & 31);
-                        const int br = wn * 64 + i * 32 + (lane & 31);
-                        fa[p][i] = *reinterpret_cast<const f16x8*>(&sA[p][ar * kLdsRow + kof]);
-                        fb[p][i] = *reinterpret_cast<const f16x8*>(&sB[p][br * kLdsRow + kof]);
-                    }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[0][i], fb[0][j],
-                                                                          acc[i][j], 0, 0, 0);
-                        if constexpr (NTERM == 3) {
-                            accx[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                fa[0][i], fb[1][j], accx[i][j], 0, 0, 0);
-                            accx[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                fa[1][i], fb[0][j], accx[i][j], 0, 0, 0);
-                        }
-                    }
-            }
-            __syncthreads();
-        }
-        // ---- epilogue: distances, threshold test, append ----
-        const bool diag = (cb == r0);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
-            const bool cok = c < n;
-            const float cn = cok ? a.xn[c] : 0.f;
-            const float cs = cok ? a.scale[c] : 1.f;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                int rbase = wm * 64 + i * 32 + (lane >> 5) * 4;
-                asm volatile("" : "+v"(rbase));
-                epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn, cs, rscale, thr,
-                                       rnorm, cnt, a, NTERM == 3, &accx[i][j]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        __syncthreads();
-        if (tid < kBM && cnt[tid] > a.cap - kBN) atomicOr(&need, 1);
-        __syncthreads();
-        if (need) {
-            for (int rl = wave; rl < kBM; rl += 4) {
-                const int64_t r = r0 + rl;
-                if (r < n && cnt[rl] > a.cap - kBN)
-                    compact_row_w(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C, &thr[rl],
-                                  &cnt[rl]);
-            }
-            __syncthreads();
-            if (tid == 0) need = 0;
-            __syncthreads();
-        }
-    }
-    if (tid < kBM && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
-}
-
 // ---------------------------------------------------------------------------
 // fp16 operands (NTERM = 1): workgroup tile 256 x 256 with eight waves of
 // 128 x 64 (4 x 2 blocks of 32 x 32; 128 accumulators each), so two waves share
@@ -350,13 +218,14 @@ constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;
 
 struct Stage { f16x8 a[2], b[2]; };
 
-template <int METRIC>
+template <int METRIC, int SCALED>
 __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) {
     __shared__ __align__(16) _Float16 sA[2][kBM2 * kLdsRow];
     __shared__ __align__(16) _Float16 sB[2][kBN2 * kLdsRow];
     __shared__ __align__(16) float thr[kBM2];
     __shared__ int cnt[kBM2];
     __shared__ __align__(16) float rnorm[kBM2];
+    __shared__ __align__(16) float rscale[kBM2];
     __shared__ int need;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -370,6 +239,7 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
         thr[tid] = r0 + tid < n ? INFINITY : -INFINITY;
         cnt[tid] = 0;
         rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
+        if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
     }
     if (tid == 0) need = 0;
 
@@ -389,11 +259,9 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
     const int64_t nct = (n + kBN2 - 1) / kBN2;
     const int64_t nsteps = nct * nk;
 
-    auto gload = [&](Stage& S, int64_t t) {
+    auto gload = [&](Stage& S, int64_t t, int kt, int64_t cb) {
         const f16x8 z = {};
         if (t >= nsteps) return;
-        const int kt = (int)(t % nk);
-        const int64_t cb = (t / nk) * kBN2;
         const int k0 = kt * kBK;
         const bool kfull = k0 + kBK <= dim;
 #pragma unroll
@@ -417,16 +285,25 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
         }
     };
 
+    // (kt, cb) of the current step and of the step three ahead, kept by
+    // increments: no 64-bit division per step
+    int kt_c = 0, kt_f = 0;
+    int64_t cb_c = 0, cb_f = 0;
+    auto adv = [&](int& kt, int64_t& cb) {
+        if (++kt == nk) { kt = 0; cb += kBN2; }
+    };
     f32x16 acc[4][2];
     Stage S0, S1;
-    gload(S0, 0);
-    gload(S1, 1);
+    gload(S0, 0, kt_f, cb_f); adv(kt_f, cb_f);
+    gload(S1, 1, kt_f, cb_f); adv(kt_f, cb_f);
     lstore(S0, 0);
-    gload(S0, 2);
+    gload(S0, 2, kt_f, cb_f); adv(kt_f, cb_f);
     __syncthreads();
 
     auto step = [&](int64_t t, Stage& Snext) {
-        const int kt = (int)(t % nk);
+        const int kt = kt_c;
+        const int64_t cbt = cb_c;
+        adv(kt_c, cb_c);
         const int buf = (int)(t & 1);
         if (kt == 0) {
 #pragma unroll
@@ -436,13 +313,13 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
         }
         // column norms of this tile, loaded before the next steps' prefetch so
         // the epilogue never waits on it
-        float cn[2] = {0.f, 0.f};
-        if (METRIC == SWANN_METRIC_L2 && kt == nk - 1) {
-            const int64_t cb = (t / nk) * kBN2;
+        float cn[2] = {0.f, 0.f}, cs[2] = {1.f, 1.f};
+        if (kt == nk - 1) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
-                cn[j] = c < n ? a.xn[c] : 0.f;
+                const int64_t c = cbt + wn * 64 + j * 32 + (lane & 31);
+                if (METRIC == SWANN_METRIC_L2) cn[j] = c < n ? a.xn[c] : 0.f;
+                if (SCALED) cs[j] = c < n ? a.scale[c] : 1.f;
             }
         }
 #pragma unroll
@@ -465,10 +342,11 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
                                                                       0, 0, 0);
         }
         if (t + 1 < nsteps) lstore(Snext, buf ^ 1);
-        gload(Snext, t + 3);
+        gload(Snext, t + 3, kt_f, cb_f);
+        adv(kt_f, cb_f);
         if (kt == nk - 1) {
             // ---- epilogue of this column tile: distance, threshold, append ----
-            const int64_t cb = (t / nk) * kBN2;
+            const int64_t cb = cbt;
             const bool diag = (cb == r0);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -478,8 +356,8 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
                 for (int i = 0; i < 4; ++i) {
                     int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
                     asm volatile("" : "+v"(rbase));
-                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], 1.f, nullptr,
-                                           thr, rnorm, cnt, a, 0, nullptr);
+                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], cs[j],
+                                           rscale, thr, rnorm, cnt, a, SCALED ? 2 : 0, nullptr);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -510,9 +388,41 @@ inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 }  // namespace
 
-// Workspace layout for the MFMA sweep (bytes), after the row buffers.
+// Runs the MFMA sweep into the row buffers (bkey/bid/bcnt); the caller sorts.
+// fp16 rows: exact products, one term.  fp32 rows: one fp16 term of the
+// power-of-two-scaled rows (a screen; the caller re-ranks the survivors in fp32).
+int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
+                   float* bkey, int32_t* bid, int32_t* bcnt, char* extra, hipStream_t st) {
+    float* xn = (float*)extra; extra += al256(n * 4);
+    float* scale = (float*)extra; extra += al256(n * 4);
+    const _Float16* hi;
+    const int scaled = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
+    if (!scaled) {
+        hi = (const _Float16*)X;
+        hipLaunchKernelGGL(norms_f16, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, hi, n, dim,
+                           xn, scale);
+    } else {
+        _Float16* h = (_Float16*)extra;
+        hipLaunchKernelGGL(split_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
+                           (const float*)X, n, dim, h, (_Float16*)nullptr, scale, xn);
+        hi = h;
+    }
+    MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled};
+    const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
+    const bool ip = metric == SWANN_METRIC_IP;
+    if (scaled) {
+        if (ip) hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
+        else hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
+    } else {
+        if (ip) hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_IP, 0>), dim3(grid), dim3(kT2), 0, st, a);
+        else hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_L2, 0>), dim3(grid), dim3(kT2), 0, st, a);
+    }
+    return launch_status("sweep (mfma)");
+}
+
+// Extra workspace: norms, scales and (fp32 corpus) the fp16 plane.
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
-    const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 2;
+    const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
     return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2);
 }
 
@@ -520,39 +430,6 @@ int sweep_mfma_cap(int C) {
     // room for one 256-column tile of appends above the C kept
     int cap = C + 768;
     return cap > 1024 ? 1024 : cap;
-}
-
-// Runs the MFMA sweep into the row buffers (bkey/bid/bcnt); the caller sorts.
-int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
-                   float* bkey, int32_t* bid, int32_t* bcnt, char* extra, hipStream_t st) {
-    float* xn = (float*)extra; extra += al256(n * 4);
-    float* scale = (float*)extra; extra += al256(n * 4);
-    const _Float16* hi;
-    const _Float16* lo = nullptr;
-    if (x_dtype == SWANN_DTYPE_F16) {
-        hi = (const _Float16*)X;
-        hipLaunchKernelGGL(norms_f16, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, hi, n, dim,
-                           xn, scale);
-    } else {
-        _Float16* h = (_Float16*)extra; extra += al256(n * (int64_t)dim * 2);
-        _Float16* l = (_Float16*)extra;
-        hipLaunchKernelGGL(split_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
-                           (const float*)X, n, dim, h, l, scale, xn);
-        hi = h;
-        lo = l;
-    }
-    MfmaSweepArgs a{hi, lo, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt};
-    const bool ip = metric == SWANN_METRIC_IP;
-    if (x_dtype == SWANN_DTYPE_F16) {
-        const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
-        if (ip) hipLaunchKernelGGL(sweep_mfma256_kernel<SWANN_METRIC_IP>, dim3(grid), dim3(kT2), 0, st, a);
-        else hipLaunchKernelGGL(sweep_mfma256_kernel<SWANN_METRIC_L2>, dim3(grid), dim3(kT2), 0, st, a);
-    } else {
-        const unsigned grid = (unsigned)((n + kBM - 1) / kBM);
-        if (ip) hipLaunchKernelGGL((sweep_mfma_kernel<3, SWANN_METRIC_IP>), dim3(grid), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((sweep_mfma_kernel<3, SWANN_METRIC_L2>), dim3(grid), dim3(256), 0, st, a);
-    }
-    return launch_status("sweep (mfma)");
 }
 
 }  // namespace swann

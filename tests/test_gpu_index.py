@@ -177,8 +177,9 @@ def test_c1_built_graph_recall_matches_reference_graph():
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_matches_oracle(metric, dtype):
-    """The MFMA sweep (dim % 8 == 0): fp32 rows through the three-term fp16
-    split, fp16 rows as exact products; ragged n exercises the tile edges."""
+    """The MFMA sweep (dim % 8 == 0): fp32 rows through a power-of-two scaled
+    fp16 screen of C+32 per row and an exact fp32 re-rank, fp16 rows as exact
+    products; ragged n exercises the tile edges."""
     n, d = 3001, 64
     X = gaussian(n, d, 401 + metric, metric == 0)
     if metric == 1:
