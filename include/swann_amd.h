@@ -76,10 +76,11 @@ int swann_device_count(void);
 int swann_validate_init(int64_t n, int dim, int x_dtype, int64_t Q, int J, int V, int L,
                         int H, int metric, int team_size, int Hc);
 
-/* Host-only validation of advance arguments (no GPU needed). */
+/* Host-only validation of advance arguments (no GPU needed).  `cwords` is the
+ * sign codes' words per row, 0 when the filter is off. */
 int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, int J, int L,
                            int H, int metric, int team_size, int policy, int V, int Hc,
-                           int64_t nactive, int has_codes);
+                           int64_t nactive, int cwords);
 
 /* Seed every branch, clear the per-query table and bound (init_kernel,
  * local_search.cu:271-351). */
@@ -93,9 +94,16 @@ int swann_init_states(const void* X, int x_dtype, int64_t n, int dim,
 
 /* Up to `delta` best-first expansions per branch, in place (advance_kernel,
  * local_search.cu:353-688).  `active` (nactive entries of flattened q*J+j)
- * restricts the grid to those branches; NULL = all Q*J.  The sign-code filter
- * arguments (codes, cwords, alpha, cmu, code_margin) must be NULL/0: the
- * filter is not built yet and a non-NULL `codes` is refused. */
+ * restricts the grid to those branches; NULL = all Q*J.
+ *
+ * Sign-code pre-filter (local_search.cu:205-243, :560-575; metric ip only):
+ * codes [n, cwords] int32 (bit b of word w: dimension 32w + b above the
+ * mean), alpha [n] fp32, cmu [dim] fp32; NULL codes = off.  A neighbour that
+ * would be scored is first estimated from its code and skipped when the
+ * estimate exceeds the step's stop line by more than code_margin; a skip adds
+ * 1 to counters[3] (which also holds the exhausted flag, as in the
+ * reference), leaves the neighbour a candidate at FLT_MAX and its row
+ * unread. */
 int swann_advance(const void* X, int x_dtype, int64_t n, int dim,
                   const int32_t* G, int D, const float* Qv, int64_t Q, int J,
                   int32_t* ids, float* dist, uint8_t* expd, uint8_t* lin, int L,
@@ -107,6 +115,16 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim,
                   const int32_t* active, int64_t nactive,
                   const int32_t* codes, int cwords, const float* alpha, const float* cmu,
                   float code_margin, void* stream);
+
+/* Sign codes for the pre-filter (no counterpart in the reference, which
+ * ships only their consumer and loader, swann/_engine.py:320-337): mu = the
+ * column means (or mu_in when given), bit set where x > mu, alpha = mean
+ * |x - mu| per row.  codes [n, ceil(dim/32)] int32, alpha [n], mu_out [dim].
+ * `workspace`: swann_codes_workspace_size bytes (unused when mu_in is given). */
+int64_t swann_codes_workspace_size(int64_t n, int dim);
+int swann_build_codes(const void* X, int x_dtype, int64_t n, int dim, const float* mu_in,
+                      int32_t* codes, float* alpha, float* mu_out, void* workspace,
+                      void* stream);
 
 /* Per-query dedup top-k of branch results (merge_branches_kernel,
  * local_search.cu:863-919).  bids/bdist [Q, V, kk] -> out [Q, k]; missing

@@ -72,12 +72,12 @@ def _declare(L):
     L.so_init_branch.argtypes = [P, I, I, P, P, I, I, I, I, I, P, P, P, P, P, P]
     L.so_advance_branch.restype = None
     L.so_advance_branch.argtypes = [P, I, I, P, I, P, P, P, P, P, I, P, I, P,
-                                    I, I, I, I, I, I, F, I, I, F]
+                                    I, I, I, I, I, I, F, I, I, F, P, I, P, P, F]
     L.so_merge.restype = None
     L.so_merge.argtypes = [P, P, I64, I, I, I, P, P]
     L.so_search_query.restype = None
     L.so_search_query.argtypes = [P, I, I, P, I, P, P, I, I, I, I, I, I, I, I, F, I,
-                                  I, I, I, I, F, P, P, P, P, P, P, P, P, P]
+                                  I, I, I, I, F, P, P, P, P, P, P, P, P, P, P, I, P, P, F]
     L.so_search_batch.restype = None
     L.so_search_batch.argtypes = [P, I, I, P, I, P, I64, P, I, I, I, I, I, I, I, I,
                                   F, I, I, I, I, I, P, P, P, I]
@@ -87,6 +87,12 @@ def _declare(L):
     L.so_robust_prune.argtypes = [P, I64, I, I, P, P, I, I, F, P, I]
     L.so_add_reverse.restype = None
     L.so_add_reverse.argtypes = [P, I64, I, I, P, I, F, I, P, I]
+    L.so_code_sums.restype = None
+    L.so_code_sums.argtypes = [P, P, I, P, P]
+    L.so_code_ip.restype = F
+    L.so_code_ip.argtypes = [P, P, F, F, F, I, I, I]
+    L.so_build_codes.restype = None
+    L.so_build_codes.argtypes = [P, I64, I, P, P, P, P]
     L.so_half_to_float_export.restype = F
     L.so_half_to_float_export.argtypes = [ctypes.c_uint16]
 
@@ -159,20 +165,34 @@ def init_branch(X, q, seeds, L=16, H=None, B=16, D=32, metric=METRIC_IP, team=32
     return br
 
 
+def _codes(codes):
+    """(codes [n, cwords] int32, alpha [n] fp32, mu [dim] fp32, margin) or None."""
+    if codes is None:
+        return None, 0, None, None, 0.0, ()
+    cd, al, mu, margin = codes
+    cd = np.ascontiguousarray(cd, dtype=np.int32)
+    al = np.ascontiguousarray(al, dtype=np.float32)
+    mu = np.ascontiguousarray(mu, dtype=np.float32)
+    return _p(cd), cd.shape[1], _p(al), _p(mu), float(margin), (cd, al, mu)
+
+
 def advance_branch(X, G, q, br, delta, B, metric=METRIC_IP, team=32,
                    policy=POLICY_BEST, stop_eps=-1.0, kstop=10, stall_patience=0,
-                   crowd_frac=0.0):
-    """local_search.cu:451-683 for one branch, in place."""
+                   crowd_frac=0.0, codes=None):
+    """local_search.cu:451-683 for one branch, in place.  `codes` is the
+    sign-code filter's (codes, alpha, mu, margin), as the reference's
+    `advance` takes it (_engine.py:281-317)."""
     X, dt = _corpus(X)
     G = np.ascontiguousarray(G, dtype=np.int32)
     q = np.ascontiguousarray(q, dtype=np.float32)
+    cp, cw, ap, mp, mg, _keep = _codes(codes)
     L = len(br.ids)
     lib().so_advance_branch(_p(X), dt, X.shape[1], _p(G), G.shape[1], _p(q),
                             _p(br.ids), _p(br.dist), _p(br.expanded), _p(br.lineage), L,
                             _p(br.visited), len(br.visited), _p(br.counters),
                             int(metric), int(team), int(delta), int(B), int(policy),
                             int(br.V), float(stop_eps), int(kstop), int(stall_patience),
-                            float(crowd_frac))
+                            float(crowd_frac), cp, cw, ap, mp, mg)
     return br
 
 
@@ -197,10 +217,12 @@ def cache_size(J, B, D, share=4.0, cap=1 << 20):
 
 def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                  policy=POLICY_BEST, stop_eps=-1.0, kstop=10, H=None, Hc=0,
-                 bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0):
+                 bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0,
+                 codes=None):
     """All J branches of one query, stepped in turn (every step atomic).
     seeds: [J] or [J, V].  Returns a dict of [J, ...] arrays."""
     X, dt = _corpus(X)
+    cp, cw, ap, mp, mg, _keep = _codes(codes)
     G = np.ascontiguousarray(G, dtype=np.int32)
     q = np.ascontiguousarray(q, dtype=np.float32)
     seeds = np.asarray(seeds, dtype=np.int32)
@@ -219,7 +241,7 @@ def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                           int(kstop), int(Hc), int(bool(bound)), int(bool(exclusive)),
                           int(stall_patience), float(crowd_frac),
                           _p(ids), _p(dist), _p(expd), _p(lin), _p(vis), _p(ctr),
-                          _p(cid), _p(cdd), _p(bnd))
+                          _p(cid), _p(cdd), _p(bnd), cp, cw, ap, mp, mg)
     return dict(ids=ids, dist=dist, expanded=expd, lineage=lin, visited=vis,
                 counters=ctr, cache_id=cid[:Hc], cache_d=cdd[:Hc], bound=bnd[0])
 
@@ -246,6 +268,38 @@ def search_batch(X, G, Q, seeds, k=10, L=16, B=16, metric=METRIC_IP, team=32,
                           int(bool(exclusive)), int(k), _p(oi), _p(od), _p(oc),
                           int(nthreads))
     return (oi, od, oc) if counters else (oi, od)
+
+
+# -- sign codes ----------------------------------------------------------
+def code_sums(q, mu):
+    """(<q, mu>, sum(q)) in the fixed 64-partial order the kernel uses."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    mu = np.ascontiguousarray(mu, dtype=np.float32)
+    a = np.zeros(1, np.float32); b = np.zeros(1, np.float32)
+    lib().so_code_sums(_p(q), _p(mu), len(q), _p(a), _p(b))
+    return a[0], b[0]
+
+
+def code_ip(q, code_row, alpha, mu, team=16):
+    """The code's IP-distance estimate, local_search.cu:222-243."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    code_row = np.ascontiguousarray(code_row, dtype=np.int32)
+    qmu, qsum = code_sums(q, mu)
+    return np.float32(lib().so_code_ip(_p(q), _p(code_row), float(alpha), float(qmu),
+                                       float(qsum), len(q), len(code_row), int(team)))
+
+
+def build_codes(X, mu=None):
+    """Sign codes around the corpus mean: (codes [n, ceil(d/32)] int32,
+    alpha [n] fp32, mu [d] fp32)."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    n, d = X.shape
+    cw = (d + 31) // 32
+    codes = np.empty((n, cw), np.int32); alpha = np.empty(n, np.float32)
+    mu_out = np.empty(d, np.float32)
+    mu_in = None if mu is None else np.ascontiguousarray(mu, dtype=np.float32)
+    lib().so_build_codes(_p(X), n, d, _p(mu_in), _p(codes), _p(alpha), _p(mu_out))
+    return codes, alpha, mu_out
 
 
 # -- merge ---------------------------------------------------------------

@@ -232,7 +232,56 @@ typedef struct {
     float stop_eps; int kstop;
     int32_t* cid; float* cdd; int Hc; float* bound; int exclusive;
     int stall_patience; float crowd_frac;
+    /* sign-code filter (local_search.cu:205-243, :560-575); codes == NULL: off */
+    const int32_t* codes; int cwords; const float* calpha; float qmu, qsum, cmargin;
 } so_cfg;
+
+/* <q, mu> and sum(q) of the code filter, in the kernel's fixed order: 64
+ * partial sums over t = l, l + 64, ..., folded with off = 32 .. 1.  (The
+ * reference's shared-memory atomics, local_search.cu:430-441, leave the order
+ * unspecified; any order is a legal reference result.) */
+void so_code_sums(const float* q, const float* mu, int dim, float* qmu, float* qsum) {
+    float m[64], s[64];
+    for (int l = 0; l < 64; ++l) {
+        m[l] = 0.0f; s[l] = 0.0f;
+        for (int t = l; t < dim; t += 64) {
+            const float p = q[t] * mu[t];
+            m[l] = m[l] + p;
+            s[l] = s[l] + q[t];
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1)
+        for (int l = 0; l < off; ++l) { m[l] = m[l] + m[l + off]; s[l] = s[l] + s[l + off]; }
+    *qmu = m[0]; *qsum = s[0];
+}
+
+/* The code's IP estimate, team_code_ip (local_search.cu:222-243): lane l of
+ * the team adds q over the set bits of words l, l + team, ..., in ascending
+ * dimension; the team folds with off = team/2 .. 1; then
+ * 1 - (alpha * (2 acc - qsum) + qmu), every operation rounded on its own. */
+float so_code_ip(const float* q, const int32_t* code, float alpha, float qmu, float qsum,
+                 int dim, int cwords, int team) {
+    float acc[64];
+    for (int l = 0; l < team; ++l) {
+        float a = 0.0f;
+        for (int w = l; w < cwords; w += team) {
+            const uint32_t bits = (uint32_t)code[w];
+            for (int b = 0; b < 32; ++b) {
+                const int i = w * 32 + b;
+                if (i >= dim) break;
+                if (bits & (1u << b)) a = a + q[i];
+            }
+        }
+        acc[l] = a;
+    }
+    for (int off = team / 2; off > 0; off >>= 1)
+        for (int l = 0; l < off; ++l) acc[l] = acc[l] + acc[l + off];
+    const float t = 2.0f * acc[0];
+    const float u = t - qsum;
+    const float v = alpha * u;
+    const float w = v + qmu;
+    return 1.0f - w;
+}
 
 /* One expansion step of one branch, local_search.cu:451-683.  Returns 0 when
  * the branch's loop ends (budget spent, exhausted, or stalled). */
@@ -248,6 +297,7 @@ static int so_step(const so_cfg* c, int32_t* ids, float* dist, uint8_t* expd, ui
         if (gb < radius) radius = gb;
     }
     const float limit = (radius == FLT_MAX) ? FLT_MAX : radius * (1.0f + c->stop_eps);
+    const float rad = limit;               /* the code filter's line, :471-478 */
     int slot = -1;
     if (c->policy == SO_POLICY_RR && c->V > 1) {
         for (int turn = 0; turn < c->V && slot < 0; ++turn) {
@@ -303,9 +353,19 @@ static int so_step(const so_cfg* c, int32_t* ids, float* dist, uint8_t* expd, ui
         if (c->exclusive && cs >= 0 && !claimed && d != FLT_MAX) {
             ctr[4] += 1;                              /* taken by another branch */
         } else if (d == FLT_MAX) {
-            d = so_team_distance(c->q, c->X, c->dt, v, c->dim, c->metric, c->team);
-            if (cs >= 0) { c->cdd[cs] = d; ctr[5] += 1; }
-            ctr[1] += 1;
+            int skip = 0;
+            if (c->codes) {
+                const float est = so_code_ip(c->q, c->codes + (int64_t)v * c->cwords,
+                                             c->calpha[v], c->qmu, c->qsum, c->dim, c->cwords,
+                                             c->team);
+                skip = (rad != FLT_MAX) && (est > rad + c->cmargin);
+                if (skip) ctr[3] += 1;         /* the reference counts skips in [3] */
+            }
+            if (!skip) {
+                d = so_team_distance(c->q, c->X, c->dt, v, c->dim, c->metric, c->team);
+                if (cs >= 0) { c->cdd[cs] = d; ctr[5] += 1; }
+                ctr[1] += 1;
+            }
         } else {
             ctr[4] += 1;                              /* cache hit */
         }
@@ -384,9 +444,14 @@ void so_advance_branch(const void* X, int dt, int dim, const int32_t* G, int D,
                        uint8_t* lin, int L, int32_t* visited, int H, int32_t* ctr,
                        int metric, int team, int delta, int max_exp, int policy,
                        int V, float stop_eps, int kstop, int stall_patience,
-                       float crowd_frac) {
+                       float crowd_frac, const int32_t* codes, int cwords, const float* calpha,
+                       const float* cmu, float cmargin) {
     so_cfg c;
     memset(&c, 0, sizeof(c));
+    if (codes) {
+        c.codes = codes; c.cwords = cwords; c.calpha = calpha; c.cmargin = cmargin;
+        so_code_sums(q, cmu, dim, &c.qmu, &c.qsum);
+    }
     c.X = X; c.dt = dt; c.dim = dim; c.G = G; c.D = D; c.q = q;
     c.L = L; c.H = H; c.metric = metric; c.team = team;
     c.max_exp = max_exp; c.policy = policy; c.V = V;
@@ -449,7 +514,9 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
                      int stall_patience, float crowd_frac,
                      int32_t* ids, float* dist, uint8_t* expd, uint8_t* lin,
                      int32_t* visited, int32_t* counters,
-                     int32_t* cache_id, float* cache_d, float* bound_out) {
+                     int32_t* cache_id, float* cache_d, float* bound_out,
+                     const int32_t* codes, int cwords, const float* calpha, const float* cmu,
+                     float cmargin) {
     for (int t = 0; t < Hc; ++t) { cache_id[t] = 0; cache_d[t] = FLT_MAX; }
     float bound = FLT_MAX;
     for (int j = 0; j < J; ++j)
@@ -467,6 +534,10 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
     c.bound = use_bound ? &bound : NULL;
     c.exclusive = exclusive;
     c.stall_patience = stall_patience; c.crowd_frac = crowd_frac;
+    if (codes) {
+        c.codes = codes; c.cwords = cwords; c.calpha = calpha; c.cmargin = cmargin;
+        so_code_sums(q, cmu, dim, &c.qmu, &c.qsum);
+    }
     so_locals* lo = (so_locals*)malloc(sizeof(so_locals) * (size_t)J);
     for (int j = 0; j < J; ++j) so_locals_reset(&lo[j]);
     for (int s = 0; s < B; ++s) {
@@ -516,7 +587,8 @@ void so_search_batch(const void* X, int dt, int dim, const int32_t* G, int D,
         for (int64_t qi = 0; qi < nq; ++qi) {
             so_search_query(X, dt, dim, G, D, Qv + qi * dim, seeds + qi * (int64_t)J * V, J, V,
                             L, B, H, metric, team, policy, stop_eps, kstop, Hc, use_bound,
-                            exclusive, 0, 0.0f, ids, dist, expd, lin, vis, ctr, cid, cdd, NULL);
+                            exclusive, 0, 0.0f, ids, dist, expd, lin, vis, ctr, cid, cdd, NULL,
+                            NULL, 0, NULL, NULL, 0.0f);
             for (int j = 0; j < J; ++j)
                 for (int t = 0; t < kk; ++t) {
                     bi[j * kk + t] = ids[j * L + t];
@@ -742,4 +814,40 @@ void so_add_reverse(const float* X, int64_t n, int dim, int metric, const int32_
         free(row); free(sc); free(cand); free(cd); free(vn); free(kept);
     }
     free(cnt); free(in);
+}
+
+/* ------------------------------------------------------------------ */
+/* Sign codes for the filter.  The reference ships the consumer
+ * (local_search.cu:205-243, _engine.py:320-337) but not the builder; the
+ * definition here is the one the consumer's estimator assumes: mu is the
+ * corpus mean (double sums, rounded to fp32, unless given), bit b of word w is
+ * set when x[32w + b] > mu[32w + b], and alpha = sum |x - mu| / dim (double
+ * sum of the fp32 differences, rounded to fp32). */
+void so_build_codes(const float* X, int64_t n, int dim, const float* mu_in, int32_t* codes,
+                    float* alpha, float* mu_out) {
+    const int cwords = (dim + 31) / 32;
+    if (mu_in) {
+        memcpy(mu_out, mu_in, sizeof(float) * (size_t)dim);
+    } else {
+        double* acc = (double*)calloc((size_t)dim, sizeof(double));
+        for (int64_t r = 0; r < n; ++r)
+            for (int t = 0; t < dim; ++t) acc[t] += (double)X[r * dim + t];
+        for (int t = 0; t < dim; ++t) mu_out[t] = (float)(acc[t] / (double)n);
+        free(acc);
+    }
+    for (int64_t r = 0; r < n; ++r) {
+        double l1 = 0.0;
+        for (int w = 0; w < cwords; ++w) {
+            uint32_t bits = 0;
+            for (int b = 0; b < 32; ++b) {
+                const int t = w * 32 + b;
+                if (t >= dim) break;
+                const float df = X[r * dim + t] - mu_out[t];
+                if (df > 0.0f) bits |= (1u << b);
+                l1 += (double)fabsf(df);
+            }
+            codes[r * cwords + w] = (int32_t)bits;
+        }
+        alpha[r] = (float)(l1 / (double)dim);
+    }
 }

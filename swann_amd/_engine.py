@@ -222,12 +222,29 @@ def advance(X, G, Qv, state: SearchState, delta_expansions: int, active=None,
             codes=None) -> SearchState:
     """Advance every branch by up to delta more expansions, in place;
     swann/_engine.py:281-317.  `active` (int32 flattened q*J+j) restricts the
-    launch to those branches.  The sign-code filter (`codes`) is not built."""
+    launch to those branches.
+
+    `codes` is an optional (codes, alpha, mu, margin), as `load_codes` or
+    `swann_amd.codes.build_codes` give it: each neighbour that would be scored
+    is first estimated from its sign code and its row is read only when the
+    estimate leaves it within `margin` of the step's stop line.  It changes
+    which distances are computed, so it is off unless asked for; a skip adds 1
+    to `exhausted` (counter 3), exactly as the reference counts it."""
     if not (G.is_cuda and G.dtype == torch.int32 and G.is_contiguous() and G.dim() == 2):
         raise RuntimeError("G: contiguous cuda int32 [n, D]")
-    if codes is not None:
-        raise NotImplementedError("the sign-code pre-filter is not implemented in swann_amd")
     _check_corpus(X, Qv)
+    cd = al = cm = None
+    cw, mg = 0, 0.0
+    if codes is not None:
+        cd, al, cm, mg = codes
+        if not (cd.is_cuda and cd.dtype == torch.int32 and cd.is_contiguous() and cd.dim() == 2):
+            raise RuntimeError("codes: contiguous cuda int32 [n, words]")
+        if not (al.is_cuda and al.dtype == torch.float32 and al.is_contiguous()
+                and cm.is_cuda and cm.dtype == torch.float32 and cm.is_contiguous()):
+            raise RuntimeError("alpha and mu: contiguous cuda float32")
+        if al.numel() != cd.shape[0] or cd.shape[0] != X.shape[0] or cm.numel() != X.shape[1]:
+            raise RuntimeError("codes, alpha and mu must agree with the corpus")
+        cw = cd.shape[1]
     Q, J, L = state.ids.shape
     H = state.visited.shape[-1]
     Hc = state.cache_id.shape[1] if state.cache_id is not None and state.cache_id.numel() else 0
@@ -247,8 +264,27 @@ def advance(X, G, Qv, state: SearchState, delta_expansions: int, active=None,
              ptr(state.cache_id) if Hc else None, ptr(state.cache_d) if Hc else None, Hc,
              ptr(state.bound), int(bool(state.exclusive)), int(state.stall_patience),
              float(state.crowd_frac), ptr(active) if nact else None, nact,
-             None, 0, None, None, 0.0, stream_of(dev))
+             ptr(cd) if cw else None, cw, ptr(al) if cw else None, ptr(cm) if cw else None,
+             float(mg), stream_of(dev))
     return state
+
+
+def load_codes(data, name=None, margin=0.20, device="cuda"):
+    """The sign code, its per-node scale and the corpus mean, as `advance`
+    wants them (swann/_engine.py:320-337): codes_<name>.npy, alpha_<name>.npy
+    and mu_<name>.npy under `data`; `name` defaults from manifest.json's
+    metric ("1bit" for ip).  `margin` is in the corpus's distance units."""
+    import json
+    from pathlib import Path
+    import numpy as np
+    d = Path(data)
+    if name is None:
+        man = json.loads((d / "manifest.json").read_text())
+        name = "1bit" if man["metric"].startswith("ip") else "int8"
+    cd = torch.from_numpy(np.load(d / f"codes_{name}.npy")).to(device)
+    al = torch.from_numpy(np.load(d / f"alpha_{name}.npy")).to(device)
+    cm = torch.from_numpy(np.load(d / f"mu_{name}.npy")).to(device)
+    return cd.contiguous(), al.contiguous(), cm.contiguous(), margin
 
 
 def branch_topk(state: SearchState, k: int):

@@ -41,6 +41,8 @@ PROTOTYPES = {
     "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P]),
     "swann_reverse_workspace_size": (I64, [I64, I, I]),
     "swann_build_reverse": (I, [P, I, I64, I, I, P, I, F, I, P, P, P]),
+    "swann_codes_workspace_size": (I64, [I64, I]),
+    "swann_build_codes": (I, [P, I, I64, I, P, P, P, P, P, P]),
 }
 
 _lib = None

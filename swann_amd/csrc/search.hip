@@ -132,6 +132,34 @@ __device__ __forceinline__ float team_dist_m(const float* sq, const XT* x, int d
                                      : team_dist<TEAM, XT, SWANN_METRIC_L2>(sq, x, dim, tl, vec_ok);
 }
 
+// Sign-code estimate of the IP distance (local_search.cu:205-243): with the
+// node's code b in {-1, +1}^dim taken around the corpus mean mu and its scale
+// alpha, <q, x> ~ alpha * <q, b> + <q, mu> and <q, b> = 2 * (sum of q over set
+// bits) - sum(q).  Lane tl of a TEAM owns code words tl, tl + TEAM, ...; each
+// lane adds q over its set bits in ascending dimension, then the team folds
+// with off = TEAM/2 .. 1.  Walking only the set bits (ctz) adds exactly the
+// terms the bit-by-bit loop adds, in the same order.  Meaningful in tl == 0.
+template <int TEAM>
+__device__ __forceinline__ float team_code_ip(const float* __restrict__ sq,
+                                              const int32_t* __restrict__ code, float alpha,
+                                              float qmu, float qsum, int dim, int cwords,
+                                              int tl) {
+    float acc = 0.f;
+    for (int w = tl; w < cwords; w += TEAM) {
+        unsigned bits = (unsigned)code[w];
+        const int base = w * 32;
+        while (bits) {
+            const int i = base + __builtin_ctz(bits);
+            if (i >= dim) break;
+            acc = acc + sq[i];
+            bits &= bits - 1u;
+        }
+    }
+#pragma unroll
+    for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
+    return 1.f - (alpha * (2.f * acc - qsum) + qmu);
+}
+
 // Per-branch visited set: open addressing, linear probe, slot = key + 1
 // (local_search.cu:94-110).  Private to the workgroup.
 __device__ __forceinline__ int vis_insert(int* tab, int H, int key, int* fail) {
@@ -345,6 +373,7 @@ struct AdvArgs {
     int stall_patience; float crowd_frac;
     const int32_t* active; int64_t nblocks, nbranch, n;
     int vec_ok;
+    const int32_t* codes; const float* calpha; const float* cmu; int cwords; float cmargin;
 };
 
 template <int TEAM, typename XT, int BLOCK>
@@ -387,7 +416,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     __shared__ int s_ctr[kNctr];
     __shared__ int s_slot, s_p, s_plin, s_nkeep, s_nwork, s_nbr, s_cov, s_stall, s_crowd_run;
     __shared__ unsigned s_retired[8];
-    __shared__ float s_best_k;
+    __shared__ float s_best_k, s_rad, s_qmu, s_qsum;
 
     int32_t* vis = a.visited + flat * (int64_t)a.H;
     int32_t* ctr = a.counters + flat * kNctr;
@@ -406,6 +435,26 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     if (tid < 8) s_retired[tid] = 0u;
     if (tid == 0) { s_best_k = FLT_MAX; s_stall = 0; s_crowd_run = 0; }
     __syncthreads();
+
+    if (a.codes && wave == 0) {
+        // <q, mu> and sum(q), once per call, in a fixed order that does not
+        // depend on BLOCK: lane l sums t = l, l + 64, ..., then the wave folds
+        // with off = 32 .. 1.  (The reference sums through shared-memory
+        // atomics, local_search.cu:430-441, whose order is unspecified.)
+        float m = 0.f, s = 0.f;
+        for (int t = lane; t < a.dim; t += 64) {
+            const float qt = sq[t];
+            m = m + qt * a.cmu[t];
+            s = s + qt;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            m = m + __shfl_down(m, off, 64);
+            s = s + __shfl_down(s, off, 64);
+        }
+        if (lane == 0) { s_qmu = m; s_qsum = s; }
+    }
+    if (a.codes) __syncthreads();
 
     int r_evals = 0, r_fail = 0, r_hits = 0, r_claim = 0;
     const bool early = (a.stop_eps >= 0.f);
@@ -465,6 +514,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             }
             if (lane == 0) {
                 s_slot = slot;
+                s_rad = limit;                  // the code filter's line (:471-478)
                 if (slot >= 0) {
                     qa_e[slot] = 1;
                     s_p = qa_id[slot];
@@ -513,6 +563,23 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         const int nw = s_nwork;
         for (int w = team; w < nw; w += NT) {
             const int v = w_v[w];
+            if (a.codes) {
+                // decide from the code before reading the row (:560-575); a
+                // skipped neighbour stays a candidate at FLT_MAX, unscored,
+                // with its table slot claimed but never filled
+                float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords, a.calpha[v],
+                                               s_qmu, s_qsum, a.dim, a.cwords, tl);
+                est = __shfl(est, 0, TEAM);
+                const float rad = s_rad;
+                if (rad != FLT_MAX && est > rad + a.cmargin) {
+                    if (tl == 0) {
+                        const int nidx = w_nidx[w] & 0xffff;
+                        atomicAdd(&s_ctr[3], 1);
+                        c_id[nidx] = v; c_d[nidx] = FLT_MAX; c_l[nidx] = plin;
+                    }
+                    continue;
+                }
+            }
             const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
                                                  a.vec_ok, a.metric);
             if (tl == 0) {
@@ -781,7 +848,7 @@ int swann_validate_init(int64_t n, int dim, int x_dtype, int64_t Q, int J, int V
 
 int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, int J, int L,
                            int H, int metric, int team_size, int policy, int V, int Hc,
-                           int64_t nactive, int has_codes) {
+                           int64_t nactive, int cwords) {
     clear_error();
     SWANN_REQUIRE(n > 0 && dim > 0, "X must be a non-empty [n, dim] matrix");
     SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
@@ -802,8 +869,12 @@ int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, in
     SWANN_REQUIRE(nactive >= 0 && nactive <= Q * (int64_t)J, "active list longer than Q*J");
     SWANN_REQUIRE(Q * (int64_t)J <= (int64_t)INT32_MAX / 64,
                   "Q*J = %lld branches exceed the launch limit", (long long)(Q * J));
-    SWANN_REQUIRE(!has_codes,
-                  "the sign-code filter is not supported by this build (pass codes=None)");
+    SWANN_REQUIRE(cwords >= 0, "cwords must be >= 0 (0: no sign codes)");
+    SWANN_REQUIRE(cwords == 0 || metric == SWANN_METRIC_IP,
+                  "the sign-code filter is written for the normalised inner-product corpora; "
+                  "an unnormalised L2 corpus needs int8 codes and a stored squared norm");
+    SWANN_REQUIRE(cwords == 0 || (int64_t)cwords * 32 >= dim,
+                  "code words do not cover the dimension");
     const size_t lds = advance_lds(dim, D, L);
     SWANN_REQUIRE(lds <= kMaxLds, "advance needs %zu B of LDS (limit %zu); lower L or the dimension",
                   lds, kMaxLds);
@@ -839,10 +910,11 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
                   int exclusive, int stall_patience, float crowd_frac, const int32_t* active,
                   int64_t nactive, const int32_t* codes, int cwords, const float* alpha,
                   const float* cmu, float code_margin, void* stream) {
-    (void)cwords; (void)alpha; (void)cmu; (void)code_margin;
     int rc = swann_validate_advance(n, dim, x_dtype, D, Q, J, L, H, metric, team_size, policy, V,
-                                    Hc, active ? nactive : 0, codes != nullptr);
+                                    Hc, active ? nactive : 0, codes ? cwords : 0);
     if (rc) return rc;
+    SWANN_REQUIRE(!codes || cwords > 0, "advance: codes given with cwords = 0");
+    SWANN_REQUIRE(!codes || (alpha && cmu), "advance: codes need alpha and cmu");
     SWANN_REQUIRE(Q == 0 || (X && G && Qv && ids && dist && expd && lin && visited && counters),
                   "advance: a required pointer is NULL");
     SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "advance: Hc > 0 needs cache_id and cache_d");
@@ -853,7 +925,9 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
               delta, max_expansions, policy, V, stop_eps, kstop,
               Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound, exclusive ? 1 : 0,
               stall_patience, crowd_frac, active, nb, Q * J, n,
-              rows_vec_ok(X, dim, x_dtype) ? 1 : 0};
+              rows_vec_ok(X, dim, x_dtype) ? 1 : 0,
+              codes, codes ? alpha : nullptr, codes ? cmu : nullptr, codes ? cwords : 0,
+              code_margin};
     const int block = search_block_for(nb);
     SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
                    advance_lds(dim, D, L), (hipStream_t)stream, a);

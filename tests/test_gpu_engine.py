@@ -385,3 +385,103 @@ def test_claims_and_bound_multi_branch_statistics():
         for i, dv in zip(ids[q], dist[q]):
             if i >= 0:
                 assert dv == O.team_distance(Q[q], X, int(i), 0, 16)
+
+
+def test_code_filter_matches_oracle(block):
+    """The sign-code pre-filter (local_search.cu:205-243, :560-575) against the
+    oracle: independent branches, several teams and margins, bit-exact queues
+    and counters -- counter 3 carries the skips, as in the reference."""
+    X, G = toy(seed=5)
+    codes, alpha, mu = O.build_codes(X)
+    rng = np.random.default_rng(17)
+    nq, J, L, budget = 6, 3, 16, 24
+    Qv = gaussian(nq, X.shape[1], 55, True)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg, Cg, Ag, Mg = to_gpu(X, G, Qv, codes, alpha, mu)
+    skipped = 0
+    for team in (4, 16, 64):
+        for margin in (0.0, 0.05, 0.2):
+            note("code filter", block, team, margin)
+            st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=L, B=budget, D=G.shape[1],
+                               team_size=team, stop_eps=0.1, kstop=10)
+            E.advance(Xg, Gg, Qg, st, budget, codes=(Cg, Ag, Mg, margin))
+            for qi in range(nq):
+                for j in range(J):
+                    br = O.init_branch(X, Qv[qi], [int(seeds[qi, j])], L=L, B=budget,
+                                       D=G.shape[1], team=team)
+                    O.advance_branch(X, G, Qv[qi], br, budget, budget, team=team, stop_eps=0.1,
+                                     kstop=10, codes=(codes, alpha, mu, margin))
+                    assert_queue(st, qi, j, br, ("codes", team, margin, qi, j))
+            skipped += int(st.counters[..., 3].sum())
+    assert skipped > 0                      # the filter did act
+
+
+def test_code_filter_with_shared_table_matches_serial_schedule():
+    """Codes plus the shared table (no claims, no bound): a skipped neighbour
+    leaves its claimed slot unfilled and other branches score it themselves,
+    so every branch's answer equals the oracle's serial schedule."""
+    X, G = toy(seed=6)
+    codes, alpha, mu = O.build_codes(X)
+    rng = np.random.default_rng(19)
+    nq, J, L, budget = 4, 4, 16, 16
+    Qv = gaussian(nq, X.shape[1], 56, True)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg, Cg, Ag, Mg = to_gpu(X, G, Qv, codes, alpha, mu)
+    st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=L, B=budget, D=G.shape[1],
+                       team_size=16, stop_eps=0.1, kstop=10, shared_cache=True)
+    E.advance(Xg, Gg, Qg, st, budget, codes=(Cg, Ag, Mg, 0.05))
+    Hc = st.cache_id.shape[1]
+    for qi in range(nq):
+        r = O.search_query(X, G, Qv[qi], seeds[qi], L=L, B=budget, team=16, stop_eps=0.1,
+                           kstop=10, Hc=Hc, codes=(codes, alpha, mu, 0.05))
+        assert np.array_equal(st.ids[qi].cpu().numpy(), r["ids"])
+        assert st.dist[qi].cpu().numpy().tobytes() == r["dist"].tobytes()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_build_codes_matches_oracle(dtype):
+    from swann_amd.codes import build_codes
+    X = gaussian(5000, 200, 9, False)            # 200 = 6 words + 8 bits
+    if dtype == "f16":
+        X = X.astype(np.float16)
+    Xg = torch.from_numpy(X).cuda()
+    c, a, m = build_codes(Xg)
+    oc, oa, om = O.build_codes(X.astype(np.float32))
+    assert c.shape == (5000, 7) and c.dtype == torch.int32
+    assert np.allclose(m.cpu().numpy(), om, rtol=1e-6, atol=1e-8)
+    # given the same mean, the bits are exact and alpha agrees to rounding
+    c2, a2, m2 = build_codes(Xg, mu=torch.from_numpy(om).cuda())
+    assert np.array_equal(c2.cpu().numpy(), oc)
+    assert np.allclose(a2.cpu().numpy(), oa, rtol=1e-6, atol=0)
+    assert torch.equal(m2.cpu(), torch.from_numpy(om))
+    assert (c.cpu().numpy() == oc).mean() > 0.999
+
+
+def test_code_filter_cuts_reads_at_small_recall_cost():
+    """Multi-branch search with claims and bound on a low-rank corpus: the
+    filter reads fewer rows, and recall stays close (statistical: the
+    reference reports 100% of admitted candidates kept at its margin)."""
+    from swann_amd.codes import build_codes
+    rng = np.random.default_rng(3)
+    n, d, r = 20000, 128, 16
+    W = rng.standard_normal((r, d)).astype(np.float32)
+
+    def draw(m):
+        x = rng.standard_normal((m, r)).astype(np.float32) @ W / np.sqrt(r)
+        x += 0.1 * rng.standard_normal((m, d)).astype(np.float32)
+        return (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32)
+    X, Q = draw(n), draw(300)
+    G = knn_graph(X, 32, 0)
+    Xg, Gg, Qg = to_gpu(X, G, Q)
+    cd, al, cm = build_codes(Xg)
+    seeds = torch.from_numpy(rng.integers(0, n, (300, 16)).astype(np.int32)).cuda()
+    truth = exact_topk(X, Q, 10)
+    out = {}
+    for name, codes in (("plain", None), ("codes", (cd, al, cm, 0.2))):
+        ids, _, st = E.search(Xg, Gg, Qg, seeds, k=10, L=32, B=48, metric=0, team_size=16,
+                              stop_eps=0.1, shared_cache=True, shared_bound=True, exclusive=True,
+                              elide_visited=True, codes=codes)
+        out[name] = (recall(ids.cpu().numpy(), truth, 10), int(st.dist_evals.sum()))
+    note("code filter recall/evals", out)
+    assert out["codes"][1] < out["plain"][1]
+    assert out["codes"][0] >= out["plain"][0] - 0.05

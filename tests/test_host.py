@@ -43,7 +43,7 @@ def _vinit(**kw):
 
 def _vadv(**kw):
     a = dict(n=1000, dim=128, x_dtype=0, D=32, Q=4, J=2, L=16, H=1024, metric=0, team_size=16,
-             policy=0, V=1, Hc=0, nactive=0, has_codes=0)
+             policy=0, V=1, Hc=0, nactive=0, cwords=0)
     a.update(kw)
     return _lib.lib().swann_validate_advance(*a.values())
 
@@ -61,6 +61,8 @@ def test_validation_accepts_the_reference_configs():
     assert _vadv(dim=4096, x_dtype=1, D=64, L=12, Q=512, J=128, H=1, Hc=524288) == 0
     # no 65535-query cap
     assert _vinit(Q=70000, J=32) == 0 and _vadv(Q=70000, J=32) == 0
+    # sign codes (ip): one bit per dimension, at least ceil(dim / 32) words
+    assert _vadv(cwords=4) == 0 and _vadv(dim=1536, x_dtype=1, D=64, cwords=48) == 0
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -83,7 +85,9 @@ def test_init_validation_refuses(kw, msg):
     (dict(L=600), "MAXL"),
     (dict(V=300), "uint8"),
     (dict(policy=7), "policy"),
-    (dict(has_codes=1), "sign-code"),
+    (dict(cwords=4, metric=1), "inner-product"),
+    (dict(cwords=3), "code words do not cover"),
+    (dict(cwords=-1), "cwords"),
     (dict(nactive=100), "active"),
     (dict(dim=20000), "LDS"),
 ])

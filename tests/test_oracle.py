@@ -372,3 +372,127 @@ def test_prune_rule_invariants():
                             1.2 * ((X64[w] - X64[c]) ** 2).sum() <= cdist[u, i] - 1e-4]
             else:
                 assert blockers
+
+
+# -- sign-code filter (local_search.cu:205-243, :560-575) ---------------------
+def test_code_builder_matches_its_definition():
+    """Bits are x > mu with bit b of word w for dimension 32w + b; mu is the
+    column mean and alpha the mean |x - mu| (both against float64 numpy)."""
+    rng = np.random.default_rng(21)
+    X = rng.standard_normal((60, 70)).astype(np.float32)
+    codes, alpha, mu = O.build_codes(X)
+    assert codes.shape == (60, 3) and codes.dtype == np.int32
+    assert np.allclose(mu, X.astype(np.float64).mean(0), rtol=0, atol=1e-7)
+    w = codes.view(np.uint32)
+    bits = np.stack([(w[:, t // 32] >> np.uint32(t % 32)) & 1 for t in range(70)], 1)
+    assert np.array_equal(bits.astype(bool), X > mu[None, :])
+    assert (w[:, 2] >> np.uint32(6)).max() == 0                       # bits past dim stay 0
+    want = np.abs(X.astype(np.float64) - mu.astype(np.float64)).mean(1)
+    assert np.allclose(alpha, want, rtol=1e-6, atol=0)
+    # a given mu is used as is
+    c2, a2, m2 = O.build_codes(X, mu=np.zeros(70, np.float32))
+    assert np.array_equal(m2, np.zeros(70, np.float32))
+    w2 = c2.view(np.uint32)
+    assert np.array_equal(np.stack([(w2[:, t // 32] >> np.uint32(t % 32)) & 1 for t in range(70)], 1)
+                          .astype(bool), X > 0)
+    assert np.allclose(a2, np.abs(X.astype(np.float64)).mean(1), rtol=1e-6)
+
+
+def test_code_estimate_closed_form():
+    """1 - (alpha <q, b> + <q, mu>) with b in {-1, +1}, in float64, for every
+    team: a dropped sum(q), a sign error or a misread bit moves it by O(1)."""
+    rng = np.random.default_rng(22)
+    for d in (32, 70, 128, 1536):
+        X = rng.standard_normal((5, d)).astype(np.float32)
+        codes, alpha, mu = O.build_codes(X)
+        q = rng.standard_normal(d).astype(np.float32) / np.sqrt(d)
+        for r in range(5):
+            b = np.where(X[r] > mu, 1.0, -1.0)
+            want = 1.0 - (float(alpha[r]) * float(q.astype(np.float64) @ b)
+                          + float(q.astype(np.float64) @ mu.astype(np.float64)))
+            for team in (4, 16, 64):
+                got = O.code_ip(q, codes[r], alpha[r], mu, team)
+                assert abs(float(got) - want) < 1e-5 * max(1.0, abs(want)), (d, r, team)
+
+
+def test_code_estimate_bit_order():
+    """q = 3 e_37 and mu = 0: the estimate is 1 - alpha (2 * 3 * bit - 3), so
+    only bit 5 of word 1 may move it."""
+    q = np.zeros(70, np.float32); q[37] = 3.0
+    mu = np.zeros(70, np.float32)
+    code = np.zeros(3, np.int32)
+    assert O.code_ip(q, code, 0.5, mu, 4) == np.float32(1.0 - 0.5 * -3.0)
+    code[1] = 1 << 5
+    assert O.code_ip(q, code, 0.5, mu, 4) == np.float32(1.0 - 0.5 * 3.0)
+    code[1] = 1 << 4; code[0] = -1
+    assert O.code_ip(q, code, 0.5, mu, 4) == np.float32(1.0 - 0.5 * -3.0)
+
+
+def test_code_estimate_lane_layout():
+    """team 2: lane 0 owns words 0 and 2, lane 1 owns word 1.  With 2^24 in
+    word 0 and -2^24 in word 2 cancelling in lane 0, the two 1s of lane 1
+    survive; summed in dimension order they would be absorbed.  sum(q) uses
+    64 partials (t = l, l + 64, ...): 2^24 and -2^24 meet in partial 0."""
+    q = np.zeros(96, np.float32)
+    q[0], q[64], q[32], q[33] = 2.0 ** 24, -(2.0 ** 24), 1.0, 1.0
+    mu = np.zeros(96, np.float32)
+    code = np.array([1, 3, 1], np.int32)          # bits at dims 0, 32, 33, 64
+    qmu, qsum = O.code_sums(q, mu)
+    assert qsum == np.float32(2.0) and qmu == np.float32(0.0)
+    # acc = 2 (lane order), est = 1 - (1 * (2 * 2 - 2) + 0) = -1
+    assert O.code_ip(q, code, 1.0, mu, 2) == np.float32(-1.0)
+
+
+def _star_case():
+    """Seed 0 with neighbours 1..5; q = e_0.  Codes put 1 and 2 at estimate 0.5
+    and 3, 4, 5 at 1.5; the stop line after init is d(seed) = 0.5."""
+    d = 32
+    X = np.zeros((6, d), np.float32)
+    X[0, 0], X[1, 0], X[2, 0], X[3, 0], X[4, 0], X[5, 0] = 0.5, 0.9, 0.8, 0.95, 0.97, 0.99
+    X[:, 1] = np.sqrt(1.0 - X[:, 0] ** 2)
+    G = np.full((6, 8), -1, np.int32)
+    G[0, :5] = [1, 2, 3, 4, 5]
+    q = np.zeros(d, np.float32); q[0] = 1.0
+    codes = np.zeros((6, 1), np.int32)
+    codes[[1, 2], 0] = 1                           # bit 0 set: estimate 1 - 0.5 = 0.5
+    alpha = np.full(6, 0.5, np.float32)
+    mu = np.zeros(d, np.float32)
+    return X, G, q, (codes, alpha, mu, 0.1)
+
+
+def test_code_filter_skip_semantics():
+    """One expansion: 3, 4 and 5 estimate beyond 0.5 + 0.1 and are skipped --
+    their rows are not read and [3] counts 3.  They stay candidates at
+    FLT_MAX and pass the filter (the queue is not full, so its worst is
+    FLT_MAX: [8] counts 5), but the queue's empty slots are (FLT_MAX, -1) and
+    win that tie in the merge, so they never enter."""
+    X, G, q, codes = _star_case()
+    br = O.init_branch(X, q, [0], L=8, H=64, B=4, D=8, metric=O.METRIC_IP, team=4)
+    O.advance_branch(X, G, q, br, 1, 4, metric=O.METRIC_IP, team=4, stop_eps=0.0, kstop=1,
+                     codes=codes)
+    d1 = O.team_distance(q, X, 1, O.METRIC_IP, 4)
+    d2 = O.team_distance(q, X, 2, O.METRIC_IP, 4)
+    d0 = O.team_distance(q, X, 0, O.METRIC_IP, 4)
+    assert list(br.ids) == [1, 2, 0, -1, -1, -1, -1, -1]
+    assert list(br.dist[:3]) == [d1, d2, d0] and (br.dist[3:] == F32MAX).all()
+    assert list(br.expanded) == [0, 0, 1, 1, 1, 1, 1, 1]
+    assert br.counters[3] == 3 and br.counters[1] == 3 and br.counters[8] == 5
+    # without codes every neighbour is scored and [3] stays 0
+    br2 = O.init_branch(X, q, [0], L=8, H=64, B=4, D=8, metric=O.METRIC_IP, team=4)
+    O.advance_branch(X, G, q, br2, 1, 4, metric=O.METRIC_IP, team=4, stop_eps=0.0, kstop=1)
+    assert br2.counters[3] == 0 and br2.counters[1] == 6
+
+
+def test_code_filter_is_inert_with_a_huge_margin():
+    X, G = gaussian(1500, 64, 31, True), None
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 24, 0)
+    codes, alpha, mu = O.build_codes(X)
+    Qv = gaussian(6, 64, 32, True)
+    for qi in range(6):
+        a = O.run(X, G, Qv[qi], [qi * 7], L=16, B=20, team=16, stop_eps=0.1, kstop=10)
+        br = O.init_branch(X, Qv[qi], [qi * 7], L=16, B=20, D=24, team=16)
+        O.advance_branch(X, G, Qv[qi], br, 20, 20, team=16, stop_eps=0.1, kstop=10,
+                         codes=(codes, alpha, mu, 1e30))
+        assert np.array_equal(a.ids, br.ids) and a.dist.tobytes() == br.dist.tobytes()
+        assert np.array_equal(a.counters, br.counters)
