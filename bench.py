@@ -40,7 +40,12 @@ CONFIGS = {
                nq=10_000, D=64, cand=128, branches=32, team=16),
     "c3": dict(n=1_000_000, d=1536, dtype="f16", metric="ip", gen="lowrank", rank=256, seed=3,
                nq=10_000, D=64, cand=128, branches=32, team=16),
+    # small-batch latency; --config c4 prints its own line (see run_c4)
+    "c4": dict(n=500_000, d=4096, dtype="f16", metric="ip", gen="lowrank", rank=512, seed=4,
+               nq=2048, D=64, cand=128, branches=32, team=32),
 }
+C4_BRANCHES = (32, 128)
+C4_BATCHES = (1, 8, 64, 512)
 EPS_SWEEP = (0.02, 0.05, 0.1, 0.2)
 # If no stop_eps reaches the target at the configured knobs, the search effort
 # is raised along this ladder (branches, queue, budget, stop_eps), cheapest first.
@@ -198,6 +203,82 @@ def cpu_baseline(X, G, Q, seeds, cfg, eps, k, nsample, metric_id, elem_bytes):
                 seconds=round(dt, 2))
 
 
+def run_c4(a, dev):
+    """Config C4: p50/p99 latency of one batch (1, 8, 64, 512 queries) at
+    branches 32 and 128, queue 12, team 32, the other knobs at their defaults,
+    each batch drawn uniformly from a 2,048-query pool.  The search is
+    captured once per (branches, batch) as a HIP graph (`Index.capture`, no
+    overflow guard) and replayed; the eager search is timed beside it.  A
+    latency is the host's wall clock from replay to completion."""
+    import swann_amd
+    from swann_amd.build import build_graph
+    cfg = dict(CONFIGS["c4"])
+    n = a.n or cfg["n"]
+    npool = a.nq or cfg["nq"]
+    k = 10
+    t0 = time.perf_counter()
+    X32, Qpool = generate(cfg, n, npool, dev)
+    truth = ground_truth(X32, Qpool, k, cfg["metric"])
+    X = X32.half()
+    del X32
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+    log(f"c4: generated n={n} d={cfg['d']} pool={npool} in {time.perf_counter() - t0:.1f}s")
+    tb = time.perf_counter()
+    G = build_graph(X, metric="ip", degree=cfg["D"], candidates=cfg["cand"], alpha=1.2)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - tb
+    log(f"c4: graph built in {build_s:.1f}s")
+    index = swann_amd.Index(X, G, metric="ip")
+    rng = np.random.default_rng(0)
+    rows = []
+    for J in C4_BRANCHES:
+        for b in C4_BATCHES:
+            knobs = dict(branches=J, queue=12, team=cfg["team"])
+            cs = index.capture(b, k=k, **knobs)
+            reps = {1: 200, 8: 100, 64: 40, 512: 12}[b]
+            lat_g, lat_e, hits = [], [], 0.0
+            for r in range(reps + 2):
+                idx = torch.from_numpy(rng.choice(npool, size=b, replace=False)).to(dev)
+                qb = Qpool[idx].contiguous()
+                torch.cuda.synchronize()
+                t1 = time.perf_counter()
+                ids, _ = cs.run(qb)
+                torch.cuda.synchronize()
+                tg = time.perf_counter() - t1
+                t1 = time.perf_counter()
+                index.search_async(qb, k=k, **knobs)
+                torch.cuda.synchronize()
+                te = time.perf_counter() - t1
+                if r >= 2:                                   # two warm replays
+                    lat_g.append(tg * 1e3); lat_e.append(te * 1e3)
+                    hits += recall(ids, truth[idx], k) * b
+            ng = np.array(lat_g); ne = np.array(lat_e)
+            row = dict(branches=J, batch=b, replays=reps,
+                       p50_ms=round(float(np.percentile(ng, 50)), 4),
+                       p99_ms=round(float(np.percentile(ng, 99)), 4),
+                       eager_p50_ms=round(float(np.percentile(ne, 50)), 4),
+                       eager_p99_ms=round(float(np.percentile(ne, 99)), 4),
+                       qps_at_p50=round(b / (float(np.percentile(ng, 50)) / 1e3), 1),
+                       recall_at_10=round(hits / (reps * b), 4))
+            log(row)
+            rows.append(row)
+            del cs
+            torch.cuda.empty_cache()
+    out = {
+        "metric": "C4 per-batch latency p50/p99 (hipGraph replay) and recall@10",
+        "unit": "ms", "higher_is_better": False, "n_gpus": 1, "dtype": "f32",
+        "data": "synthetic (generated on the GPU from fixed seeds; graph built by this library)",
+        "config": {"workload": f"C4: n={n:,} x d={cfg['d']} fp16 ip (lowrank {cfg['rank']}), "
+                               f"pool of {npool:,} fp32 queries, D={cfg['D']}, k={k}, "
+                               f"queue=12, team={cfg['team']}, budget=64, stop_eps=0.05, "
+                               f"overflow guard off"},
+        "build_s": round(build_s, 2),
+        "rows": rows,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,6 +299,12 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+
+    if a.config == "c4":
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        run_c4(a, dev)
+        return
 
     import swann_amd
     from swann_amd.build import build_graph

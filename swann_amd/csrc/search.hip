@@ -10,8 +10,9 @@
 // run:
 //   * one workgroup per (query, branch) over a 1-D grid (no 65535-query cap),
 //     XCD-remapped so a query's branches share one L2;
-//   * BLOCK = 64 (one wave; every barrier folds away) for batch work, or 256
-//     for small batches where latency rules;
+//   * BLOCK = 64 (one wave; every barrier folds away) for batch work, 256
+//     for small batches, 1024 for grids too small to give every CU two
+//     branches, where the serial chain of expansions is the latency;
 //   * the neighbour list of an expansion is screened lane-parallel first
 //     (visited insert, table probe, claim), then only the survivors are
 //     scored, TEAM lanes per distance, with every 16-byte row load of a lane
@@ -771,14 +772,19 @@ size_t advance_lds(int dim, int D, int L) {
 }
 
 int search_block_for(int64_t nbranch) {
-    // SWANN_SEARCH_BLOCK=64|256 pins the workgroup size (tests use it to run
-    // both layouts on the same inputs); read per call, it costs a getenv.
+    // SWANN_SEARCH_BLOCK=64|256|1024 pins the workgroup size (tests use it to
+    // run every layout on the same inputs); read per call, it costs a getenv.
     const char* e = getenv("SWANN_SEARCH_BLOCK");
     const int forced = e ? atoi(e) : 0;
-    if (forced == 64 || forced == 256) return forced;
-    // A batch that cannot fill 256 CUs with one-wave branches gets four
-    // waves per branch instead: more neighbours in flight per expansion.
-    return nbranch < 4096 ? 256 : 64;
+    if (forced == 64 || forced == 256 || forced == 1024) return forced;
+    // Batch work fills 256 CUs with one-wave branches.  A batch that cannot
+    // gets four waves per branch, and a grid smaller than two branches per
+    // CU (batch 1-8 at 32 branches) sixteen: an expansion's neighbours are
+    // then scored by 1024 / team teams at once instead of a few in turn, and
+    // a branch's chain of expansions -- the latency at small batch -- is
+    // shorter.
+    if (nbranch >= 4096) return 64;
+    return nbranch >= 512 ? 256 : 1024;
 }
 
 bool rows_vec_ok(const void* X, int dim, int x_dtype) {
@@ -799,8 +805,10 @@ bool rows_vec_ok(const void* X, int dim, int x_dtype) {
     do {                                                                                  \
         if ((BLK) == 64)                                                                  \
             hipLaunchKernelGGL((KERNEL<TM, T, 64>), GRID, dim3(64), LDS, ST, ARGS);       \
-        else                                                                              \
+        else if ((BLK) == 256)                                                            \
             hipLaunchKernelGGL((KERNEL<TM, T, 256>), GRID, dim3(256), LDS, ST, ARGS);     \
+        else                                                                              \
+            hipLaunchKernelGGL((KERNEL<TM, T, 1024>), GRID, dim3(1024), LDS, ST, ARGS);   \
     } while (0)
 
 #define SWANN_DISPATCH_T(KERNEL, T, TEAMV, BLK, GRID, LDS, ST, ARGS)                       \

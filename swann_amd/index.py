@@ -10,6 +10,10 @@ deliberate differences: there is no 65535-query cap (the kernels run on a
 1-D grid), and the overflow check no longer costs its own host
 synchronisation: it is computed on the device with the search and read after
 the results' own copy back.
+
+For small batches, where launch overhead is a large part of the latency,
+`Index.capture(batch)` records the whole search once as a HIP graph and
+replays it (`CapturedSearch`).
 """
 from __future__ import annotations
 
@@ -93,6 +97,12 @@ class Index:
                 raise TypeError(f"unknown search option {key!r}")
             setattr(cfg, key, value)
         Q = _as_cuda(queries).float().contiguous()
+        return self._search_device(Q, k, cfg)
+
+    def _search_device(self, Q: torch.Tensor, k: int, cfg: SearchConfig):
+        """select -> seeds -> init -> advance -> top-k -> merge -> overflow,
+        all stream-ordered device work with no host synchronisation (so it can
+        be captured)."""
         entries = S.select_nearest(Q, self._cat, cfg.branches, metric=self._m)
         seeds = self.catalogue[entries].to(torch.int32)
         ids, dist, st = E.search(
@@ -100,6 +110,17 @@ class Index:
             team_size=cfg.team, stop_eps=cfg.stop_eps, shared_cache=True, shared_bound=True,
             exclusive=True, elide_visited=True, check=False)
         return ids, dist, st, st.overflow()
+
+    def capture(self, batch: int, k: int = 10, config: SearchConfig | None = None,
+                **overrides) -> "CapturedSearch":
+        """A search of exactly `batch` queries recorded as one HIP graph; see
+        `CapturedSearch`.  The knobs are fixed at capture time."""
+        cfg = config or SearchConfig(k=k)
+        for key, value in overrides.items():
+            if not hasattr(cfg, key):
+                raise TypeError(f"unknown search option {key!r}")
+            setattr(cfg, key, value)
+        return CapturedSearch(self, int(batch), k, cfg)
 
     def search(self, queries, k: int = 10, config: SearchConfig | None = None, **overrides):
         """Return (ids, distances), each (nq, k), as numpy arrays
@@ -146,3 +167,50 @@ def _as_cuda(a) -> torch.Tensor:
     if a.device.type != "cuda":
         a = a.cuda()
     return a.contiguous()
+
+
+class CapturedSearch:
+    """One search of a fixed batch size, recorded once as a HIP graph
+    (`torch.cuda.CUDAGraph`) and replayed.
+
+    Every kernel of the search (selection GEMM and top-k, seed gather, branch
+    init, advance, per-branch top-k, merge, overflow count) is one node; the
+    state, table, workspace and outputs live in the graph's private memory
+    pool and are reused by every replay.  The overflow guard is not applied:
+    `overflow` is a device scalar the caller may read when it likes.  Nothing
+    in the captured work clears memory with a memset node; every clear is a
+    kernel.
+
+        cs = index.capture(8, k=10, branches=32)
+        ids, dist = cs.run(Q8)          # device tensors, valid until the next run
+    """
+
+    def __init__(self, index: Index, batch: int, k: int, cfg: SearchConfig, warmup: int = 2):
+        if batch < 1:
+            raise ValueError("batch must be >= 1")
+        dev = index.X.device
+        self.index, self.batch, self.k, self.cfg = index, batch, k, cfg
+        self.queries = torch.zeros((batch, index.X.shape[1]), dtype=torch.float32, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                index._search_device(self.queries, k, cfg)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.ids, self.dist, self.state, self.overflow = index._search_device(
+                self.queries, k, cfg)
+
+    def run(self, queries) -> tuple[torch.Tensor, torch.Tensor]:
+        """Copy `queries` (batch x d) into the graph's input and replay it on
+        the current stream.  Returns the graph's (ids, dist) device tensors,
+        overwritten by the next run."""
+        q = _as_cuda(queries)
+        if q.shape != self.queries.shape:
+            raise ValueError(f"captured for queries of shape {tuple(self.queries.shape)}, "
+                             f"got {tuple(q.shape)}")
+        self.queries.copy_(q, non_blocking=True)
+        self.graph.replay()
+        return self.ids, self.dist

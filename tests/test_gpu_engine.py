@@ -36,7 +36,7 @@ def toy(n=2000, d=64, deg=32, seed=0, metric=0):
     return X, knn_graph(X, deg, metric)
 
 
-@pytest.fixture(params=["64", "256"], autouse=False)
+@pytest.fixture(params=["64", "256", "1024"], autouse=False)
 def block(request, monkeypatch):
     monkeypatch.setenv("SWANN_SEARCH_BLOCK", request.param)
     return int(request.param)

@@ -199,3 +199,101 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     # self is never a candidate, rows are ascending
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
     assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
+
+
+def test_captured_search_replays_exactly():
+    """The whole search path under hipGraph capture (selection, seed gather,
+    init, advance, top-k, merge, overflow count), in a deterministic
+    configuration (no shared table, bound or claims): recorded once, replayed
+    with four different batches, with eager work and synchronisations between
+    the replays; every replay equals the eager search bit for bit."""
+    from swann_amd import _engine as E
+    X, Q = corpus(n=4000, d=64, nq=64, seed=4)
+    Xg = torch.from_numpy(X).cuda()
+    index = swann.Index.build(Xg, degree=32, candidates=48)
+
+    def run(Qb):
+        ent = S.select_nearest(Qb, index._cat, 8, metric=0)
+        seeds = index.catalogue[ent].to(torch.int32)
+        ids, dist, st = E.search(index.X, index.G, Qb, seeds, k=10, L=16, B=24, metric=0,
+                                 team_size=16, stop_eps=0.1, check=False)
+        return ids, dist, st.overflow()
+
+    static_q = torch.zeros((8, 64), device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(static_q)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi, gd, go = run(static_q)
+    Qg = torch.from_numpy(Q).cuda()
+    for rep in range(4):
+        note("capture replay", rep)
+        Qb = Qg[rep * 8:(rep + 1) * 8].contiguous()
+        ei, ed, eo = run(Qb)                       # eager, on the same stream
+        torch.cuda.synchronize()
+        static_q.copy_(Qb)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gi, ei) and torch.equal(gd.view(torch.int32), ed.view(torch.int32))
+        assert int(go) == int(eo) == 0
+        _ = (Qg @ Qg.T).sum().item()               # unrelated eager work between replays
+
+
+def test_index_capture_matches_eager_search():
+    """`Index.capture`: the production configuration (shared table, bound,
+    claims -- racy by design) replayed on several batches agrees with the
+    eager search, and its distances are exact."""
+    X, Q = corpus(n=6000, d=96, nq=64, seed=5)
+    index = swann.Index.build(X, degree=32, candidates=48)
+    cs = index.capture(16, k=10, branches=16, queue=16)
+    Xd = X.astype(np.float64)
+    truth = exact_topk(X, Q, 10)
+    agree, rg, re = [], [], []
+    for rep in range(4):
+        sl = slice(rep * 16, (rep + 1) * 16)
+        ei, _ = index.search(Q[sl], k=10, branches=16, queue=16)
+        gi, gd = cs.run(Q[sl])
+        torch.cuda.synchronize()
+        gi, gd = gi.cpu().numpy(), gd.cpu().numpy()
+        agree.append(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(gi, ei)]))
+        rg.append(recall(gi, truth[sl], 10)); re.append(recall(ei, truth[sl], 10))
+        assert int(cs.overflow) == 0
+        for qi in range(16):
+            for i, dv in zip(gi[qi], gd[qi]):
+                if i >= 0:
+                    assert abs(dv - (1.0 - Q[rep * 16 + qi].astype(np.float64) @ Xd[i])) < 1e-5
+    note("capture set agreement / recall graph / recall eager", agree, np.mean(rg), np.mean(re))
+    assert np.mean(agree) > 0.95
+    assert abs(np.mean(rg) - np.mean(re)) < 0.03
+    with pytest.raises(ValueError):
+        cs.run(Q[:3])
+
+
+@pytest.mark.parametrize("nq", [1, 3, 8, 64, 300])
+@pytest.mark.parametrize("metric", [0, 1])
+def test_select_small_and_large_batches_match_oracle(nq, metric):
+    """Selection at every batch shape: split-K partials for small grids, the
+    radix top-E for rows up to 16384 and the chunked bitonic beyond; ties
+    (duplicated catalogue rows) resolve to the lower index, as the oracle's
+    (d, index) order."""
+    rng = np.random.default_rng(100 + nq)
+    for P, d, E in ((4096, 256, 32), (5000, 72, 128), (20000, 64, 40)):
+        V = rng.standard_normal((P, d)).astype(np.float32)
+        V[P // 2:P // 2 + 50] = V[:50]                     # exact duplicates -> ties
+        Q = rng.standard_normal((nq, d)).astype(np.float32)
+        Q[0] = V[7]
+        idx = S.select_nearest(torch.from_numpy(Q).cuda(), torch.from_numpy(V).cuda(), E,
+                               metric=metric).cpu().numpy()
+        want, _ = O.select_nearest(Q, V, E, metric, nthreads=8)
+        note("select", nq, metric, P, d, E, (idx == want).mean())
+        assert idx.shape == (nq, E)
+        assert (idx == want).mean() > 0.995
+        assert (np.sort(idx, 1)[:, 1:] != np.sort(idx, 1)[:, :-1]).all()   # distinct
+        if metric == 1:
+            # q = V[7], which has an exact duplicate at P//2 + 7: a tie at the
+            # top, resolved to the lower index
+            assert idx[0, 0] == 7 and idx[0, 1] == P // 2 + 7
