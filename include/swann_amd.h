@@ -162,20 +162,25 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
                       int32_t* cand, float* cdist, void* workspace, void* stream);
 
 /* Prune (build.py:46-91): keep candidate i of node u unless an already kept
- * w satisfies alpha * d(w, i) <= d(u, i); deg kept ids per row, -1 padded.
- * C <= 128. */
+ * w satisfies alpha * d(w, i) <= d(u, i); rows of `deg` ids, -1 padded.
+ * C <= 128, deg <= 128.  deg_per_node [n] (or NULL) caps node u at
+ * min(deg_per_node[u], deg) kept; protect [n, C] bytes (or NULL): a nonzero
+ * entry exempts that candidate from the detour test (build.py:78-81). */
 int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
                       const int32_t* cand, const float* cdist, int C, int deg, float alpha,
-                      int32_t* out, void* stream);
+                      const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
+                      void* stream);
 
 /* Reverse (build.py:94-150): offer every edge u->v back to v (ascending
  * source, at most max_in per target), dedup [G_u | in_u] minus self, score
- * exactly, keep the nearest 128 and prune to deg.
+ * exactly, keep the nearest 128 and prune to deg (G and out have deg
+ * columns; deg_per_node caps the prune per node as in swann_build_prune).
  * `workspace`: swann_reverse_workspace_size bytes. */
 int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in);
 int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metric,
-                        const int32_t* G, int deg, float alpha, int max_in, int32_t* out,
-                        void* workspace, void* stream);
+                        const int32_t* G, int deg, float alpha, int max_in,
+                        const int32_t* deg_per_node, int32_t* out, void* workspace,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -84,9 +84,9 @@ def _declare(L):
     L.so_topk_rows.restype = None
     L.so_topk_rows.argtypes = [P, I64, P, I64, I, I, I, I64, P, P, I]
     L.so_robust_prune.restype = None
-    L.so_robust_prune.argtypes = [P, I64, I, I, P, P, I, I, F, P, I]
+    L.so_robust_prune.argtypes = [P, I64, I, I, P, P, I, I, F, P, P, P, I]
     L.so_add_reverse.restype = None
-    L.so_add_reverse.argtypes = [P, I64, I, I, P, I, F, I, P, I]
+    L.so_add_reverse.argtypes = [P, I64, I, I, P, I, F, I, P, P, I]
     L.so_code_sums.restype = None
     L.so_code_sums.argtypes = [P, P, I, P, P]
     L.so_code_ip.restype = F
@@ -333,24 +333,36 @@ def knn_candidates(X, C, metric=METRIC_IP, nthreads=0):
     return topk_rows(X, X, C, metric, 0, nthreads)
 
 
-def robust_prune(X, cand, cdist, deg, alpha=1.2, metric=METRIC_IP, nthreads=0):
-    """build.py:46-91"""
+def robust_prune(X, cand, cdist, deg, alpha=1.2, metric=METRIC_IP, nthreads=0,
+                 deg_per_node=None, protect=None):
+    """build.py:46-91.  With `deg_per_node` the row width is its maximum and
+    node u keeps at most deg_per_node[u]; `protect` [n, C] bool exempts a
+    candidate from the detour test."""
     X = np.ascontiguousarray(X, dtype=np.float32)
     cand = np.ascontiguousarray(cand, dtype=np.int32)
     cdist = np.ascontiguousarray(cdist, dtype=np.float32)
-    out = np.empty((X.shape[0], deg), np.int32)
+    dpn = None if deg_per_node is None else np.ascontiguousarray(deg_per_node, dtype=np.int32)
+    width = int(deg) if dpn is None else int(dpn.max())
+    prot = None if protect is None else np.ascontiguousarray(protect, dtype=np.uint8)
+    out = np.empty((X.shape[0], width), np.int32)
     lib().so_robust_prune(_p(X), X.shape[0], X.shape[1], int(metric), _p(cand), _p(cdist),
-                          cand.shape[1], int(deg), float(alpha), _p(out), int(nthreads))
+                          cand.shape[1], width, float(alpha), _p(dpn), _p(prot), _p(out),
+                          int(nthreads))
     return out
 
 
-def add_reverse(X, G, deg, alpha=1.2, max_in=64, metric=METRIC_IP, nthreads=0):
-    """build.py:94-150"""
+def add_reverse(X, G, deg, alpha=1.2, max_in=64, metric=METRIC_IP, nthreads=0,
+                deg_per_node=None):
+    """build.py:94-150; with `deg_per_node` the width is its maximum (G must
+    have that many columns) and node u keeps at most deg_per_node[u]."""
     X = np.ascontiguousarray(X, dtype=np.float32)
     G = np.ascontiguousarray(G, dtype=np.int32)
-    out = np.empty((X.shape[0], deg), np.int32)
-    lib().so_add_reverse(_p(X), X.shape[0], X.shape[1], int(metric), _p(G), int(deg),
-                         float(alpha), int(max_in), _p(out), int(nthreads))
+    dpn = None if deg_per_node is None else np.ascontiguousarray(deg_per_node, dtype=np.int32)
+    width = int(deg) if dpn is None else int(dpn.max())
+    assert G.shape[1] == width
+    out = np.empty((X.shape[0], width), np.int32)
+    lib().so_add_reverse(_p(X), X.shape[0], X.shape[1], int(metric), _p(G), width,
+                         float(alpha), int(max_in), _p(dpn), _p(out), int(nthreads))
     return out
 
 

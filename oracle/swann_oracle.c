@@ -695,30 +695,39 @@ void so_topk_rows(const float* Xr, int64_t nr, const float* Y, int64_t ny, int d
 }
 
 /* Sequential alpha rule over one node's ascending candidate list,
- * build.py:46-91.  cand/cd: C entries; writes deg ids (-1 padded). */
+ * build.py:46-91.  cand/cd: C entries; at most `cap` kept; a candidate whose
+ * `protect` flag is set survives the detour test (build.py:80-81); writes
+ * `width` ids (-1 padded). */
 static void so_prune_row(const float* X, int dim, int metric, const int32_t* cand,
-                         const float* cd, int C, int deg, float alpha, int32_t* out,
-                         float* vn_scratch, int* kept_scratch) {
+                         const float* cd, int C, int cap, int width, float alpha,
+                         const uint8_t* protect, int32_t* out, float* vn_scratch,
+                         int* kept_scratch) {
     int nk = 0;
     for (int i = 0; i < C; ++i) {
         const int ci = cand[i];
-        if (nk >= deg) break;
+        if (nk >= cap) break;
         if (ci < 0) continue;
         int viol = 0;
-        for (int t = 0; t < nk && !viol; ++t) {
-            const int w = kept_scratch[t];
-            const int cw = cand[w];
-            const float dot = (float)so_dot_d(X + (int64_t)cw * dim, X + (int64_t)ci * dim, dim);
-            const float pr = so_pair_dist(dot, vn_scratch[w], vn_scratch[i], metric);
-            if (alpha * pr <= cd[i]) viol = 1;
+        if (!(protect && protect[i])) {
+            for (int t = 0; t < nk && !viol; ++t) {
+                const int w = kept_scratch[t];
+                const int cw = cand[w];
+                const float dot = (float)so_dot_d(X + (int64_t)cw * dim, X + (int64_t)ci * dim, dim);
+                const float pr = so_pair_dist(dot, vn_scratch[w], vn_scratch[i], metric);
+                if (alpha * pr <= cd[i]) viol = 1;
+            }
         }
         if (!viol) kept_scratch[nk++] = i;
     }
-    for (int t = 0; t < deg; ++t) out[t] = t < nk ? cand[kept_scratch[t]] : -1;
+    for (int t = 0; t < width; ++t) out[t] = t < nk ? cand[kept_scratch[t]] : -1;
 }
 
+/* deg: the row width (and every node's cap when deg_per_node is NULL);
+ * deg_per_node [n] caps node u at min(deg_per_node[u], deg); protect [n, C]
+ * (0/1 bytes) or NULL. */
 void so_robust_prune(const float* X, int64_t n, int dim, int metric, const int32_t* cand,
-                     const float* cdist, int C, int deg, float alpha, int32_t* out,
+                     const float* cdist, int C, int deg, float alpha,
+                     const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
                      int nthreads) {
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -736,7 +745,10 @@ void so_robust_prune(const float* X, int64_t n, int dim, int metric, const int32
                 const int ci = cr[i] >= 0 ? cr[i] : 0;
                 vn[i] = (float)so_dot_d(X + (int64_t)ci * dim, X + (int64_t)ci * dim, dim);
             }
-            so_prune_row(X, dim, metric, cr, cdist + u * C, C, deg, alpha, out + u * deg, vn, kept);
+            int cap = deg;
+            if (deg_per_node && deg_per_node[u] < cap) cap = deg_per_node[u];
+            so_prune_row(X, dim, metric, cr, cdist + u * C, C, cap, deg, alpha,
+                         protect ? protect + u * C : NULL, out + u * deg, vn, kept);
         }
         free(vn); free(kept);
     }
@@ -752,7 +764,8 @@ static int so_i32_cmp(const void* a, const void* b) {
  * [G_u | in_u] minus self, deduped, scored exactly (1 - <v,u> or the
  * direct sum of squares), sorted ascending, cut to 128, then pruned. */
 void so_add_reverse(const float* X, int64_t n, int dim, int metric, const int32_t* G,
-                    int deg, float alpha, int max_in, int32_t* out, int nthreads) {
+                    int deg, float alpha, int max_in, const int32_t* deg_per_node,
+                    int32_t* out, int nthreads) {
     int32_t* cnt = (int32_t*)calloc((size_t)n, sizeof(int32_t));
     int32_t* in = (int32_t*)malloc(sizeof(int32_t) * (size_t)n * max_in);
     for (int64_t i = 0; i < n * max_in; ++i) in[i] = -1;
@@ -809,7 +822,10 @@ void so_add_reverse(const float* X, int64_t n, int dim, int metric, const int32_
                 cand[t] = sc[t].id; cd[t] = sc[t].d;
                 vn[t] = (float)so_dot_d(X + (int64_t)cand[t] * dim, X + (int64_t)cand[t] * dim, dim);
             }
-            so_prune_row(X, dim, metric, cand, cd, keepn, deg, alpha, out + u * deg, vn, kept);
+            int cap = deg;
+            if (deg_per_node && deg_per_node[u] < cap) cap = deg_per_node[u];
+            so_prune_row(X, dim, metric, cand, cd, keepn, cap, deg, alpha, NULL, out + u * deg,
+                         vn, kept);
         }
         free(row); free(sc); free(cand); free(cd); free(vn); free(kept);
     }

@@ -38,9 +38,9 @@ PROTOTYPES = {
     "swann_select_nearest": (I, [P, I64, I, P, I64, I, I, P, P, P, P]),
     "swann_sweep_workspace_size": (I64, [I64, I, I, I]),
     "swann_build_sweep": (I, [P, I, I64, I, I, I, P, P, P, P]),
-    "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P]),
+    "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P]),
     "swann_reverse_workspace_size": (I64, [I64, I, I]),
-    "swann_build_reverse": (I, [P, I, I64, I, I, P, I, F, I, P, P, P]),
+    "swann_build_reverse": (I, [P, I, I64, I, I, P, I, F, I, P, P, P, P]),
     "swann_codes_workspace_size": (I64, [I64, I]),
     "swann_build_codes": (I, [P, I, I64, I, P, P, P, P, P, P]),
 }

@@ -68,41 +68,57 @@ def knn_candidates(Xg, C, chunk=4096, metric="ip"):
 def robust_prune(Xg, cand, cdist, deg, alpha=1.2, chunk=4096, deg_per_node=None, metric="ip",
                  protect=None):
     """Keep a candidate only when no nearer kept neighbour detours to it
-    (swann/build.py:46-91).  Returns int32 [n, deg], -1 padded."""
+    (swann/build.py:46-91).  Returns int32 [n, width], -1 padded, where width
+    is `deg`, or max(deg_per_node) when per-node degrees are given (node u then
+    keeps at most deg_per_node[u]).  `protect` [n, C] bool exempts a
+    candidate from the detour test (a mutual pair survives it)."""
     del chunk
-    if deg_per_node is not None or protect is not None:
-        raise NotImplementedError("per-node degrees and mutual protection are offline-builder "
-                                  "extras not built in swann_amd")
     Xg = _rows(Xg)
     cand = cand.to(device=Xg.device, dtype=torch.int32).contiguous()
     cdist = cdist.to(device=Xg.device, dtype=torch.float32).contiguous()
     n, C = cand.shape
-    out = torch.empty((n, deg), dtype=torch.int32, device=Xg.device)
+    width = int(deg)
+    dpn = None
+    if deg_per_node is not None:
+        dpn = deg_per_node.to(device=Xg.device, dtype=torch.int32).contiguous()
+        if dpn.shape != (n,):
+            raise ValueError("deg_per_node must have one entry per node")
+        width = int(dpn.max())
+    prot = None
+    if protect is not None:
+        prot = protect.to(device=Xg.device, dtype=torch.bool).contiguous()
+        if prot.shape != (n, C):
+            raise ValueError("protect must be [n, C] like the candidates")
+    out = torch.empty((n, width), dtype=torch.int32, device=Xg.device)
     with torch.cuda.device(Xg.device):
         call("swann_build_prune", ptr(Xg), _DT[Xg.dtype], n, Xg.shape[1], _m(metric), ptr(cand),
-             ptr(cdist), int(C), int(deg), float(alpha), ptr(out), stream_of(Xg.device))
+             ptr(cdist), int(C), width, float(alpha), ptr(dpn), ptr(prot), ptr(out),
+             stream_of(Xg.device))
     return out
 
 
 @torch.no_grad()
 def add_reverse(Xg, G, deg, chunk=2048, alpha=1.2, max_in=64, deg_per_node=None, metric="ip"):
     """Offer every edge back to its target, then re-prune the union per node
-    (swann/build.py:94-150)."""
+    (swann/build.py:94-150).  With `deg_per_node` the width is its maximum and
+    node u keeps at most deg_per_node[u]."""
     del chunk
-    if deg_per_node is not None:
-        raise NotImplementedError("per-node degrees are an offline-builder extra not built "
-                                  "in swann_amd")
     Xg = _rows(Xg)
     G = G.to(device=Xg.device, dtype=torch.int32).contiguous()
     n, d = Xg.shape
-    if G.shape[1] != deg:
-        raise ValueError(f"G has {G.shape[1]} columns, deg is {deg}")
-    out = torch.empty((n, deg), dtype=torch.int32, device=Xg.device)
-    ws = torch.empty(int(lib().swann_reverse_workspace_size(n, deg, max_in)), dtype=torch.uint8,
-                     device=Xg.device)
+    width = int(deg)
+    dpn = None
+    if deg_per_node is not None:
+        dpn = deg_per_node.to(device=Xg.device, dtype=torch.int32).contiguous()
+        width = int(dpn.max())
+    if G.shape[1] != width:
+        raise ValueError(f"G has {G.shape[1]} columns, the row width is {width}")
+    out = torch.empty((n, width), dtype=torch.int32, device=Xg.device)
+    ws = torch.empty(int(lib().swann_reverse_workspace_size(n, width, max_in)),
+                     dtype=torch.uint8, device=Xg.device)
     with torch.cuda.device(Xg.device):
-        call("swann_build_reverse", ptr(Xg), _DT[Xg.dtype], n, d, _m(metric), ptr(G), int(deg),
-             float(alpha), int(max_in), ptr(out), ptr(ws), stream_of(Xg.device))
+        call("swann_build_reverse", ptr(Xg), _DT[Xg.dtype], n, d, _m(metric), ptr(G), width,
+             float(alpha), int(max_in), ptr(dpn), ptr(out), ptr(ws), stream_of(Xg.device))
     return out
 
 

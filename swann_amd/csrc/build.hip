@@ -268,6 +268,8 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
                                                     const int32_t* __restrict__ cand,
                                                     const float* __restrict__ cdist, int C,
                                                     int deg, float alpha,
+                                                    const int32_t* __restrict__ dpn,
+                                                    const uint8_t* __restrict__ protect,
                                                     int32_t* __restrict__ out) {
     __shared__ float gram[kPruneMaxC * (kPruneMaxC - 1) / 2];
     __shared__ float vn[kPruneMaxC];
@@ -326,16 +328,22 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
     __syncthreads();
     // The sequential rule, one wave.  Every decision is wave-uniform, so the
     // kept list lives in registers: lane t holds kept[t] and kept[64 + t].
+    // Node u keeps at most min(dpn[u], deg); a protected candidate skips the
+    // detour test (build.py:78-81).
     if (tid < 64) {
         const int lane = tid;
         int k0 = -1, k1 = -1;
         int nk = 0;
-        for (int i = 0; i < C && nk < deg; ++i) {
+        int cap = deg;
+        if (dpn) { const int c = dpn[u]; cap = c < cap ? c : cap; }
+        for (int i = 0; i < C && nk < cap; ++i) {
             if (cid[i] < 0) continue;
             const float du = cdu[i];
             bool v = false;
-            if (lane < nk) v = alpha * pair_formula(gram[tri(k0, i)], vn[k0], vn[i], metric) <= du;
-            if (64 + lane < nk)
+            const bool prot = protect && protect[u * C + i];
+            if (!prot && lane < nk)
+                v = alpha * pair_formula(gram[tri(k0, i)], vn[k0], vn[i], metric) <= du;
+            if (!prot && 64 + lane < nk)
                 v = v || alpha * pair_formula(gram[tri(k1, i)], vn[k1], vn[i], metric) <= du;
             if (__ballot(v) == 0ull) {
                 if (nk < 64) { if (lane == nk) k0 = i; }
@@ -691,7 +699,8 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
 
 int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
                       const int32_t* cand, const float* cdist, int C, int deg, float alpha,
-                      int32_t* out, void* stream) {
+                      const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
+                      void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
@@ -699,15 +708,17 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
                   "X: float32 or float16");
     SWANN_REQUIRE(C >= 1 && C <= kPruneMaxC, "prune: candidates per node must be in 1..%d",
                   kPruneMaxC);
-    SWANN_REQUIRE(deg >= 1 && deg <= C, "prune: degree must be in 1..C");
+    SWANN_REQUIRE(deg >= 1 && deg <= kPruneMaxC, "prune: degree must be in 1..%d", kPruneMaxC);
     SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
     SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
     SWANN_BY_DTYPE(x_dtype,
         hipLaunchKernelGGL(prune_kernel<float>, dim3((unsigned)n), dim3(256), 0, st,
-                           (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha, out),
+                           (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                           deg_per_node, protect, out),
         hipLaunchKernelGGL(prune_kernel<_Float16>, dim3((unsigned)n), dim3(256), 0, st,
-                           (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha, out));
+                           (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                           deg_per_node, protect, out));
     return launch_status("prune");
 }
 
@@ -718,8 +729,9 @@ int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in) {
 }
 
 int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metric,
-                        const int32_t* G, int deg, float alpha, int max_in, int32_t* out,
-                        void* workspace, void* stream) {
+                        const int32_t* G, int deg, float alpha, int max_in,
+                        const int32_t* deg_per_node, int32_t* out, void* workspace,
+                        void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
@@ -758,8 +770,8 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
                            keepn, cand2, cd2));
     rc = launch_status("reverse assemble");
     if (rc) return rc;
-    return swann_build_prune(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha, out,
-                             stream);
+    return swann_build_prune(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha,
+                             deg_per_node, nullptr, out, stream);
 }
 
 }  // extern "C"

@@ -10,7 +10,11 @@ What is imported from the reference, and why nothing else pins it:
     retirement, the eps stop rule and the merge -- whose trajectories no closed
     form fixes; plus fp16 distances with vec=8.
   * swann/build.py on CPU tensors: knn_candidates / robust_prune / add_reverse,
-    whose torch.topk / argsort tie behaviour only the code itself defines.
+    whose torch.topk / argsort tie behaviour only the code itself defines,
+    including robust_prune's per-node degrees and protect mask.
+  * offline/build_graph.py on CPU tensors: candidates_from_graph,
+    mutual_rank, fill_degree and enforce_min_in (the offline builder's
+    extras), whose selection orders only the code defines.
   * swann/_select.py select_nearest (fp32, CPU) and
     swann/_engine.py _merge_branches_tensor: the C1 seeds and merged answers.
 
@@ -42,6 +46,10 @@ def _load(name, path, package=None):
     sys.modules[name] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+def ref_offline():
+    return _load("ref_offline_build", REF / "offline" / "build_graph.py")
 
 
 def ref_modules():
@@ -195,6 +203,46 @@ def _c1_run(args):
     return q, j, pack_queue(st, 12)
 
 
+def make_build_extras(build, offline):
+    """Per-node degrees, the protect mask and the offline extras on CPU
+    tensors (build.py:46-150, offline/build_graph.py:72-386), n = 800."""
+    import contextlib
+    import io
+    import torch
+    out = {}
+    for tag, metric in (("ip", "ip"), ("l2", "l2")):
+        X = gaussian(800, 24, 23 if tag == "ip" else 24, tag == "ip")
+        Xt = torch.from_numpy(X)
+        cand, cdist = build.knn_candidates(Xt, 32, metric=metric)
+        rng = np.random.default_rng(5)
+        dpn = torch.from_numpy(np.where(rng.random(800) < 0.1, 20, 12).astype(np.int32))
+        prot = offline.mutual_rank(cand, 8)
+        Gp = build.robust_prune(Xt, cand, cdist, 12, alpha=1.2, metric=metric)
+        Gd = build.robust_prune(Xt, cand, cdist, 12, alpha=1.2, deg_per_node=dpn, metric=metric)
+        Gm = build.robust_prune(Xt, cand, cdist, 12, alpha=1.2, metric=metric, protect=prot)
+        Gb = build.robust_prune(Xt, cand, cdist, 12, alpha=1.2, deg_per_node=dpn,
+                                metric=metric, protect=prot)
+        Rd = build.add_reverse(Xt, Gd, 12, alpha=1.2, deg_per_node=dpn, metric=metric)
+        R = build.add_reverse(Xt, Gp, 12, alpha=1.2, metric=metric)
+        cg, cgd = offline.candidates_from_graph(Xt, R, 12, metric=metric)
+        fills = {rule: offline.fill_degree(Gp, cand, rule=rule).numpy().astype(np.int16)
+                 for rule in ("near", "far", "bridge")}
+        with contextlib.redirect_stdout(io.StringIO()):
+            Gmin = offline.enforce_min_in(Xt, R.clone(), cand, 8, metric=metric, rounds=4)
+        out.update({f"{tag}_X_sha": np.array(sha(X)), f"{tag}_cand": cand.numpy().astype(np.int16),
+                    f"{tag}_cdist": cdist.numpy(), f"{tag}_dpn": dpn.numpy().astype(np.int16),
+                    f"{tag}_prot": prot.numpy(), f"{tag}_Gp": Gp.numpy().astype(np.int16),
+                    f"{tag}_Gd": Gd.numpy().astype(np.int16), f"{tag}_Gm": Gm.numpy().astype(np.int16),
+                    f"{tag}_Gb": Gb.numpy().astype(np.int16), f"{tag}_R": R.numpy().astype(np.int16),
+                    f"{tag}_Rd": Rd.numpy().astype(np.int16),
+                    f"{tag}_cg": cg.numpy().astype(np.int16), f"{tag}_cgd": cgd.numpy(),
+                    f"{tag}_Gmin": Gmin.numpy().astype(np.int16)})
+        for rule, g in fills.items():
+            out[f"{tag}_fill_{rule}"] = g
+    np.savez_compressed(OUT / "refbuild_extras.npz", **out)
+    print("refbuild_extras.npz written")
+
+
 def make_c1(refcpu, build, select, engine):
     """10k x 128 fp32 IP, D=32 cand=64 alpha=1.2, 200
     queries, 8 branches each searched independently by _refcpu (claims off),
@@ -233,8 +281,10 @@ def make_c1(refcpu, build, select, engine):
           float(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(mi.numpy(), gt)])))
 
 
-def main(which=("branch", "distance", "build", "c1")):
+def main(which=("branch", "distance", "build", "extras", "c1")):
     refcpu, build, select, engine, _ = ref_modules()
+    if "extras" in which:
+        make_build_extras(build, ref_offline())
     if "distance" in which:
         make_distance(refcpu)
     if "branch" in which:

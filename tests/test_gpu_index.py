@@ -297,3 +297,35 @@ def test_select_small_and_large_batches_match_oracle(nq, metric):
             # q = V[7], which has an exact duplicate at P//2 + 7: a tie at the
             # top, resolved to the lower index
             assert idx[0, 0] == 7 and idx[0, 1] == P // 2 + 7
+
+
+@pytest.mark.parametrize("tag,metric", [("ip", 0), ("l2", 1)])
+def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
+    """robust_prune(deg_per_node=, protect=) and add_reverse(deg_per_node=)
+    against the reference's CPU-torch build.py (refbuild_extras.npz) and,
+    on identical inputs, the oracle."""
+    g = golden("refbuild_extras.npz")
+    X = regen(800, 24, 23 if tag == "ip" else 24, tag == "ip", g[f"{tag}_X_sha"])
+    m = "ip" if metric == 0 else "l2"
+    Xg = torch.from_numpy(X).cuda()
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    dpn = g[f"{tag}_dpn"].astype(np.int32); prot = g[f"{tag}_prot"]
+    rcg, rdg = torch.from_numpy(rc).cuda(), torch.from_numpy(rd).cuda()
+    dpng, protg = torch.from_numpy(dpn).cuda(), torch.from_numpy(prot).cuda()
+    for key, kw, okw in (("Gd", dict(deg_per_node=dpng), dict(deg_per_node=dpn)),
+                         ("Gm", dict(protect=protg), dict(protect=prot)),
+                         ("Gb", dict(deg_per_node=dpng, protect=protg),
+                          dict(deg_per_node=dpn, protect=prot))):
+        got = B.robust_prune(Xg, rcg, rdg, 12, alpha=1.2, metric=m, **kw).cpu().numpy()
+        want = g[f"{tag}_{key}"].astype(np.int32)
+        assert got.shape == want.shape
+        rows = (got == want).all(1).mean()
+        ora = O.robust_prune(X, rc, rd, 12, 1.2, metric, nthreads=8, **okw)
+        note("prune extras", tag, key, rows, (got == ora).all(1).mean())
+        assert rows > 0.98
+        assert (got == ora).all(1).mean() > 0.99
+    Rd = B.add_reverse(Xg, torch.from_numpy(g[f"{tag}_Gd"].astype(np.int32)).cuda(), 12,
+                       alpha=1.2, deg_per_node=dpng, metric=m).cpu().numpy()
+    same = np.mean([set(a) == set(b) for a, b in zip(Rd, g[f"{tag}_Rd"].astype(np.int32))])
+    note("reverse dpn", tag, same)
+    assert same > 0.97

@@ -350,6 +350,52 @@ def test_prune_and_reverse_match_reference(tag, metric):
     assert same_sets > 0.97, same_sets
 
 
+@pytest.mark.parametrize("tag,metric", [("ip", O.METRIC_IP), ("l2", O.METRIC_L2)])
+def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
+    """robust_prune's deg_per_node and protect, and add_reverse's
+    deg_per_node, against the reference's CPU-torch build.py on its own
+    candidate lists (tests/golden/refbuild_extras.npz)."""
+    g = golden("refbuild_extras.npz")
+    X = regen(800, 24, 23 if tag == "ip" else 24, tag == "ip", g[f"{tag}_X_sha"])
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    dpn = g[f"{tag}_dpn"].astype(np.int32); prot = g[f"{tag}_prot"]
+    for key, kw in (("Gp", {}), ("Gd", dict(deg_per_node=dpn)), ("Gm", dict(protect=prot)),
+                    ("Gb", dict(deg_per_node=dpn, protect=prot))):
+        got = O.robust_prune(X, rc, rd, 12, 1.2, metric, nthreads=4, **kw)
+        want = g[f"{tag}_{key}"].astype(np.int32)
+        assert got.shape == want.shape, key
+        rows = (got == want).all(1).mean()
+        assert rows > 0.98, (key, rows)
+    got = O.add_reverse(X, g[f"{tag}_Gd"].astype(np.int32), 12, 1.2, 64, metric, nthreads=4,
+                        deg_per_node=dpn)
+    want = g[f"{tag}_Rd"].astype(np.int32)
+    assert np.mean([set(a) == set(b) for a, b in zip(got, want)]) > 0.97
+
+
+def test_prune_caps_and_protect_closed_forms():
+    """A cap keeps a prefix of the uncapped kept list; protecting every
+    candidate keeps the first cap valid ones; protecting none is no protect."""
+    X = gaussian(600, 20, 61, False)
+    rc, rd = O.knn_candidates(X, 32, O.METRIC_L2, nthreads=4)
+    rc[::7, 5] = -1                                   # holes are never kept
+    full = O.robust_prune(X, rc, rd, 32, 1.2, O.METRIC_L2, nthreads=4)
+    caps = np.random.default_rng(3).integers(1, 20, 600).astype(np.int32)
+    capped = O.robust_prune(X, rc, rd, 20, 1.2, O.METRIC_L2, nthreads=4, deg_per_node=caps)
+    assert capped.shape == (600, int(caps.max()))
+    for u in range(600):
+        k = min(caps[u], int((full[u] >= 0).sum()))
+        assert list(capped[u, :k]) == list(full[u, :k])
+        assert (capped[u, k:] == -1).all()
+    allp = O.robust_prune(X, rc, rd, 12, 1.2, O.METRIC_L2, nthreads=4,
+                          protect=np.ones(rc.shape, bool))
+    for u in range(600):
+        valid = [c for c in rc[u] if c >= 0][:12]
+        assert list(allp[u, :len(valid)]) == valid
+    nonep = O.robust_prune(X, rc, rd, 12, 1.2, O.METRIC_L2, nthreads=4,
+                           protect=np.zeros(rc.shape, bool))
+    assert np.array_equal(nonep, O.robust_prune(X, rc, rd, 12, 1.2, O.METRIC_L2, nthreads=4))
+
+
 def test_prune_rule_invariants():
     """DiskANN's rule, stated as invariants: every kept edge has no kept,
     nearer neighbour that is alpha-closer to it; every dropped candidate
