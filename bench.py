@@ -59,7 +59,7 @@ HBM_PEAK = 8.0e12
 # was measured on (SHA-256 prefix of swann_amd/csrc/search.hip) and the same
 # workload and knobs; otherwise `traffic` is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "032ba46d1ea7e189"): 5.620e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "6d609080657bb8e5"): 5.620e12,
 }
 
 

@@ -262,7 +262,68 @@ constexpr int kPKC = 16;
 
 __device__ __forceinline__ int tri(int w, int i) { return i * (i - 1) / 2 + w; }   // w < i
 
-template <typename XT>
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+
+// The Gram of a node's candidates on MFMA (fp16 rows: products exact, sums
+// in fp32).  Wave w owns candidate rows [32w, 32w + 32) and the 32x32 tiles
+// j >= w of the upper triangle; fragments come straight from the rows in
+// HBM/L2 as 16-byte loads (A: row l%32, halves (l/32)*8..+7 of each 16-wide
+// K step; B likewise), four K steps in flight.  Output tile element e of lane
+// l is <row (e/4)*8 + (l/32)*4 + e%4 of the strip, row l%32 of tile j>.
+__device__ void gram_mfma(const _Float16* __restrict__ X, int64_t n, int dim, const int* cid,
+                          int C, float* gram, float* vn) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (w * 32 >= C) return;
+    const int half = (lane >> 5) * 8;
+    auto rowp = [&](int i) -> const _Float16* {
+        const int c = (i < C) ? cid[i] : -1;
+        return (c >= 0 && c < n) ? X + (int64_t)c * dim + half : nullptr;
+    };
+    const _Float16* pa = rowp(w * 32 + (lane & 31));
+    const _Float16* pb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pb[j] = (j >= w) ? rowp(j * 32 + (lane & 31)) : nullptr;
+    f32x16v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+    const h16x8 z = {};
+    constexpr int kU = 4;
+    for (int k0 = 0; k0 < dim; k0 += 16 * kU) {
+        h16x8 a[kU], b[kU][4];
+#pragma unroll
+        for (int s = 0; s < kU; ++s) {
+            const int k = k0 + s * 16;
+            const bool kin = k < dim;
+            a[s] = (pa && kin) ? *reinterpret_cast<const h16x8*>(pa + k) : z;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                b[s][j] = (j >= w && pb[j] && kin) ? *reinterpret_cast<const h16x8*>(pb[j] + k) : z;
+        }
+#pragma unroll
+        for (int s = 0; s < kU; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j >= w) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s], b[s][j], acc[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < w) continue;
+        const int cc = j * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            if (r < C && cc < C) {
+                if (r < cc) gram[tri(r, cc)] = acc[j][e];
+                else if (r == cc) vn[r] = acc[j][e];
+            }
+        }
+    }
+}
+
+template <typename XT, bool MFMA>
 __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
                                                     const int32_t* __restrict__ cand,
@@ -273,7 +334,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
                                                     int32_t* __restrict__ out) {
     __shared__ float gram[kPruneMaxC * (kPruneMaxC - 1) / 2];
     __shared__ float vn[kPruneMaxC];
-    __shared__ float Vs[kPKC][kPruneMaxC + 4];
+    __shared__ float Vs[MFMA ? 1 : kPKC][kPruneMaxC + 4];
     __shared__ int cid[kPruneMaxC];
     __shared__ float cdu[kPruneMaxC];
     const int64_t u = blockIdx.x;
@@ -284,6 +345,9 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
         cdu[i] = cdist[u * C + i];
     }
     __syncthreads();
+    if constexpr (MFMA) {
+        gram_mfma(reinterpret_cast<const _Float16*>(X), n, dim, cid, C, gram, vn);
+    } else {
     // thread (ty, tx) accumulates Gram rows ty*8.., columns tx*8.. (C <= 128)
     float acc[8][8] = {};
     const bool active = (ty * 8 < C) && (tx * 8 < C) && (tx >= ty);
@@ -324,6 +388,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
                 }
             }
         }
+    }
     }
     __syncthreads();
     // The sequential rule, one wave.  Every decision is wave-uniform, so the
@@ -712,13 +777,21 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
     SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
     SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
-    SWANN_BY_DTYPE(x_dtype,
-        hipLaunchKernelGGL(prune_kernel<float>, dim3((unsigned)n), dim3(256), 0, st,
-                           (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                           deg_per_node, protect, out),
-        hipLaunchKernelGGL(prune_kernel<_Float16>, dim3((unsigned)n), dim3(256), 0, st,
+    // fp16 rows with 16-byte aligned 16-wide K steps: the Gram on MFMA
+    const bool mfma = x_dtype == SWANN_DTYPE_F16 && dim % 16 == 0 && (uintptr_t)X % 16 == 0 &&
+                      !getenv_flag("SWANN_PRUNE_SIMT");
+    if (mfma)
+        hipLaunchKernelGGL((prune_kernel<_Float16, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                           deg_per_node, protect, out));
+                           deg_per_node, protect, out);
+    else
+        SWANN_BY_DTYPE(x_dtype,
+            hipLaunchKernelGGL((prune_kernel<float, false>), dim3((unsigned)n), dim3(256), 0, st,
+                               (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                               deg_per_node, protect, out),
+            hipLaunchKernelGGL((prune_kernel<_Float16, false>), dim3((unsigned)n), dim3(256), 0,
+                               st, (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                               deg_per_node, protect, out));
     return launch_status("prune");
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <stdio.h>
 
 #include "swann_amd.h"
@@ -37,6 +38,13 @@ inline int launch_status(const char* what) {
 }
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// A test hook: true when the environment variable is set to a non-zero value
+// (used to run an alternative code path on the same inputs).
+inline bool getenv_flag(const char* name) {
+    const char* e = getenv(name);
+    return e && *e && *e != '0';
+}
 
 inline int pow2_at_least(int x, int lo, int cap) {
     int n = lo;

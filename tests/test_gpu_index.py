@@ -329,3 +329,31 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
     same = np.mean([set(a) == set(b) for a, b in zip(Rd, g[f"{tag}_Rd"].astype(np.int32))])
     note("reverse dpn", tag, same)
     assert same > 0.97
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_prune_mfma_gram_matches_simt_and_oracle(metric, monkeypatch):
+    """fp16 corpora prune on an MFMA Gram (exact products, fp32 sums); the
+    fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle (double dots) on the
+    same inputs keep the same rows up to near-ties.  d = 80 leaves a ragged
+    last K group; per-node caps and protect ride along."""
+    X = gaussian(3000, 80, 71 + metric, metric == 0)
+    if metric == 1:
+        X = X * 2.0 + 0.5
+    X16 = X.astype(np.float16)
+    m = "ip" if metric == 0 else "l2"
+    Xg = torch.from_numpy(X16).cuda()
+    cand, cdist = B.knn_candidates(Xg, 48, metric=m)
+    rng = np.random.default_rng(8)
+    dpn = np.where(rng.random(3000) < 0.2, 32, 20).astype(np.int32)
+    prot = rng.random((3000, 48)) < 0.1
+    kw = dict(alpha=1.2, metric=m, deg_per_node=torch.from_numpy(dpn).cuda(),
+              protect=torch.from_numpy(prot).cuda())
+    g_mfma = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
+    monkeypatch.setenv("SWANN_PRUNE_SIMT", "1")
+    g_simt = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
+    ora = O.robust_prune(X16.astype(np.float32), cand.cpu().numpy(), cdist.cpu().numpy(), 24,
+                         1.2, metric, nthreads=8, deg_per_node=dpn, protect=prot)
+    a, b = (g_mfma == g_simt).all(1).mean(), (g_mfma == ora).all(1).mean()
+    note("prune mfma vs simt / oracle", m, a, b)
+    assert a > 0.99 and b > 0.99
