@@ -384,6 +384,195 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
     if (tid < kBM2 && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
 }
 
+// ---------------------------------------------------------------------------
+// dim % 64 == 0: the same 256 x 256 workgroup tile and 128 x 64 wave tiles,
+// with the operands moved global -> LDS by the gfx950 direct load
+// (global_load_lds_dwordx4: lane i's 16 bytes land at the wave-uniform base
+// + 16 i), so no registers stage them.  K stage 64 (128 bytes of a row), two
+// LDS buffers of 64 KB: the load of stage t + 1 is issued right after the
+// barrier that opens stage t and lands while stage t computes.  Inside a
+// stage the four 16-wide substeps double-buffer their fragments in
+// registers, so LDS reads overlap MFMAs; one barrier per 32 MFMAs per wave.
+//
+// LDS layout: row-major, 128 bytes per row per stage, with the eight 16-byte
+// chunks of row r stored at chunk (c ^ swz(r)), swz(r) = (r & 7) ^ ((r >> 3) & 1):
+// a fragment read (32 consecutive rows, one logical chunk) touches eight
+// distinct chunk positions in every group of 8 rows and in every group of 16
+// rows of either parity, so it is free of bank conflicts.  Each direct-load
+// instruction fills 1 KB = 8 rows; lane i fetches row 8q + i/8, logical chunk
+// (i % 8) ^ swz(row), which lands at physical chunk i % 8.
+constexpr int kBK3 = 64;
+constexpr int kRowBytes = kBK3 * 2;
+constexpr int kStage = kBM2 * kRowBytes;           // 32 KB per operand per stage
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+__device__ __forceinline__ void dma16(const _Float16* g, unsigned char* lds) {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_vptr)lds, 16, 0, 0);
+}
+
+template <int METRIC, int SCALED>
+__global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
+    __shared__ __align__(16) unsigned char sA[2][kStage];
+    __shared__ __align__(16) unsigned char sB[2][kStage];
+    __shared__ __align__(16) float thr[kBM2];
+    __shared__ int cnt[kBM2];
+    __shared__ __align__(16) float rnorm[kBM2];
+    __shared__ __align__(16) float rscale[kBM2];
+    __shared__ int need;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;           // rows wm*128.., cols wn*64..
+    const int64_t n = a.n;
+    const int dim = a.dim;
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    const int64_t r0 = xcd_remap(blockIdx.x, ntile) * kBM2;
+
+    if (tid < kBM2) {
+        thr[tid] = r0 + tid < n ? INFINITY : -INFINITY;
+        cnt[tid] = 0;
+        rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
+        if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
+    }
+    if (tid == 0) need = 0;
+
+    // direct-load assignment: instruction j of this wave fills rows
+    // 8 (4 wave + j) .. + 7 of the stage; this lane fetches one 16-byte chunk
+    int lrow[4], lchunk[4];
+    int64_t aoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lrow[j] = (wave * 4 + j) * 8 + (lane >> 3);
+        lchunk[j] = ((lane & 7) ^ swz(lrow[j])) * 8;
+        const int64_t r = r0 + lrow[j] < n ? r0 + lrow[j] : n - 1;
+        aoff[j] = r * (int64_t)dim + lchunk[j];
+    }
+    const int nk = dim / kBK3;
+    const int64_t nct = (n + kBN2 - 1) / kBN2;
+    const int64_t nsteps = nct * nk;
+    const _Float16* X = a.hi;
+
+    auto issue = [&](int64_t t, int kt, int64_t cb) {
+        if (t >= nsteps) return;
+        const int buf = (int)(t & 1);
+        const int k0 = kt * kBK3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = wave * 4 + j;
+            dma16(X + aoff[j] + k0, &sA[buf][q * 1024]);
+            const int64_t rb = cb + lrow[j] < n ? cb + lrow[j] : n - 1;
+            dma16(X + rb * (int64_t)dim + lchunk[j] + k0, &sB[buf][q * 1024]);
+        }
+    };
+
+    // fragment addresses: row r's logical chunk c sits at r*128 + ((c ^ swz(r)) * 16);
+    // the fragment rows are (multiple of 32) + lane % 32, so swz is per lane
+    const int fsw = swz(lane & 31);
+    int aro[4], bro[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aro[i] = (wm * 128 + i * 32 + (lane & 31)) * kRowBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bro[j] = (wn * 64 + j * 32 + (lane & 31)) * kRowBytes;
+
+    int kt_c = 0, kt_f = 0;
+    int64_t cb_c = 0, cb_f = 0;
+    auto adv = [&](int& kt, int64_t& cb) {
+        if (++kt == nk) { kt = 0; cb += kBN2; }
+    };
+    f32x16 acc[4][2];
+    issue(0, kt_f, cb_f);
+    adv(kt_f, cb_f);
+
+    for (int64_t t = 0; t < nsteps; ++t) {
+        const int kt = kt_c;
+        const int64_t cbt = cb_c;
+        adv(kt_c, cb_c);
+        const int buf = (int)(t & 1);
+        // column norms/scales of a finishing tile, issued before the next
+        // stage's loads so the epilogue's wait does not include them
+        float cn[2] = {0.f, 0.f}, cs[2] = {1.f, 1.f};
+        if (kt == nk - 1) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t c = cbt + wn * 64 + j * 32 + (lane & 31);
+                if (METRIC == SWANN_METRIC_L2) cn[j] = c < n ? a.xn[c] : 0.f;
+                if (SCALED) cs[j] = c < n ? a.scale[c] : 1.f;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's stage-t loads
+        __syncthreads();                                // every wave's stage-t loads have landed
+        issue(t + 1, kt_f, cb_f);
+        adv(kt_f, cb_f);
+        if (kt == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
+        }
+        const unsigned char* pA = sA[buf];
+        const unsigned char* pB = sB[buf];
+        f16x8 fa[2][4], fb[2][2];
+        auto fload = [&](int sub, int slot) {
+            const int co = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[slot][i] = *reinterpret_cast<const f16x8*>(pA + aro[i] + co);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[slot][j] = *reinterpret_cast<const f16x8*>(pB + bro[j] + co);
+        };
+        fload(0, 0);
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+            if (sub < 3) fload(sub + 1, (sub + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[sub & 1][i],
+                                                                      fb[sub & 1][j], acc[i][j],
+                                                                      0, 0, 0);
+        }
+        if (kt == nk - 1) {
+            // ---- epilogue of this column tile: distance, threshold, append ----
+            const int64_t cb = cbt;
+            const bool diag = (cb == r0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
+                const bool cok = c < n;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
+                    asm volatile("" : "+v"(rbase));
+                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], cs[j],
+                                           rscale, thr, rnorm, cnt, a, SCALED ? 2 : 0, nullptr);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __syncthreads();
+            if (tid < kBM2 && cnt[tid] > a.cap - kBN2) atomicOr(&need, 1);
+            __syncthreads();
+            if (need) {
+                for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+                    const int64_t r = r0 + rl;
+                    if (r < n && cnt[rl] > a.cap - kBN2)
+                        compact_row_w(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C,
+                                      &thr[rl], &cnt[rl]);
+                }
+                __syncthreads();
+                if (tid == 0) need = 0;
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (tid < kBM2 && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 }  // namespace
@@ -410,6 +599,16 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled};
     const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
     const bool ip = metric == SWANN_METRIC_IP;
+    if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
+        if (scaled) {
+            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
+            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
+        } else {
+            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0>), dim3(grid), dim3(kT2), 0, st, a);
+            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0>), dim3(grid), dim3(kT2), 0, st, a);
+        }
+        return launch_status("sweep (mfma, direct loads)");
+    }
     if (scaled) {
         if (ip) hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
         else hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
