@@ -126,6 +126,38 @@ int swann_build_codes(const void* X, int x_dtype, int64_t n, int dim, const floa
                       int32_t* codes, float* alpha, float* mu_out, void* workspace,
                       void* stream);
 
+/* ---- the offline builder's extras (offline/build_graph.py) --------------- */
+
+/* candidates_from_graph (build_graph.py:63-91): the first C entries of each
+ * row of an existing graph Gc [n, gw] with exact distances (1 - <a,v>, or the
+ * direct sum of squares), -1 entries and self at 3.4e38, ascending by
+ * (distance, column).  C <= min(gw, 256). */
+int swann_candidates_from_graph(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                                const int32_t* Gc, int gw, int C, int32_t* out_idx,
+                                float* out_dist, void* stream);
+
+/* mutual_rank (build_graph.py:93-131): out [n, C] bytes, 1 where j < M and
+ * u = cand[u, j]'s node is among cand[cand[u, j], :M]. */
+int swann_mutual_rank(const int32_t* cand, int64_t n, int C, int M, uint8_t* out, void* stream);
+
+/* fill_degree (build_graph.py:132-200): G [n, W] -> out [n, W] (may equal G);
+ * rule 0 near, 1 far, 2 bridge; chunks of `chunk` nodes in order, each
+ * reading the graph as the earlier chunks left it.  W <= 128, C <= 256.
+ * `workspace`: swann_fill_workspace_size bytes. */
+int64_t swann_fill_workspace_size(int64_t n, int W, int chunk);
+int swann_fill_degree(const int32_t* G, int64_t n, int W, const int32_t* cand, int C, int rule,
+                      int chunk, int32_t* out, void* workspace, void* stream);
+
+/* enforce_min_in (build_graph.py:203-294), in place on G [n, W]: `rounds`
+ * rounds of offering every node below min_in in-edges to its candidates,
+ * column by column; a target takes the lowest offering node in place of its
+ * farthest edge whose head stays above the floor (never slot 0).  (The
+ * reference picks among several offers to one target by an unstable sort.)
+ * `workspace`: swann_min_in_workspace_size bytes. */
+int64_t swann_min_in_workspace_size(int64_t n);
+int swann_enforce_min_in(int32_t* G, int64_t n, int W, const int32_t* cand, int C, int min_in,
+                         int rounds, void* workspace, void* stream);
+
 /* Per-query dedup top-k of branch results (merge_branches_kernel,
  * local_search.cu:863-919).  bids/bdist [Q, V, kk] -> out [Q, k]; missing
  * entries are (-1, +inf).  Needs V*kk <= 8192. */

@@ -93,6 +93,14 @@ def _declare(L):
     L.so_code_ip.argtypes = [P, P, F, F, F, I, I, I]
     L.so_build_codes.restype = None
     L.so_build_codes.argtypes = [P, I64, I, P, P, P, P]
+    L.so_candidates_from_graph.restype = None
+    L.so_candidates_from_graph.argtypes = [P, I64, I, I, P, I, I, P, P, I]
+    L.so_mutual_rank.restype = None
+    L.so_mutual_rank.argtypes = [P, I64, I, I, P]
+    L.so_fill_degree.restype = None
+    L.so_fill_degree.argtypes = [P, I64, I, P, I, I, I, P]
+    L.so_enforce_min_in.restype = I
+    L.so_enforce_min_in.argtypes = [P, I64, I, P, I, I, I]
     L.so_half_to_float_export.restype = F
     L.so_half_to_float_export.argtypes = [ctypes.c_uint16]
 
@@ -372,3 +380,45 @@ def build_graph(X, metric=METRIC_IP, degree=96, candidates=128, alpha=1.2, nthre
     cand, cdist = knn_candidates(X, candidates, metric, nthreads)
     G = robust_prune(X, cand, cdist, degree, alpha, metric, nthreads)
     return add_reverse(X, G, degree, alpha, 64, metric, nthreads)
+
+
+# -- the offline builder's extras (offline/build_graph.py) ----------------
+FILL_RULES = {"near": 0, "far": 1, "bridge": 2}
+
+
+def candidates_from_graph(X, Gc, C, metric=METRIC_IP, nthreads=0):
+    """build_graph.py:63-91"""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    Gc = np.ascontiguousarray(Gc, dtype=np.int32)
+    C = min(int(C), Gc.shape[1])
+    idx = np.empty((X.shape[0], C), np.int32); dst = np.empty((X.shape[0], C), np.float32)
+    lib().so_candidates_from_graph(_p(X), X.shape[0], X.shape[1], int(metric), _p(Gc),
+                                   Gc.shape[1], C, _p(idx), _p(dst), int(nthreads))
+    return idx, dst
+
+
+def mutual_rank(cand, M):
+    """build_graph.py:93-131"""
+    cand = np.ascontiguousarray(cand, dtype=np.int32)
+    out = np.empty(cand.shape, np.uint8)
+    lib().so_mutual_rank(_p(cand), cand.shape[0], cand.shape[1], int(M), _p(out))
+    return out.astype(bool)
+
+
+def fill_degree(G, cand, rule="bridge", chunk=1024):
+    """build_graph.py:132-200"""
+    G = np.ascontiguousarray(G, dtype=np.int32)
+    cand = np.ascontiguousarray(cand, dtype=np.int32)
+    out = np.empty_like(G)
+    lib().so_fill_degree(_p(G), G.shape[0], G.shape[1], _p(cand), cand.shape[1],
+                         FILL_RULES[rule], int(chunk), _p(out))
+    return out
+
+
+def enforce_min_in(G, cand, min_in, rounds=4):
+    """build_graph.py:203-294; returns a new graph."""
+    G = np.array(G, dtype=np.int32, order="C", copy=True)
+    cand = np.ascontiguousarray(cand, dtype=np.int32)
+    lib().so_enforce_min_in(_p(G), G.shape[0], G.shape[1], _p(cand), cand.shape[1],
+                            int(min_in), int(rounds))
+    return G

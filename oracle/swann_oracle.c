@@ -867,3 +867,186 @@ void so_build_codes(const float* X, int64_t n, int dim, const float* mu_in, int3
         alpha[r] = (float)(l1 / (double)dim);
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* The offline builder's extras, offline/build_graph.py. */
+
+typedef struct { float d; int pos; } so_dp;
+static int so_dp_cmp(const void* a, const void* b) {
+    const so_dp* x = (const so_dp*)a; const so_dp* y = (const so_dp*)b;
+    if (x->d < y->d) return -1;
+    if (x->d > y->d) return 1;
+    return (x->pos > y->pos) - (x->pos < y->pos);
+}
+
+/* candidates_from_graph, build_graph.py:63-91: the first C ids of each row
+ * of an existing graph Gc [n, gw], exact distances (1 - <a, v>, or the
+ * direct sum of squares), -1 entries and self at 3.4e38, ascending
+ * (ties in column order). */
+void so_candidates_from_graph(const float* X, int64_t n, int dim, int metric,
+                              const int32_t* Gc, int gw, int C, int32_t* out_idx,
+                              float* out_d, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        so_dp* row = (so_dp*)malloc(sizeof(so_dp) * (size_t)C);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t u = 0; u < n; ++u) {
+            const float* a = X + u * dim;
+            for (int j = 0; j < C; ++j) {
+                const int v = Gc[u * gw + j];
+                float d;
+                if (v < 0 || v == u) d = 3.4e38f;
+                else if (metric == SO_METRIC_IP) d = 1.0f - (float)so_dot_d(a, X + (int64_t)v * dim, dim);
+                else {
+                    double s = 0.0;
+                    for (int e = 0; e < dim; ++e) { const double df = (double)a[e] - (double)X[(int64_t)v * dim + e]; s += df * df; }
+                    d = (float)s;
+                }
+                row[j].d = d; row[j].pos = j;
+            }
+            qsort(row, (size_t)C, sizeof(so_dp), so_dp_cmp);
+            for (int j = 0; j < C; ++j) {
+                out_idx[u * C + j] = Gc[u * gw + row[j].pos];
+                out_d[u * C + j] = row[j].d;
+            }
+        }
+        free(row);
+    }
+}
+
+/* mutual_rank, build_graph.py:93-131: out[u, j] = 1 when j < M, cand[u, j]
+ * = v >= 0 and u is among cand[v, :M]. */
+void so_mutual_rank(const int32_t* cand, int64_t n, int C, int M, uint8_t* out) {
+    if (M > C) M = C;
+    for (int64_t u = 0; u < n; ++u)
+        for (int j = 0; j < C; ++j) {
+            uint8_t m = 0;
+            const int v = cand[u * C + j];
+            if (j < M && v >= 0)
+                for (int t = 0; t < M; ++t)
+                    if (cand[(int64_t)v * C + t] == (int32_t)u) { m = 1; break; }
+            out[u * C + j] = m;
+        }
+}
+
+static int so_contains(const int32_t* a, int len, int32_t x) {
+    for (int i = 0; i < len; ++i) if (a[i] == x) return 1;
+    return 0;
+}
+
+/* fill_degree, build_graph.py:132-200.  rule 0 near, 1 far, 2 bridge.
+ * Chunks of `chunk` nodes in order; a chunk reads the graph as the earlier
+ * chunks left it.  Per node: a candidate is free unless it is already an
+ * out-neighbour, the node itself or -1 (bridge: or two hops away through the
+ * kept neighbours); free candidates go, nearest first (far: farthest first),
+ * into the empty slots in ascending position. */
+void so_fill_degree(const int32_t* G, int64_t n, int W, const int32_t* cand, int C, int rule,
+                    int chunk, int32_t* out) {
+    memcpy(out, G, sizeof(int32_t) * (size_t)n * W);
+    int32_t* next = (int32_t*)malloc(sizeof(int32_t) * (size_t)chunk * W);
+    int32_t* two = (int32_t*)malloc(sizeof(int32_t) * (size_t)W * W);
+    int* pick = (int*)malloc(sizeof(int) * (size_t)C);
+    int* empty = (int*)malloc(sizeof(int) * (size_t)W);
+    for (int64_t s = 0; s < n; s += chunk) {
+        const int64_t e = s + chunk < n ? s + chunk : n;
+        for (int64_t u = s; u < e; ++u) {
+            const int32_t* kept = out + u * W;
+            int32_t* nr = next + (u - s) * W;
+            memcpy(nr, kept, sizeof(int32_t) * (size_t)W);
+            if (rule == 2)
+                for (int k = 0; k < W; ++k)
+                    for (int t = 0; t < W; ++t)
+                        two[k * W + t] = kept[k] >= 0 ? out[(int64_t)kept[k] * W + t] : -1;
+            int nfree = 0;
+            for (int j = 0; j < C; ++j) {
+                const int32_t c = cand[u * C + j];
+                int taken = (c < 0) || (c == (int32_t)u) || so_contains(kept, W, c);
+                if (!taken && rule == 2 && so_contains(two, W * W, c)) taken = 1;
+                if (!taken) pick[nfree++] = j;
+            }
+            int nempty = 0;
+            for (int k = 0; k < W; ++k) if (kept[k] < 0) empty[nempty++] = k;
+            const int take = nfree < nempty ? nfree : nempty;
+            for (int t = 0; t < take; ++t) {
+                const int j = rule == 1 ? pick[nfree - 1 - t] : pick[t];
+                nr[empty[t]] = cand[u * C + j];
+            }
+        }
+        memcpy(out + s * W, next, sizeof(int32_t) * (size_t)(e - s) * W);
+    }
+    free(next); free(two); free(pick); free(empty);
+}
+
+/* enforce_min_in, build_graph.py:203-294, in place on G [n, W].  Each round
+ * recounts in-degrees; every node short of min_in is offered, column by
+ * column of its candidate list, to that candidate, which takes it in place of
+ * its farthest out-edge whose head stays above the floor (never its first
+ * slot).  One offer per target per column (the lowest offering node); an
+ * edge already present is skipped.  In-degree updates follow the reference's
+ * indexed assignment: a node that loses several edges in one column is
+ * decremented once.  Returns the number of rounds run. */
+int so_enforce_min_in(int32_t* G, int64_t n, int W, const int32_t* cand, int C, int min_in,
+                      int rounds) {
+    int32_t* indeg = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t* remaining = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t* winner = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    uint8_t* vflag = (uint8_t*)malloc((size_t)n);
+    int r;
+    for (r = 0; r < rounds; ++r) {
+        memset(indeg, 0, sizeof(int32_t) * (size_t)n);
+        for (int64_t i = 0; i < n * W; ++i) if (G[i] >= 0) indeg[G[i]] += 1;
+        int64_t nweak = 0;
+        for (int64_t u = 0; u < n; ++u) {
+            remaining[u] = 0;
+            if (indeg[u] < min_in) {
+                int need = min_in - indeg[u];
+                remaining[u] = need < C ? need : C;
+                ++nweak;
+            }
+        }
+        if (nweak == 0) break;
+        for (int i = 0; i < C; ++i) {
+            int any = 0;
+            for (int64_t u = 0; u < n; ++u) winner[u] = -1;
+            for (int64_t s = 0; s < n; ++s) {
+                if (remaining[s] <= 0) continue;
+                any = 1;
+                const int32_t t = cand[s * C + i];
+                if (t < 0 || t == (int32_t)s) continue;
+                if (so_contains(G + (int64_t)t * W, W, (int32_t)s)) continue;
+                if (winner[t] < 0) winner[t] = (int32_t)s;     /* lowest s per target */
+            }
+            if (!any) break;
+            memset(vflag, 0, (size_t)n);
+            /* decide every slot against the column's starting in-degrees */
+            for (int64_t t = 0; t < n; ++t) {
+                const int32_t s = winner[t];
+                if (s < 0) continue;
+                int slot = -1;
+                for (int k = 0; k < W; ++k) {
+                    const int32_t h = G[t * W + k];
+                    if (h >= 0 && indeg[h] > min_in) slot = k;
+                }
+                if (slot < 1) { winner[t] = -1; continue; }
+                vflag[G[t * W + slot]] = 1;
+                G[t * W + slot] = -2 - slot;        /* placeholder until the counts move */
+            }
+            for (int64_t v = 0; v < n; ++v) if (vflag[v]) indeg[v] -= 1;
+            for (int64_t t = 0; t < n; ++t) {
+                const int32_t s = winner[t];
+                if (s < 0) continue;
+                for (int k = 0; k < W; ++k)
+                    if (G[t * W + k] <= -2) { G[t * W + k] = s; break; }
+                indeg[s] += 1;
+                remaining[s] -= 1;
+            }
+        }
+    }
+    free(indeg); free(remaining); free(winner); free(vflag);
+    return r;
+}

@@ -43,6 +43,12 @@ PROTOTYPES = {
     "swann_build_reverse": (I, [P, I, I64, I, I, P, I, F, I, P, P, P, P]),
     "swann_codes_workspace_size": (I64, [I64, I]),
     "swann_build_codes": (I, [P, I, I64, I, P, P, P, P, P, P]),
+    "swann_candidates_from_graph": (I, [P, I, I64, I, I, P, I, I, P, P, P]),
+    "swann_mutual_rank": (I, [P, I64, I, I, P, P]),
+    "swann_fill_workspace_size": (I64, [I64, I, I]),
+    "swann_fill_degree": (I, [P, I64, I, P, I, I, I, P, P, P]),
+    "swann_min_in_workspace_size": (I64, [I64]),
+    "swann_enforce_min_in": (I, [P, I64, I, P, I, I, I, P, P]),
 }
 
 _lib = None

@@ -225,7 +225,8 @@ def make_build_extras(build, offline):
         Rd = build.add_reverse(Xt, Gd, 12, alpha=1.2, deg_per_node=dpn, metric=metric)
         R = build.add_reverse(Xt, Gp, 12, alpha=1.2, metric=metric)
         cg, cgd = offline.candidates_from_graph(Xt, R, 12, metric=metric)
-        fills = {rule: offline.fill_degree(Gp, cand, rule=rule).numpy().astype(np.int16)
+        Gp24 = build.robust_prune(Xt, cand, cdist, 24, alpha=1.2, metric=metric)
+        fills = {rule: offline.fill_degree(Gp24, cand, rule=rule).numpy().astype(np.int16)
                  for rule in ("near", "far", "bridge")}
         with contextlib.redirect_stdout(io.StringIO()):
             Gmin = offline.enforce_min_in(Xt, R.clone(), cand, 8, metric=metric, rounds=4)
@@ -236,7 +237,8 @@ def make_build_extras(build, offline):
                     f"{tag}_Gb": Gb.numpy().astype(np.int16), f"{tag}_R": R.numpy().astype(np.int16),
                     f"{tag}_Rd": Rd.numpy().astype(np.int16),
                     f"{tag}_cg": cg.numpy().astype(np.int16), f"{tag}_cgd": cgd.numpy(),
-                    f"{tag}_Gmin": Gmin.numpy().astype(np.int16)})
+                    f"{tag}_Gmin": Gmin.numpy().astype(np.int16),
+                    f"{tag}_Gp24": Gp24.numpy().astype(np.int16)})
         for rule, g in fills.items():
             out[f"{tag}_fill_{rule}"] = g
     np.savez_compressed(OUT / "refbuild_extras.npz", **out)
