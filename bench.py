@@ -40,6 +40,8 @@ CONFIGS = {
                nq=10_000, D=64, cand=128, branches=32, team=16),
     "c3": dict(n=1_000_000, d=1536, dtype="f16", metric="ip", gen="lowrank", rank=256, seed=3,
                nq=10_000, D=64, cand=128, branches=32, team=16),
+    "c5": dict(n=1_000_000, d=1024, dtype="f32", metric="l2", gen="gmm", rank=0, seed=5,
+               nq=10_000, D=64, cand=128, branches=32, team=16),
     # small-batch latency; --config c4 prints its own line (see run_c4)
     "c4": dict(n=500_000, d=4096, dtype="f16", metric="ip", gen="lowrank", rank=512, seed=4,
                nq=2048, D=64, cand=128, branches=32, team=32),
@@ -49,8 +51,8 @@ C4_BATCHES = (1, 8, 64, 512)
 EPS_SWEEP = (0.02, 0.05, 0.1, 0.2)
 # If no stop_eps reaches the target at the configured knobs, the search effort
 # is raised along this ladder (branches, queue, budget, stop_eps), cheapest first.
-LADDER = ((64, 32, 64, 0.3), (96, 32, 64, 0.3), (64, 48, 128, 0.3), (128, 24, 64, 0.3),
-          (128, 32, 64, 0.3), (64, 64, 128, 0.3), (128, 48, 128, 0.3))
+LADDER = ((64, 32, 64, 0.3), (64, 48, 64, 0.2), (96, 32, 64, 0.3), (64, 48, 128, 0.3),
+          (128, 24, 128, 0.2), (128, 32, 64, 0.3), (64, 64, 128, 0.3), (128, 48, 128, 0.3))
 TARGET_RECALL = 0.95
 HBM_PEAK = 8.0e12
 # HBM bytes per advance launch measured by rocprofv3 --pmc (FETCH_SIZE x 2.000 +
@@ -60,6 +62,7 @@ HBM_PEAK = 8.0e12
 # workload and knobs; otherwise `traffic` is reported as null.
 PMC_TRAFFIC = {
     ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "6d609080657bb8e5"): 5.620e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "6d609080657bb8e5"): 5.635e12,
 }
 
 
@@ -203,6 +206,69 @@ def cpu_baseline(X, G, Q, seeds, cfg, eps, k, nsample, metric_id, elem_bytes):
                 seconds=round(dt, 2))
 
 
+SWEEP_GRID = dict(branches=(16, 32, 64, 128), queue=(12, 24, 48), budget=(64, 128),
+                  stop_eps=(0.05, 0.1, 0.2, 0.3))
+SWEEP_SHARED_V = (8, 16, 32)
+FRONTIER_TARGETS = (0.90, 0.95, 0.99)
+
+
+def cheapest(rows, target):
+    """The fastest row that reaches `target` (bench/pick_settings.py:40-43)."""
+    ok = [r for r in rows if r["recall"] >= target]
+    return max(ok, key=lambda r: r["qps"]) if ok else None
+
+
+def run_sweep(index, Q, truth, k, cfg, nq):
+    """Recall-QPS grid over the production search path (branches, queue,
+    budget, stop_eps; shared table, bound and claims on), plus the
+    shared-fanout rows of bench/entry_arms.py: one branch holding V seeds
+    (best-first and round-robin lineage policies, budget 128).  Each row is
+    the best of two timed searches of the whole batch after one warm-up."""
+    from swann_amd import _engine as E
+    from swann_amd import _select as S
+    rows = []
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        best, ids = None, None
+        for _ in range(2):
+            t1 = time.perf_counter()
+            ids = fn()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t1
+            best = dt if best is None else min(best, dt)
+        return ids, best
+
+    for J in SWEEP_GRID["branches"]:
+        for L in SWEEP_GRID["queue"]:
+            for Bud in SWEEP_GRID["budget"]:
+                for eps in SWEEP_GRID["stop_eps"]:
+                    ids, dt = timed(lambda: index.search_async(
+                        Q, k=k, branches=J, queue=L, budget=Bud, stop_eps=eps,
+                        team=cfg["team"])[0])
+                    row = dict(fanout="branch", branches=J, V=1, queue=L, budget=Bud,
+                               stop_eps=eps, recall=round(recall(ids, truth, k), 4),
+                               qps=round(nq / dt, 1))
+                    log(row)
+                    rows.append(row)
+    for V in SWEEP_SHARED_V:
+        ent = S.select_nearest(Q, index._cat, V, metric=index._m)
+        seeds = index.catalogue[ent].to(torch.int32).unsqueeze(1).contiguous()   # [Q, 1, V]
+        for pol, pname in ((E.POLICY_BEST, "best"), (E.POLICY_ROUND_ROBIN, "rr")):
+            for L in (24, 48):
+                ids, dt = timed(lambda: E.search(
+                    index.X, index.G, Q, seeds, k=k, L=L, B=128, metric=index._m,
+                    team_size=cfg["team"], policy=pol, stop_eps=0.3, check=False)[0])
+                row = dict(fanout=f"shared/{pname}", branches=1, V=V, queue=L, budget=128,
+                           stop_eps=0.3, recall=round(recall(ids, truth, k), 4),
+                           qps=round(nq / dt, 1))
+                log(row)
+                rows.append(row)
+    frontier = {f"{t:g}": cheapest(rows, t) for t in FRONTIER_TARGETS}
+    return rows, frontier
+
+
 def run_c4(a, dev):
     """Config C4: p50/p99 latency of one batch (1, 8, 64, 512 queries) at
     branches 32 and 128, queue 12, team 32, the other knobs at their defaults,
@@ -292,6 +358,8 @@ def main():
                     help="branches,queue,budget,stop_eps: skip the operating-point search")
     ap.add_argument("--cpu-sample", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="print the recall-QPS grid and its frontier instead of the headline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a plain 2 GiB device copy first (scale for rocprof FETCH/WRITE_SIZE)")
     a = ap.parse_args()
@@ -336,6 +404,18 @@ def main():
     log(f"graph built in {build_s:.1f}s")
     index = swann_amd.Index(X, G, metric=cfg["metric"])
     srch = Searcher(index, Q, k, cfg)
+
+    if a.sweep:
+        rows, frontier = run_sweep(index, Q, truth, k, cfg, nq)
+        print(json.dumps({
+            "metric": f"recall@10-QPS frontier ({a.config.upper()})", "unit": "queries/s",
+            "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic (generated on the GPU from fixed seeds)",
+            "config": {"workload": f"{a.config.upper()}: n={n:,} x d={cfg['d']} "
+                                   f"{cfg['dtype']} {cfg['metric']}, {nq:,} queries, "
+                                   f"D={cfg['D']}, k={k}, team={cfg['team']}"},
+            "build_s": round(build_s, 2), "frontier": frontier, "rows": rows}), flush=True)
+        return
 
     if a.calibrate_copy:
         src = torch.empty(1 << 29, dtype=torch.float32, device=dev).fill_(1.0)
