@@ -66,7 +66,11 @@ int swann_device_count(void);
  *   ids      [Q, J, L] int32, dist [Q, J, L] fp32, expd/lin [Q, J, L] uint8
  *   visited  [Q, J, H] int32 (H a power of two; H == 1 disables it)
  *   counters [Q, J, SWANN_NCTR] int32
- *   cache_id [Q, Hc] int32, cache_d [Q, Hc] fp32 (Hc a power of two; 0 = off)
+ *   cache_id [Q, Hc] int32, cache_d [Q, Hc] fp32 (Hc a power of two; 0 = off);
+ *            or one [Q, Hc, 2] allocation of (id, d) pairs, passed as
+ *            cache_id = its start and cache_d = cache_id + 1 word (the
+ *            kernels detect that adjacency and stride by 2; a claim and the
+ *            distance stored into it then share a cache line)
  *   bound    [Q] fp32 or NULL
  * A disabled feature is a NULL pointer (and Hc = 0), matching the
  * reference's empty-tensor convention (swann/_engine.py:269-274).

@@ -200,8 +200,11 @@ def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32
         crowd_frac=float(crowd_frac))
     if shared_cache and J > 1:
         Hc = cache_size(J, B, D)
-        st.cache_id = torch.empty((Q, Hc), dtype=torch.int32, device=dev)
-        st.cache_d = torch.empty((Q, Hc), dtype=torch.float32, device=dev)
+        # one allocation of (id, d) pairs: a claim and the distance later
+        # stored into it share a cache line; cache_id / cache_d are views
+        tab = torch.empty((Q, Hc, 2), dtype=torch.int32, device=dev)
+        st.cache_id = tab[..., 0]
+        st.cache_d = tab.view(torch.float32)[..., 1]
     else:
         st.cache_id = torch.empty((0, 0), dtype=torch.int32, device=dev)
         st.cache_d = torch.empty((0, 0), dtype=torch.float32, device=dev)

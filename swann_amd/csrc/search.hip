@@ -49,6 +49,9 @@ constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in 
 #ifndef SWANN_CAS_FIRST
 #define SWANN_CAS_FIRST 0
 #endif
+#ifndef SWANN_PIPE2
+#define SWANN_PIPE2 0
+#endif
 constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
 constexpr size_t kMaxLds = 64 * 1024;
 
@@ -126,6 +129,65 @@ __device__ __forceinline__ float team_dist(const float* __restrict__ sq,
     return METRIC == SWANN_METRIC_IP ? 1.f - acc : acc;
 }
 
+// Two distances at once (16-byte-aligned rows, dim % VEC == 0): the loads of
+// both rows are issued before either's arithmetic, so a team keeps two rows in
+// flight.  Each row's sum adds its chunks in the same order as team_dist, so
+// both results are bit-identical to two team_dist calls.
+#ifndef SWANN_PIPE_CHUNKS
+#define SWANN_PIPE_CHUNKS 12
+#endif
+template <int TEAM, typename XT, int METRIC>
+__device__ __forceinline__ void team_dist2(const float* __restrict__ sq, const XT* __restrict__ x0,
+                                           const XT* __restrict__ x1, bool two, int dim, int tl,
+                                           float& d0, float& d1) {
+    constexpr int VEC = Vec<XT>::N;
+    constexpr int STRIDE = TEAM * VEC;
+    constexpr int K2 = SWANN_PIPE_CHUNKS;
+    float acc0 = 0.f, acc1 = 0.f;
+    auto add = [&](float& acc, const uint4& raw, int base) {
+        if constexpr (VEC == 4) {
+            const float4v xv = __builtin_bit_cast(float4v, raw);
+            const float4v qv = *reinterpret_cast<const float4v*>(sq + base);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(qv[i], xv[i]);
+        } else {
+            const half8 hv = __builtin_bit_cast(half8, raw);
+            const float4v q0 = *reinterpret_cast<const float4v*>(sq + base);
+            const float4v q1 = *reinterpret_cast<const float4v*>(sq + base + 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q0[i], (float)hv[i]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q1[i], (float)hv[4 + i]);
+        }
+    };
+    for (int b0 = tl * VEC; b0 < dim; b0 += STRIDE * K2) {
+        uint4 r0[K2], r1[K2];
+#pragma unroll
+        for (int c = 0; c < K2; ++c) {
+            const int base = b0 + c * STRIDE;
+            if (base < dim) {
+                r0[c] = *reinterpret_cast<const uint4*>(x0 + base);
+                if (two) r1[c] = *reinterpret_cast<const uint4*>(x1 + base);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < K2; ++c) {
+            const int base = b0 + c * STRIDE;
+            if (base < dim) {
+                add(acc0, r0[c], base);
+                if (two) add(acc1, r1[c], base);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = TEAM / 2; off > 0; off >>= 1) {
+        acc0 = acc0 + __shfl_down(acc0, off, TEAM);
+        acc1 = acc1 + __shfl_down(acc1, off, TEAM);
+    }
+    d0 = METRIC == SWANN_METRIC_IP ? 1.f - acc0 : acc0;
+    d1 = METRIC == SWANN_METRIC_IP ? 1.f - acc1 : acc1;
+}
+
 template <int TEAM, typename XT>
 __device__ __forceinline__ float team_dist_m(const float* sq, const XT* x, int dim, int tl,
                                              bool vec_ok, int metric) {
@@ -184,8 +246,11 @@ __device__ __forceinline__ int vis_insert(int* tab, int H, int key, int* fail) {
 }
 
 // Per-query shared table and claims (local_search.cu:169-183).  Agent scope:
-// the branches of one query may run on different XCDs.
-__device__ __forceinline__ int cache_slot(int* cid, int Hc, int key, int* claimed) {
+// the branches of one query may run on different XCDs.  `ts` is the table's
+// stride in words: 1 for separate id and distance arrays, 2 when they are
+// interleaved (id, d) pairs, so that a claim and the distance stored into it
+// later share one cache line (half the table's DRAM activations).
+__device__ __forceinline__ int cache_slot(int* cid, int Hc, int ts, int key, int* claimed) {
     const unsigned mask = (unsigned)(Hc - 1);
     unsigned pos = (2654435761u * (unsigned)key) & mask;
     for (int probe = 0; probe < kCprobe; ++probe) {
@@ -193,18 +258,19 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int key, int* claime
         // The compare-and-swap returns the slot's value: one round trip
         // decides found / claimed / occupied.
         int expected = 0;
-        if (__hip_atomic_compare_exchange_strong(&cid[pos], &expected, key + 1, __ATOMIC_RELAXED,
-                                                 __ATOMIC_RELAXED, SWANN_TABLE_SCOPE)) {
+        if (__hip_atomic_compare_exchange_strong(&cid[pos * ts], &expected, key + 1,
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 SWANN_TABLE_SCOPE)) {
             *claimed = 1;
             return (int)pos;
         }
         if (expected == key + 1) return (int)pos;
 #else
-        int cur = __hip_atomic_load(&cid[pos], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
+        int cur = __hip_atomic_load(&cid[pos * ts], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
         if (cur == key + 1) return (int)pos;
         if (cur == 0) {
             int expected = 0;
-            if (__hip_atomic_compare_exchange_strong(&cid[pos], &expected, key + 1,
+            if (__hip_atomic_compare_exchange_strong(&cid[pos * ts], &expected, key + 1,
                                                      __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                      SWANN_TABLE_SCOPE)) {
                 *claimed = 1;
@@ -250,7 +316,7 @@ struct InitArgs {
     int32_t* ids; float* dist; uint8_t* expd; uint8_t* lin; int32_t* visited; int32_t* counters;
     int dim, J, V, L, H, metric;
     int64_t Q, n;
-    int32_t* cache_id; float* cache_d; int Hc; float* bound;
+    int32_t* cache_id; float* cache_d; int Hc; float* bound; int ts;
     int vec_ok;
 };
 
@@ -292,7 +358,12 @@ __global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
     }
     // The query's table and bound belong to all J branches; they clear it
     // between them (local_search.cu:302-313).
-    if (a.Hc > 0) {
+    if (a.Hc > 0 && a.ts == 2) {
+        // interleaved (id, d) pairs, one 8-byte store each
+        int2* p2 = reinterpret_cast<int2*>(a.cache_id + q * (int64_t)a.Hc * 2);
+        const int fm = __float_as_int(FLT_MAX);
+        for (int t = j * BLOCK + tid; t < a.Hc; t += a.J * BLOCK) p2[t] = make_int2(0, fm);
+    } else if (a.Hc > 0) {
         int32_t* cid = a.cache_id + q * (int64_t)a.Hc;
         float* cdd = a.cache_d + q * (int64_t)a.Hc;
         if ((a.Hc & 3) == 0) {
@@ -370,7 +441,7 @@ struct AdvArgs {
     int32_t* ids; float* dist; uint8_t* expd; uint8_t* lin; int32_t* visited; int32_t* counters;
     int dim, D, J, L, H, metric, delta, max_exp, policy, V;
     float stop_eps; int kstop;
-    int32_t* cache_id; float* cache_d; int Hc; float* bound; int exclusive;
+    int32_t* cache_id; float* cache_d; int Hc; float* bound; int exclusive; int ts;
     int stall_patience; float crowd_frac;
     const int32_t* active; int64_t nblocks, nbranch, n;
     int vec_ok;
@@ -422,8 +493,9 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     int32_t* vis = a.visited + flat * (int64_t)a.H;
     int32_t* ctr = a.counters + flat * kNctr;
     const int64_t qb = flat * (int64_t)L;
-    int32_t* cid = a.Hc > 0 ? a.cache_id + q * (int64_t)a.Hc : nullptr;
-    float* cdd = a.Hc > 0 ? a.cache_d + q * (int64_t)a.Hc : nullptr;
+    const int ts = a.ts;
+    int32_t* cid = a.Hc > 0 ? a.cache_id + q * (int64_t)a.Hc * ts : nullptr;
+    float* cdd = a.Hc > 0 ? a.cache_d + q * (int64_t)a.Hc * ts : nullptr;
     const float* qrow = a.Qv + q * (int64_t)a.dim;
     const XT* X = reinterpret_cast<const XT*>(a.X);
 
@@ -545,8 +617,8 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             int slot = -1, claimed = 0;
             float d = FLT_MAX;
             if (a.Hc > 0) {
-                slot = cache_slot(cid, a.Hc, v, &claimed);
-                d = (slot >= 0 && !claimed) ? load_agent_f(cdd + slot) : FLT_MAX;
+                slot = cache_slot(cid, a.Hc, ts, v, &claimed);
+                d = (slot >= 0 && !claimed) ? load_agent_f(cdd + (int64_t)slot * ts) : FLT_MAX;
             }
             if (a.exclusive && slot >= 0 && !claimed && d != FLT_MAX) {
                 ++r_hits; ++cov;                                // another branch owns it
@@ -562,7 +634,44 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
 
         // ---- score the survivors, TEAM lanes per distance ----
         const int nw = s_nwork;
+        auto record = [&](int w, int v, float d) {
+            const int slot = w_slot[w];
+            const int packed = w_nidx[w];
+            const int nidx = packed & 0xffff, claimed = packed >> 16;
+            if (slot >= 0) { store_agent_f(cdd + (int64_t)slot * ts, d); ++r_claim; }
+            ++r_evals;
+            const bool taken = a.exclusive && slot >= 0 && !claimed && d != FLT_MAX;
+            if (taken) ++cov;
+            else { c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin; }
+        };
+#if SWANN_PIPE2
+        // two work items per team in flight (no code filter: its skip
+        // decision comes between the items' loads)
+        const bool pipe = !a.codes && a.vec_ok;
+        if (pipe) {
+            for (int w = team; w < nw; w += 2 * NT) {
+                const int w1 = w + NT;
+                const bool two = w1 < nw;
+                const int v0 = w_v[w], v1 = two ? w_v[w1] : v0;
+                float d0, d1;
+                if (a.metric == SWANN_METRIC_IP)
+                    team_dist2<TEAM, XT, SWANN_METRIC_IP>(sq, X + (int64_t)v0 * a.dim,
+                                                          X + (int64_t)v1 * a.dim, two, a.dim,
+                                                          tl, d0, d1);
+                else
+                    team_dist2<TEAM, XT, SWANN_METRIC_L2>(sq, X + (int64_t)v0 * a.dim,
+                                                          X + (int64_t)v1 * a.dim, two, a.dim,
+                                                          tl, d0, d1);
+                if (tl == 0) {
+                    record(w, v0, d0);
+                    if (two) record(w1, v1, d1);
+                }
+            }
+        }
+        for (int w = pipe ? nw : team; w < nw; w += NT) {
+#else
         for (int w = team; w < nw; w += NT) {
+#endif
             const int v = w_v[w];
             if (a.codes) {
                 // decide from the code before reading the row (:560-575); a
@@ -583,16 +692,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             }
             const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
                                                  a.vec_ok, a.metric);
-            if (tl == 0) {
-                const int slot = w_slot[w];
-                const int packed = w_nidx[w];
-                const int nidx = packed & 0xffff, claimed = packed >> 16;
-                if (slot >= 0) { store_agent_f(cdd + slot, d); ++r_claim; }
-                ++r_evals;
-                const bool taken = a.exclusive && slot >= 0 && !claimed && d != FLT_MAX;
-                if (taken) ++cov;
-                else { c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin; }
-            }
+            if (tl == 0) record(w, v, d);
         }
         if (a.crowd_frac > 0.f) { block_add<BLOCK>(&s_nbr, nbr); block_add<BLOCK>(&s_cov, cov); }
         __syncthreads();
@@ -771,6 +871,15 @@ size_t advance_lds(int dim, int D, int L) {
            (size_t)nsort * (4 * 9) + (size_t)L * 4 + (size_t)nsort * 3;
 }
 
+// The table is interleaved (id, d) pairs when cache_d is the word right after
+// cache_id: two separate [Q, Hc] arrays cannot overlap that way.
+int table_stride(const int32_t* cache_id, const float* cache_d, int Hc) {
+    if (Hc > 0 && cache_id &&
+        reinterpret_cast<const char*>(cache_d) == reinterpret_cast<const char*>(cache_id) + 4)
+        return 2;
+    return 1;
+}
+
 int search_block_for(int64_t nbranch) {
     // SWANN_SEARCH_BLOCK=64|256|1024 pins the workgroup size (tests use it to
     // run every layout on the same inputs); read per call, it costs a getenv.
@@ -902,6 +1011,7 @@ int swann_init_states(const void* X, int x_dtype, int64_t n, int dim, const floa
     if (Q == 0) return SWANN_OK;
     InitArgs a{X, Qv, seeds, ids, dist, expd, lin, visited, counters, dim, J, V, L, H, metric,
                Q, n, Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound,
+               table_stride(cache_id, cache_d, Hc),
                rows_vec_ok(X, dim, x_dtype) ? 1 : 0};
     const int64_t nb = Q * J;
     const int block = search_block_for(nb);
@@ -932,6 +1042,7 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
     AdvArgs a{X, G, Qv, ids, dist, expd, lin, visited, counters, dim, D, J, L, H, metric,
               delta, max_expansions, policy, V, stop_eps, kstop,
               Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound, exclusive ? 1 : 0,
+              table_stride(cache_id, cache_d, Hc),
               stall_patience, crowd_frac, active, nb, Q * J, n,
               rows_vec_ok(X, dim, x_dtype) ? 1 : 0,
               codes, codes ? alpha : nullptr, codes ? cmu : nullptr, codes ? cwords : 0,

@@ -485,3 +485,31 @@ def test_code_filter_cuts_reads_at_small_recall_cost():
     note("code filter recall/evals", out)
     assert out["codes"][1] < out["plain"][1]
     assert out["codes"][0] >= out["plain"][0] - 0.05
+
+
+def test_interleaved_and_separate_tables_agree():
+    """The shared table as one allocation of (id, d) pairs (cache_d one word
+    after cache_id, as init_states allocates it) and as two separate arrays
+    (what the reference passes) give the same answers, the same counters and
+    the same table contents (shared table on, no claims or bound, so the
+    search is deterministic)."""
+    X, G = toy(seed=8)
+    rng = np.random.default_rng(23)
+    nq, J, L, budget = 6, 4, 16, 20
+    Qv = gaussian(nq, X.shape[1], 57, True)
+    seeds = torch.from_numpy(rng.integers(0, X.shape[0], (nq, J)).astype(np.int32))
+    Xg, Gg, Qg = to_gpu(X, G, Qv)
+    kw = dict(L=L, B=budget, D=G.shape[1], team_size=16, stop_eps=0.1, kstop=10,
+              shared_cache=True)
+    a = E.init_states(Xg, Qg, seeds, **kw)
+    assert a.cache_d.data_ptr() == a.cache_id.data_ptr() + 4      # interleaved pairs
+    E.advance(Xg, Gg, Qg, a, budget)
+    b = E.init_states(Xg, Qg, seeds, **kw)
+    b.cache_id = b.cache_id.clone()
+    b.cache_d = b.cache_d.clone()
+    assert b.cache_d.data_ptr() != b.cache_id.data_ptr() + 4       # separate arrays
+    E.advance(Xg, Gg, Qg, b, budget)
+    for f in ("ids", "dist", "expanded", "lineage", "counters"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    assert torch.equal(a.cache_id, b.cache_id)
+    assert torch.equal(a.cache_d.view(torch.int32), b.cache_d.view(torch.int32))
