@@ -63,6 +63,7 @@ HBM_PEAK = 8.0e12
 PMC_TRAFFIC = {
     ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "6d609080657bb8e5"): 5.620e12,
     ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "6d609080657bb8e5"): 5.635e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "5f8609651dd61c31"): 5.640e12,
 }
 
 
