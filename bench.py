@@ -148,6 +148,7 @@ class Searcher:
         self.E, self.S = E, S
         self.ix, self.Q, self.k = index, Q, k
         self.cfg = cfg
+        self.codes = None           # (codes, alpha, mu, margin) for the sign-code pre-filter
         self.ws = None
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
 
@@ -169,7 +170,7 @@ class Searcher:
                            elide_visited=True)
         if record:
             ev[2].record()
-        E.advance(ix.X, ix.G, self.Q, st, cfg["budget"])
+        E.advance(ix.X, ix.G, self.Q, st, cfg["budget"], codes=self.codes)
         if record:
             ev[3].record()
         bi, bd = E.branch_topk(st, self.k)
@@ -270,6 +271,50 @@ def run_sweep(index, Q, truth, k, cfg, nq):
     return rows, frontier
 
 
+CODE_KNOBS = ((64, 48, 64, 0.2), (64, 48, 128, 0.3), (32, 48, 64, 0.2), (64, 24, 64, 0.2),
+              (128, 48, 128, 0.1), (128, 48, 128, 0.2))
+CODE_MARGINS = (None, 0.02, 0.05, 0.1)
+
+
+def run_code_sweep(index, Q, truth, k, cfg, nq):
+    """The production search with the sign-code pre-filter
+    (local_search.cu:205-243, :565-572) at the knobs around the frontier and a
+    few margins (None = no codes, the same search as the plain rows).  Codes
+    are built once on the GPU from the corpus the index holds."""
+    from swann_amd import codes as C
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cd, al, mu = C.build_codes(index.X)
+    torch.cuda.synchronize()
+    codes_s = time.perf_counter() - t0
+    log(f"codes built in {codes_s:.2f}s ({cd.shape[1]} words per row)")
+    rows = []
+    for J, L, Bud, eps in CODE_KNOBS:
+        for m in CODE_MARGINS:
+            srch = Searcher(index, Q, k, dict(cfg, branches=J, queue=L, budget=Bud))
+            srch.codes = None if m is None else (cd, al, mu, m)
+            srch.step(eps)
+            torch.cuda.synchronize()
+            best, ids, st = None, None, None
+            for _ in range(2):
+                t1 = time.perf_counter()
+                ids, _, st = srch.step(eps)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t1
+                best = dt if best is None else min(best, dt)
+            ctr = st.counters.sum(dim=(0, 1)).tolist()
+            row = dict(fanout="branch" if m is None else "branch+codes", branches=J, V=1,
+                       queue=L, budget=Bud, stop_eps=eps, margin=m,
+                       recall=round(recall(ids, truth, k), 4), qps=round(nq / best, 1),
+                       rows_read_per_query=round(ctr[1] / nq, 1),
+                       ctr3_per_query=round(ctr[3] / nq, 1))    # code skips + exhausted branches
+            log(row)
+            rows.append(row)
+            del srch, st
+    frontier = {f"{t:g}": cheapest(rows, t) for t in FRONTIER_TARGETS}
+    return rows, frontier, codes_s
+
+
 def run_c4(a, dev):
     """Config C4: p50/p99 latency of one batch (1, 8, 64, 512 queries) at
     branches 32 and 128, queue 12, team 32, the other knobs at their defaults,
@@ -361,6 +406,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="print the recall-QPS grid and its frontier instead of the headline")
+    ap.add_argument("--sweep-codes", action="store_true",
+                    help="recall-QPS rows with the sign-code pre-filter at knobs around the "
+                         "frontier, instead of the headline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a plain 2 GiB device copy first (scale for rocprof FETCH/WRITE_SIZE)")
     a = ap.parse_args()
@@ -416,6 +464,19 @@ def main():
                                    f"{cfg['dtype']} {cfg['metric']}, {nq:,} queries, "
                                    f"D={cfg['D']}, k={k}, team={cfg['team']}"},
             "build_s": round(build_s, 2), "frontier": frontier, "rows": rows}), flush=True)
+        return
+
+    if a.sweep_codes:
+        rows, frontier, codes_s = run_code_sweep(index, Q, truth, k, cfg, nq)
+        print(json.dumps({
+            "metric": f"recall@10-QPS with the sign-code pre-filter ({a.config.upper()})",
+            "unit": "queries/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic (generated on the GPU from fixed seeds)",
+            "config": {"workload": f"{a.config.upper()}: n={n:,} x d={cfg['d']} "
+                                   f"{cfg['dtype']} {cfg['metric']}, {nq:,} queries, "
+                                   f"D={cfg['D']}, k={k}, team={cfg['team']}"},
+            "build_s": round(build_s, 2), "codes_build_s": round(codes_s, 2),
+            "frontier": frontier, "rows": rows}), flush=True)
         return
 
     if a.calibrate_copy:

@@ -200,22 +200,53 @@ __device__ __forceinline__ float team_dist_m(const float* sq, const XT* x, int d
 // alpha, <q, x> ~ alpha * <q, b> + <q, mu> and <q, b> = 2 * (sum of q over set
 // bits) - sum(q).  Lane tl of a TEAM owns code words tl, tl + TEAM, ...; each
 // lane adds q over its set bits in ascending dimension, then the team folds
-// with off = TEAM/2 .. 1.  Walking only the set bits (ctz) adds exactly the
-// terms the bit-by-bit loop adds, in the same order.  Meaningful in tl == 0.
+// with off = TEAM/2 .. 1.  Meaningful in tl == 0.
+//
+// A whole word is added branch-free: q[i] where bit i is set, +0.0 where it is
+// not, in ascending i.  acc + 0.0 == acc for every acc but -0.0 (which becomes
+// +0.0), and the sign of a zero partial changes no later sum and no estimate,
+// so this equals the set-bits-only loop bit for bit; its 32 LDS reads are
+// independent of the code, so they issue together instead of one per set bit.
+// The word that straddles dim walks its set bits below dim.
 template <int TEAM>
 __device__ __forceinline__ float team_code_ip(const float* __restrict__ sq,
                                               const int32_t* __restrict__ code, float alpha,
                                               float qmu, float qsum, int dim, int cwords,
                                               int tl) {
+    constexpr int kWords = 4;                    // code words in flight per lane
     float acc = 0.f;
-    for (int w = tl; w < cwords; w += TEAM) {
-        unsigned bits = (unsigned)code[w];
-        const int base = w * 32;
-        while (bits) {
-            const int i = base + __builtin_ctz(bits);
-            if (i >= dim) break;
-            acc = acc + sq[i];
-            bits &= bits - 1u;
+    for (int w0 = tl; w0 < cwords; w0 += kWords * TEAM) {
+        unsigned wb[kWords];
+#pragma unroll
+        for (int j = 0; j < kWords; ++j) {
+            const int w = w0 + j * TEAM;
+            wb[j] = w < cwords ? (unsigned)code[w] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kWords; ++j) {
+            const int w = w0 + j * TEAM;
+            if (w >= cwords) break;
+            unsigned bits = wb[j];
+            const int base = w * 32;
+            if (base + 32 <= dim) {
+                const float4v* s4 = reinterpret_cast<const float4v*>(sq + base);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float4v v = s4[c];
+                    const unsigned nib = bits >> (4 * c);
+                    acc = acc + ((nib & 1u) ? v[0] : 0.f);
+                    acc = acc + ((nib & 2u) ? v[1] : 0.f);
+                    acc = acc + ((nib & 4u) ? v[2] : 0.f);
+                    acc = acc + ((nib & 8u) ? v[3] : 0.f);
+                }
+                continue;
+            }
+            while (bits) {
+                const int i = base + __builtin_ctz(bits);
+                if (i >= dim) break;
+                acc = acc + sq[i];
+                bits &= bits - 1u;
+            }
         }
     }
 #pragma unroll

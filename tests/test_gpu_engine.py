@@ -416,6 +416,38 @@ def test_code_filter_matches_oracle(block):
     assert skipped > 0                      # the filter did act
 
 
+@pytest.mark.parametrize("d", [200, 96, 1024])
+def test_code_filter_word_layouts_match_oracle(d):
+    """The estimate's word handling: 200 dimensions end inside a word (the
+    straddling word walks its set bits below d), 96 gives fewer words than a
+    64-lane team has lanes, 1024 gives several four-word chunks per lane.
+    Queues and counters bit-exact against the oracle."""
+    X = gaussian(1500, d, 70 + d, True)
+    G = knn_graph(X, 24, 0)
+    codes, alpha, mu = O.build_codes(X)
+    rng = np.random.default_rng(d)
+    nq, J, L, budget = 4, 2, 16, 16
+    Qv = gaussian(nq, d, 71 + d, True)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg, Cg, Ag, Mg = to_gpu(X, G, Qv, codes, alpha, mu)
+    skipped = 0
+    for team in (4, 16, 64):
+        for margin in (0.0, 0.03):
+            note("code words", d, team, margin)
+            st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=L, B=budget, D=G.shape[1],
+                               team_size=team, stop_eps=0.1, kstop=10)
+            E.advance(Xg, Gg, Qg, st, budget, codes=(Cg, Ag, Mg, margin))
+            for qi in range(nq):
+                for j in range(J):
+                    br = O.init_branch(X, Qv[qi], [int(seeds[qi, j])], L=L, B=budget,
+                                       D=G.shape[1], team=team)
+                    O.advance_branch(X, G, Qv[qi], br, budget, budget, team=team, stop_eps=0.1,
+                                     kstop=10, codes=(codes, alpha, mu, margin))
+                    assert_queue(st, qi, j, br, ("codes", d, team, margin, qi, j))
+            skipped += int(st.counters[..., 3].sum())
+    assert skipped > 0
+
+
 def test_code_filter_with_shared_table_matches_serial_schedule():
     """Codes plus the shared table (no claims, no bound): a skipped neighbour
     leaves its claimed slot unfilled and other branches score it themselves,
