@@ -271,9 +271,9 @@ def run_sweep(index, Q, truth, k, cfg, nq):
     return rows, frontier
 
 
-CODE_KNOBS = ((64, 48, 64, 0.2), (64, 48, 128, 0.3), (32, 48, 64, 0.2), (64, 24, 64, 0.2),
-              (128, 48, 128, 0.1), (128, 48, 128, 0.2))
-CODE_MARGINS = (None, 0.02, 0.05, 0.1)
+CODE_KNOBS = ((64, 48, 64, 0.2), (64, 48, 64, 0.1), (64, 48, 128, 0.1), (64, 48, 128, 0.3),
+              (32, 48, 64, 0.2), (32, 48, 128, 0.1), (128, 48, 64, 0.1), (128, 48, 128, 0.1))
+CODE_MARGINS = (None, 0.0, 0.01, 0.02, 0.05)
 
 
 def run_code_sweep(index, Q, truth, k, cfg, nq):

@@ -49,14 +49,20 @@ constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in 
 #ifndef SWANN_CAS_FIRST
 #define SWANN_CAS_FIRST 0
 #endif
-#ifndef SWANN_PIPE2
-#define SWANN_PIPE2 0
-#endif
 constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
 constexpr size_t kMaxLds = 64 * 1024;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+
+// The query vector in LDS: every 32 floats are followed by 4 unused ones, so
+// element i sits at qpad(i).  Lanes that read the same 16-byte column of
+// different 32-float groups (the code estimate: one code word per lane, 128 B
+// apart in the plain layout) then fall in different LDS banks instead of all
+// in one; a 4- or 8-float vector never crosses a group, so the distance's
+// 16-byte reads stay contiguous.
+__host__ __device__ constexpr int qpad(int i) { return i + ((i >> 5) << 2); }
+__host__ __device__ constexpr int qpad_floats(int dim) { return ((dim + 31) >> 5) * 36; }
 
 template <typename XT> struct Vec;
 template <> struct Vec<float> { static constexpr int N = 4; };
@@ -87,6 +93,14 @@ __device__ __forceinline__ float team_dist(const float* __restrict__ sq,
     float acc = 0.f;
     if (vec_ok) {
         for (int b0 = tl * VEC; b0 < dim; b0 += STRIDE * kMaxChunks) {
+            // With STRIDE a multiple of 32 the chunks' padded offsets are one
+            // base plus constants: qpad(b0 + c*STRIDE) = qpad(b0) + c*STRIDE*36/32
+            // because c*STRIDE adds whole 32-float groups.
+            const float* qb = sq + qpad(b0);
+            auto qat = [&](int c, int base) -> const float* {
+                if constexpr (STRIDE % 32 == 0) return qb + c * (STRIDE / 32 * 36);
+                else return sq + qpad(base);
+            };
             uint4 raw[kMaxChunks];
 #pragma unroll
             for (int c = 0; c < kMaxChunks; ++c) {
@@ -99,13 +113,13 @@ __device__ __forceinline__ float team_dist(const float* __restrict__ sq,
                 if (base < dim) {
                     if constexpr (VEC == 4) {
                         const float4v xv = __builtin_bit_cast(float4v, raw[c]);
-                        const float4v qv = *reinterpret_cast<const float4v*>(sq + base);
+                        const float4v qv = *reinterpret_cast<const float4v*>(qat(c, base));
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(qv[i], xv[i]);
                     } else {
                         const half8 hv = __builtin_bit_cast(half8, raw[c]);
-                        const float4v q0 = *reinterpret_cast<const float4v*>(sq + base);
-                        const float4v q1 = *reinterpret_cast<const float4v*>(sq + base + 4);
+                        const float4v q0 = *reinterpret_cast<const float4v*>(qat(c, base));
+                        const float4v q1 = *reinterpret_cast<const float4v*>(qat(c, base) + 4);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q0[i], (float)hv[i]);
 #pragma unroll
@@ -120,72 +134,14 @@ __device__ __forceinline__ float team_dist(const float* __restrict__ sq,
         for (int base = tl * VEC; base < dim; base += STRIDE) {
 #pragma unroll
             for (int i = 0; i < VEC; ++i) {
-                if (base + i < dim) acc = acc + term<METRIC>(sq[base + i], (float)x[base + i]);
+                if (base + i < dim)
+                    acc = acc + term<METRIC>(sq[qpad(base + i)], (float)x[base + i]);
             }
         }
     }
 #pragma unroll
     for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
     return METRIC == SWANN_METRIC_IP ? 1.f - acc : acc;
-}
-
-// Two distances at once (16-byte-aligned rows, dim % VEC == 0): the loads of
-// both rows are issued before either's arithmetic, so a team keeps two rows in
-// flight.  Each row's sum adds its chunks in the same order as team_dist, so
-// both results are bit-identical to two team_dist calls.
-#ifndef SWANN_PIPE_CHUNKS
-#define SWANN_PIPE_CHUNKS 12
-#endif
-template <int TEAM, typename XT, int METRIC>
-__device__ __forceinline__ void team_dist2(const float* __restrict__ sq, const XT* __restrict__ x0,
-                                           const XT* __restrict__ x1, bool two, int dim, int tl,
-                                           float& d0, float& d1) {
-    constexpr int VEC = Vec<XT>::N;
-    constexpr int STRIDE = TEAM * VEC;
-    constexpr int K2 = SWANN_PIPE_CHUNKS;
-    float acc0 = 0.f, acc1 = 0.f;
-    auto add = [&](float& acc, const uint4& raw, int base) {
-        if constexpr (VEC == 4) {
-            const float4v xv = __builtin_bit_cast(float4v, raw);
-            const float4v qv = *reinterpret_cast<const float4v*>(sq + base);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(qv[i], xv[i]);
-        } else {
-            const half8 hv = __builtin_bit_cast(half8, raw);
-            const float4v q0 = *reinterpret_cast<const float4v*>(sq + base);
-            const float4v q1 = *reinterpret_cast<const float4v*>(sq + base + 4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q0[i], (float)hv[i]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc = acc + term<METRIC>(q1[i], (float)hv[4 + i]);
-        }
-    };
-    for (int b0 = tl * VEC; b0 < dim; b0 += STRIDE * K2) {
-        uint4 r0[K2], r1[K2];
-#pragma unroll
-        for (int c = 0; c < K2; ++c) {
-            const int base = b0 + c * STRIDE;
-            if (base < dim) {
-                r0[c] = *reinterpret_cast<const uint4*>(x0 + base);
-                if (two) r1[c] = *reinterpret_cast<const uint4*>(x1 + base);
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < K2; ++c) {
-            const int base = b0 + c * STRIDE;
-            if (base < dim) {
-                add(acc0, r0[c], base);
-                if (two) add(acc1, r1[c], base);
-            }
-        }
-    }
-#pragma unroll
-    for (int off = TEAM / 2; off > 0; off >>= 1) {
-        acc0 = acc0 + __shfl_down(acc0, off, TEAM);
-        acc1 = acc1 + __shfl_down(acc1, off, TEAM);
-    }
-    d0 = METRIC == SWANN_METRIC_IP ? 1.f - acc0 : acc0;
-    d1 = METRIC == SWANN_METRIC_IP ? 1.f - acc1 : acc1;
 }
 
 template <int TEAM, typename XT>
@@ -203,51 +159,73 @@ __device__ __forceinline__ float team_dist_m(const float* sq, const XT* x, int d
 // with off = TEAM/2 .. 1.  Meaningful in tl == 0.
 //
 // A whole word is added branch-free: q[i] where bit i is set, +0.0 where it is
-// not, in ascending i.  acc + 0.0 == acc for every acc but -0.0 (which becomes
+// not (q[i]'s bits ANDed with the bit spread to a full-word mask), in
+// ascending i.  acc + 0.0 == acc for every acc but -0.0 (which becomes
 // +0.0), and the sign of a zero partial changes no later sum and no estimate,
 // so this equals the set-bits-only loop bit for bit; its 32 LDS reads are
 // independent of the code, so they issue together instead of one per set bit.
 // The word that straddles dim walks its set bits below dim.
+//
+// A lane's words come in chunks of kCodeWords (words w0, w0 + TEAM, ...),
+// each chunk's loads issued together; the caller fetches the first chunk
+// (code_fetch) and passes it in.
+constexpr int kCodeWords = 4;
+
+template <int TEAM>
+__device__ __forceinline__ void code_fetch(const int32_t* __restrict__ code, int w0, int cwords,
+                                           unsigned* wb) {
+#pragma unroll
+    for (int j = 0; j < kCodeWords; ++j) {
+        const int w = w0 + j * TEAM;
+        wb[j] = w < cwords ? (unsigned)code[w] : 0u;
+    }
+}
+
+template <int TEAM>
+__device__ __forceinline__ float code_chunk(const float* __restrict__ sq, const unsigned* wb,
+                                            int w0, int cwords, int dim, float acc) {
+#pragma unroll
+    for (int j = 0; j < kCodeWords; ++j) {
+        const int w = w0 + j * TEAM;
+        if (w >= cwords) break;
+        unsigned bits = wb[j];
+        const int base = w * 32;
+        if (base + 32 <= dim) {
+            const float4v* s4 = reinterpret_cast<const float4v*>(sq + qpad(base));
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float4v v = s4[c];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // bit 4c+i spread over the word (one signed bitfield
+                    // extract), then q & mask: q or +0.0 without a compare
+                    const int m = (int)(bits << (31 - (4 * c + i))) >> 31;
+                    acc = acc + __int_as_float(__float_as_int(v[i]) & m);
+                }
+            }
+            continue;
+        }
+        while (bits) {
+            const int i = base + __builtin_ctz(bits);
+            if (i >= dim) break;
+            acc = acc + sq[qpad(i)];
+            bits &= bits - 1u;
+        }
+    }
+    return acc;
+}
+
+// `head` holds the lane's first chunk (code_fetch(code, tl, ...)).
 template <int TEAM>
 __device__ __forceinline__ float team_code_ip(const float* __restrict__ sq,
-                                              const int32_t* __restrict__ code, float alpha,
-                                              float qmu, float qsum, int dim, int cwords,
-                                              int tl) {
-    constexpr int kWords = 4;                    // code words in flight per lane
-    float acc = 0.f;
-    for (int w0 = tl; w0 < cwords; w0 += kWords * TEAM) {
-        unsigned wb[kWords];
-#pragma unroll
-        for (int j = 0; j < kWords; ++j) {
-            const int w = w0 + j * TEAM;
-            wb[j] = w < cwords ? (unsigned)code[w] : 0u;
-        }
-#pragma unroll
-        for (int j = 0; j < kWords; ++j) {
-            const int w = w0 + j * TEAM;
-            if (w >= cwords) break;
-            unsigned bits = wb[j];
-            const int base = w * 32;
-            if (base + 32 <= dim) {
-                const float4v* s4 = reinterpret_cast<const float4v*>(sq + base);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const float4v v = s4[c];
-                    const unsigned nib = bits >> (4 * c);
-                    acc = acc + ((nib & 1u) ? v[0] : 0.f);
-                    acc = acc + ((nib & 2u) ? v[1] : 0.f);
-                    acc = acc + ((nib & 4u) ? v[2] : 0.f);
-                    acc = acc + ((nib & 8u) ? v[3] : 0.f);
-                }
-                continue;
-            }
-            while (bits) {
-                const int i = base + __builtin_ctz(bits);
-                if (i >= dim) break;
-                acc = acc + sq[i];
-                bits &= bits - 1u;
-            }
-        }
+                                              const int32_t* __restrict__ code,
+                                              const unsigned* head, float alpha, float qmu,
+                                              float qsum, int dim, int cwords, int tl) {
+    float acc = code_chunk<TEAM>(sq, head, tl, cwords, dim, 0.f);
+    for (int w0 = tl + kCodeWords * TEAM; w0 < cwords; w0 += kCodeWords * TEAM) {
+        unsigned wb[kCodeWords];
+        code_fetch<TEAM>(code, w0, cwords, wb);
+        acc = code_chunk<TEAM>(sq, wb, w0, cwords, dim, acc);
     }
 #pragma unroll
     for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
@@ -315,6 +293,47 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int ts, int key, int
     return -1;
 }
 
+// The same probe over interleaved pairs, one 64-bit word per slot: low half
+// the id (key + 1, 0 = empty), high half the distance (FLT_MAX until the
+// claimer stores it).  An empty slot is exactly (0, FLT_MAX) -- init writes
+// that and only a claim changes the id -- so one 64-bit compare-and-swap
+// against it either claims the slot or returns what the slot holds: a found
+// key comes back with its distance in the same round trip.  Reading the id
+// and the distance in one access is one of the orders the word-by-word probe
+// allows (id, then distance).
+#ifndef SWANN_PAIR_PROBE
+#define SWANN_PAIR_PROBE 2
+#endif
+__device__ __forceinline__ int cache_slot_pair(unsigned long long* tab, int Hc, int key,
+                                               int* claimed, float* d) {
+    const unsigned mask = (unsigned)(Hc - 1);
+    unsigned pos = (2654435761u * (unsigned)key) & mask;
+    const unsigned long long empty = (unsigned long long)__float_as_uint(FLT_MAX) << 32;
+    const unsigned long long mine = empty | (unsigned)(key + 1);
+    for (int probe = 0; probe < kCprobe; ++probe) {
+        unsigned long long cur;
+#if SWANN_PAIR_PROBE == 1
+        cur = __hip_atomic_load(&tab[pos], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
+        if ((unsigned)cur == 0u)
+#endif
+        {
+            cur = empty;
+            if (__hip_atomic_compare_exchange_strong(&tab[pos], &cur, mine, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, SWANN_TABLE_SCOPE)) {
+                *claimed = 1;
+                *d = FLT_MAX;
+                return (int)pos;
+            }
+        }
+        if ((unsigned)cur == (unsigned)(key + 1)) {
+            *d = __uint_as_float((unsigned)(cur >> 32));
+            return (int)pos;
+        }
+        pos = (pos + 1) & mask;
+    }
+    return -1;
+}
+
 __device__ __forceinline__ float load_agent_f(const float* p) {
     const int b = __hip_atomic_load(reinterpret_cast<const int*>(p), __ATOMIC_RELAXED,
                                     SWANN_TABLE_SCOPE);
@@ -360,7 +379,7 @@ __global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
     const int64_t flat = xcd_remap(blockIdx.x, nb);
     const int64_t q = flat / a.J;
     const int j = (int)(flat % a.J);
-    const int dimp = (a.dim + 3) & ~3;
+    const int dimp = qpad_floats(a.dim);
     const int nsort = pow2_ge(a.V, 2, kMaxD);
 
     float* sq = reinterpret_cast<float*>(smem);
@@ -378,7 +397,7 @@ __global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
     const float* qrow = a.Qv + q * (int64_t)a.dim;
     const XT* X = reinterpret_cast<const XT*>(a.X);
 
-    for (int t = tid; t < a.dim; t += BLOCK) sq[t] = qrow[t];
+    for (int t = tid; t < a.dim; t += BLOCK) sq[qpad(t)] = qrow[t];
     if (a.H > 1) {
         if ((a.H & 3) == 0) {
             int4* v4 = reinterpret_cast<int4*>(vis);
@@ -438,7 +457,13 @@ __global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
         const int v = sd[si];
         const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
                                              a.vec_ok, a.metric);
-        if (tl == 0) { c_id[si] = v; c_d[si] = d; c_l[si] = (uint8_t)si; ++evals; }
+        // A NaN distance (NaN in the query or the row) cannot be ordered:
+        // the seed is scored but left out, so the rank sort below stays a
+        // permutation.
+        if (tl == 0) {
+            ++evals;
+            if (d == d) { c_id[si] = v; c_d[si] = d; c_l[si] = (uint8_t)si; }
+        }
     }
     block_add<BLOCK>(&s_evals, evals);
     __syncthreads();
@@ -490,7 +515,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     if (flat < 0 || flat >= a.nbranch) return;          // a bad active entry: no work
     const int64_t q = flat / a.J;
     const int L = a.L, D = a.D;
-    const int dimp = (a.dim + 3) & ~3;
+    const int dimp = qpad_floats(a.dim);
     const int nsort = pow2_ge(D, 2, kMaxD);
 
     // LDS carve-up; sizes must match advance_lds() on the host
@@ -530,7 +555,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     const float* qrow = a.Qv + q * (int64_t)a.dim;
     const XT* X = reinterpret_cast<const XT*>(a.X);
 
-    for (int t = tid; t < a.dim; t += BLOCK) sq[t] = qrow[t];
+    for (int t = tid; t < a.dim; t += BLOCK) sq[qpad(t)] = qrow[t];
     for (int i = tid; i < L; i += BLOCK) {
         qa_id[i] = a.ids[qb + i]; qa_d[i] = a.dist[qb + i];
         qa_e[i] = a.expd[qb + i]; qa_l[i] = a.lin[qb + i];
@@ -547,7 +572,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         // atomics, local_search.cu:430-441, whose order is unspecified.)
         float m = 0.f, s = 0.f;
         for (int t = lane; t < a.dim; t += 64) {
-            const float qt = sq[t];
+            const float qt = sq[qpad(t)];
             m = m + qt * a.cmu[t];
             s = s + qt;
         }
@@ -637,8 +662,11 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         const uint8_t plin = (uint8_t)s_plin;
 
         // ---- screen the neighbours, one lane each ----
+        // (a queue id is always a corpus row; the range test keeps a corrupt
+        // state from indexing the graph out of bounds)
         int nbr = 0, cov = 0;
-        for (int nidx = tid; nidx < D; nidx += BLOCK) {
+        const int deg = (p >= 0 && p < a.n) ? D : 0;
+        for (int nidx = tid; nidx < deg; nidx += BLOCK) {
             const int v = a.G[(int64_t)p * D + nidx];
             if (v < 0 || v >= a.n) continue;                 // -1 (or out of range): no edge
             ++nbr;
@@ -647,7 +675,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (!isnew) { ++cov; continue; }
             int slot = -1, claimed = 0;
             float d = FLT_MAX;
-            if (a.Hc > 0) {
+            if (a.Hc > 0 && SWANN_PAIR_PROBE && ts == 2) {
+                slot = cache_slot_pair(reinterpret_cast<unsigned long long*>(cid), a.Hc, v,
+                                       &claimed, &d);
+            } else if (a.Hc > 0) {
                 slot = cache_slot(cid, a.Hc, ts, v, &claimed);
                 d = (slot >= 0 && !claimed) ? load_agent_f(cdd + (int64_t)slot * ts) : FLT_MAX;
             }
@@ -675,43 +706,25 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (taken) ++cov;
             else { c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin; }
         };
-#if SWANN_PIPE2
-        // two work items per team in flight (no code filter: its skip
-        // decision comes between the items' loads)
-        const bool pipe = !a.codes && a.vec_ok;
-        if (pipe) {
-            for (int w = team; w < nw; w += 2 * NT) {
-                const int w1 = w + NT;
-                const bool two = w1 < nw;
-                const int v0 = w_v[w], v1 = two ? w_v[w1] : v0;
-                float d0, d1;
-                if (a.metric == SWANN_METRIC_IP)
-                    team_dist2<TEAM, XT, SWANN_METRIC_IP>(sq, X + (int64_t)v0 * a.dim,
-                                                          X + (int64_t)v1 * a.dim, two, a.dim,
-                                                          tl, d0, d1);
-                else
-                    team_dist2<TEAM, XT, SWANN_METRIC_L2>(sq, X + (int64_t)v0 * a.dim,
-                                                          X + (int64_t)v1 * a.dim, two, a.dim,
-                                                          tl, d0, d1);
-                if (tl == 0) {
-                    record(w, v0, d0);
-                    if (two) record(w1, v1, d1);
-                }
+        if (!a.codes) {
+            for (int w = team; w < nw; w += NT) {
+                const int v = w_v[w];
+                const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
+                                                     a.vec_ok, a.metric);
+                if (tl == 0) record(w, v, d);
             }
-        }
-        for (int w = pipe ? nw : team; w < nw; w += NT) {
-#else
-        for (int w = team; w < nw; w += NT) {
-#endif
-            const int v = w_v[w];
-            if (a.codes) {
-                // decide from the code before reading the row (:560-575); a
-                // skipped neighbour stays a candidate at FLT_MAX, unscored,
-                // with its table slot claimed but never filled
-                float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords, a.calpha[v],
-                                               s_qmu, s_qsum, a.dim, a.cwords, tl);
+        } else {
+            // decide from the code before reading the row (:560-575); a
+            // skipped neighbour stays a candidate at FLT_MAX, unscored, with
+            // its table slot claimed but never filled
+            const float rad = s_rad;
+            for (int w = team; w < nw; w += NT) {
+                const int v = w_v[w];
+                unsigned head[kCodeWords];
+                code_fetch<TEAM>(a.codes + (int64_t)v * a.cwords, tl, a.cwords, head);
+                float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords, head,
+                                               a.calpha[v], s_qmu, s_qsum, a.dim, a.cwords, tl);
                 est = __shfl(est, 0, TEAM);
-                const float rad = s_rad;
                 if (rad != FLT_MAX && est > rad + a.cmargin) {
                     if (tl == 0) {
                         const int nidx = w_nidx[w] & 0xffff;
@@ -720,10 +733,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                     }
                     continue;
                 }
+                const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
+                                                     a.vec_ok, a.metric);
+                if (tl == 0) record(w, v, d);
             }
-            const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
-                                                 a.vec_ok, a.metric);
-            if (tl == 0) record(w, v, d);
         }
         if (a.crowd_frac > 0.f) { block_add<BLOCK>(&s_nbr, nbr); block_add<BLOCK>(&s_cov, cov); }
         __syncthreads();
@@ -733,7 +746,9 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         for (int i = tid; i < nsort; i += BLOCK) {
             const int v = c_id[i];
             const float d = c_d[i];
-            if (v >= 0 && (worst == FLT_MAX || d <= worst)) {
+            // d == d drops a NaN distance, which has no place in the (d, id)
+            // order the rank sort and the merge rely on
+            if (v >= 0 && d == d && (worst == FLT_MAX || d <= worst)) {
                 const int k = atomicAdd(&s_nkeep, 1);
                 u_id[k] = v; u_d[k] = d; u_l[k] = c_l[i];
             }
@@ -893,17 +908,19 @@ __global__ __launch_bounds__(1024) void overflow_kernel(const int32_t* __restric
 // host side
 size_t init_lds(int dim, int V) {
     const int nsort = pow2_at_least(V, 2, kMaxD);
-    return (size_t)((dim + 3) & ~3) * 4 + (size_t)nsort * (4 + 4 + 4 + 4 + 1 + 1 + 1);
+    return (size_t)qpad_floats(dim) * 4 + (size_t)nsort * (4 + 4 + 4 + 4 + 1 + 1 + 1);
 }
 
 size_t advance_lds(int dim, int D, int L) {
     const int nsort = pow2_at_least(D, 2, kMaxD);
-    return (size_t)((dim + 3) & ~3) * 4 + (size_t)L * (4 + 4 + 4 + 4) +
+    return (size_t)qpad_floats(dim) * 4 + (size_t)L * (4 + 4 + 4 + 4) +
            (size_t)nsort * (4 * 9) + (size_t)L * 4 + (size_t)nsort * 3;
 }
 
 // The table is interleaved (id, d) pairs when cache_d is the word right after
-// cache_id: two separate [Q, Hc] arrays cannot overlap that way.
+// cache_id: two separate [Q, Hc] arrays cannot overlap that way.  Pairs are
+// probed as 64-bit words, so they must start 8-byte aligned (checked by the
+// entry points).
 int table_stride(const int32_t* cache_id, const float* cache_d, int Hc) {
     if (Hc > 0 && cache_id &&
         reinterpret_cast<const char*>(cache_d) == reinterpret_cast<const char*>(cache_id) + 4)
@@ -1039,6 +1056,9 @@ int swann_init_states(const void* X, int x_dtype, int64_t n, int dim, const floa
     SWANN_REQUIRE(Q == 0 || (X && Qv && seeds && ids && dist && expd && lin && visited && counters),
                   "init_states: a required pointer is NULL");
     SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "init_states: Hc > 0 needs cache_id and cache_d");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) == 1 ||
+                      (reinterpret_cast<uintptr_t>(cache_id) & 7) == 0,
+                  "init_states: an interleaved (id, d) table must be 8-byte aligned");
     if (Q == 0) return SWANN_OK;
     InitArgs a{X, Qv, seeds, ids, dist, expd, lin, visited, counters, dim, J, V, L, H, metric,
                Q, n, Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound,
@@ -1067,6 +1087,9 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
     SWANN_REQUIRE(Q == 0 || (X && G && Qv && ids && dist && expd && lin && visited && counters),
                   "advance: a required pointer is NULL");
     SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "advance: Hc > 0 needs cache_id and cache_d");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) == 1 ||
+                      (reinterpret_cast<uintptr_t>(cache_id) & 7) == 0,
+                  "advance: an interleaved (id, d) table must be 8-byte aligned");
     SWANN_REQUIRE(!exclusive || Hc > 0, "advance: exclusive claims need the shared table");
     const int64_t nb = active ? nactive : Q * J;
     if (nb == 0 || delta <= 0) return SWANN_OK;
