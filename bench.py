@@ -64,6 +64,7 @@ PMC_TRAFFIC = {
     ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "6d609080657bb8e5"): 5.620e12,
     ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "6d609080657bb8e5"): 5.635e12,
     ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "5f8609651dd61c31"): 5.640e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "88261fdb3ebbf2da"): 5.410e12,
 }
 
 
@@ -271,6 +272,9 @@ def run_sweep(index, Q, truth, k, cfg, nq):
     return rows, frontier
 
 
+# (branches, queue, budget, stop_eps, margin): the fastest recall@10 >= 0.95 row
+# of `--sweep-codes` on C3
+CODES_POINT = (64, 48, 128, 0.1, 0.05)
 CODE_KNOBS = ((64, 48, 64, 0.2), (64, 48, 64, 0.1), (64, 48, 128, 0.1), (64, 48, 128, 0.3),
               (32, 48, 64, 0.2), (32, 48, 128, 0.1), (128, 48, 64, 0.1), (128, 48, 128, 0.1))
 CODE_MARGINS = (None, 0.0, 0.01, 0.02, 0.05)
@@ -402,7 +406,9 @@ def main():
     ap.add_argument("--eps", type=float, default=None, help="skip the sweep, use this stop_eps")
     ap.add_argument("--knobs", default=None,
                     help="branches,queue,budget,stop_eps: skip the operating-point search")
-    ap.add_argument("--cpu-sample", type=int, default=200)
+    ap.add_argument("--cpu-sample", type=int, default=500)
+    ap.add_argument("--no-codes", action="store_true",
+                    help="skip the sign-code pre-filter line reported beside the headline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="print the recall-QPS grid and its frontier instead of the headline")
@@ -563,6 +569,32 @@ def main():
         except Exception as e:                                   # noqa: BLE001
             log(f"cpu baseline failed: {e}")
 
+    # the same workload with the sign-code pre-filter at its frontier point;
+    # reported beside the headline, which is the Index.search path (no codes knob)
+    with_codes = None
+    if cfg["metric"] == "ip" and not a.no_codes:
+        from swann_amd import codes as C
+        cd, al, mu = C.build_codes(index.X)
+        J, L, Bud, ceps, margin = CODES_POINT
+        cs = Searcher(index, Q, k, dict(cfg, branches=J, queue=L, budget=Bud))
+        cs.codes = (cd, al, mu, margin)
+        cs.step(ceps)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            ids_c, _, st_c = cs.step(ceps)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t1)
+        with_codes = dict(branches=J, queue=L, budget=Bud, stop_eps=ceps, margin=margin,
+                          recall_at_10=round(recall(ids_c, truth, k), 4),
+                          qps=round(nq / float(np.median(times)), 1),
+                          rows_read_per_query=round(float(st_c.dist_evals.sum()) / nq, 1),
+                          path="engine search with codes=(codes, alpha, mu, margin) "
+                               "(swann/_engine.py:281-317, local_search.cu:205-243)")
+        log(f"with codes {with_codes}")
+        del cs, cd, al, mu
+
     out = {
         "metric": "QPS at recall@10=0.95 (1 GPU) + achieved HBM GB/s fraction; build s/1M rows",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
@@ -587,6 +619,7 @@ def main():
                      "kernel": "advance_kernel",
                      "bytes_per_launch": adv_bytes, "launch_ms": round(adv_s * 1e3, 3)},
         "cpu_baseline": cpu,
+        "with_codes": with_codes,
     }
     print(json.dumps(out), flush=True)
 

@@ -70,7 +70,9 @@ int swann_device_count(void);
  *            or one [Q, Hc, 2] allocation of (id, d) pairs, passed as
  *            cache_id = its start and cache_d = cache_id + 1 word (the
  *            kernels detect that adjacency and stride by 2; a claim and the
- *            distance stored into it then share a cache line)
+ *            distance stored into it then share a cache line, and a slot is
+ *            probed as one 64-bit word, so the pairs must start 8-byte
+ *            aligned -- SWANN_E_INVALID otherwise)
  *   bound    [Q] fp32 or NULL
  * A disabled feature is a NULL pointer (and Hc = 0), matching the
  * reference's empty-tensor convention (swann/_engine.py:269-274).
