@@ -135,3 +135,25 @@ def test_no_oracle_in_the_product():
     for f in (ROOT / "swann_amd").rglob("*.py"):
         text = f.read_text()
         assert "import oracle" not in text and "from oracle" not in text, f
+
+
+def test_interleaved_table_must_be_8_byte_aligned():
+    """An interleaved (id, d) table is probed as 64-bit words: a start that is
+    only 4-byte aligned is refused before anything runs (Q = 0: no launch, no
+    GPU needed); an aligned one, and separate arrays, pass."""
+    L = _lib.lib()
+
+    def init(cid, cdd):
+        return L.swann_init_states(None, 0, 1000, 128, None, 0, None, 2, 1, None, None, None,
+                                   None, 16, None, 1, None, 0, 16, cid, cdd, 1024, None, None)
+
+    def adv(cid, cdd):
+        return L.swann_advance(None, 0, 1000, 128, None, 32, None, 0, 2, None, None, None, None,
+                               16, None, 1, None, 0, 16, 4, 4, 0, 1, 0.0, 10, cid, cdd, 1024,
+                               None, 0, 0, 0.0, None, 0, None, 0, None, None, 0.0, None)
+
+    base = 0x10000
+    for fn in (init, adv):
+        assert fn(base + 4, base + 8) != 0 and "8-byte aligned" in _err()
+        assert fn(base, base + 4) == 0                       # aligned pairs
+        assert fn(base + 4, base + 0x8000) == 0              # separate arrays
