@@ -23,8 +23,10 @@ namespace swann {
 
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype);
 int sweep_mfma_cap(int C);
+int sweep_mfma_splits(int64_t n, int dim);
 int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
-                   float* bkey, int32_t* bid, int32_t* bcnt, char* extra, hipStream_t st);
+                   int splits, float* bkey, int32_t* bid, int32_t* bcnt, char* extra,
+                   hipStream_t st, int* used);
 
 namespace {
 
@@ -216,23 +218,33 @@ __global__ __launch_bounds__(256) void sweep_kernel(SweepArgs a) {
     if (tid < kRT && r0 + tid < a.n) a.bcnt[r0 + tid] = cnt[tid];
 }
 
-// Sort each row's survivors and emit the first C.
+// Sort each row's survivors and emit the first C.  A row has G lists
+// (column splits of the sweep) of up to `cap` entries at (r * G + s) * cap;
+// they are gathered in split order and sorted together.
 __global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bkey,
                                                    const int32_t* __restrict__ bid,
                                                    const int32_t* __restrict__ bcnt, int64_t n,
-                                                   int cap, int C, int32_t* __restrict__ cand,
+                                                   int cap, int G, int C, int pad_self,
+                                                   int32_t* __restrict__ cand,
                                                    float* __restrict__ cdist) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int64_t r = blockIdx.x;
-    const int cnt = bcnt[r];
+    int segc[8], cnt = 0;
+    for (int sg = 0; sg < 8; ++sg) {
+        segc[sg] = sg < G ? bcnt[r * G + sg] : 0;
+        cnt += segc[sg];
+    }
     int np = 2;
     while (np < cnt) np <<= 1;
     float* sd = reinterpret_cast<float*>(smem);
     int* si = reinterpret_cast<int*>(sd + np);
     for (int i = threadIdx.x; i < np; i += 256) {
+        int sg = 0, off = i;
+        while (sg < G - 1 && off >= segc[sg]) { off -= segc[sg]; ++sg; }
         const bool real = i < cnt;
-        sd[i] = real ? bkey[r * cap + i] : INFINITY;
-        si[i] = real ? bid[r * cap + i] : INT32_MAX;
+        const int64_t at = (r * G + sg) * (int64_t)cap + off;
+        sd[i] = real ? bkey[at] : INFINITY;
+        si[i] = real ? bid[at] : INT32_MAX;
     }
     __syncthreads();
     for (int size = 2; size <= np; size <<= 1)
@@ -249,10 +261,14 @@ __global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bke
             }
             __syncthreads();
         }
+    // pad_self: the sweep left self out of the lists; it is the row's
+    // candidate at 3.4e38 after every real one (swann/build.py:28-43 sets the
+    // self score so), so it takes position cnt when the row has fewer than C
     for (int t = threadIdx.x; t < C; t += 256) {
         const bool ok = t < cnt;
-        cand[r * C + t] = ok ? si[t] : -1;
-        cdist[r * C + t] = ok ? sd[t] : INFINITY;
+        const bool self = pad_self && t == cnt;
+        cand[r * C + t] = ok ? si[t] : self ? (int32_t)r : -1;
+        cdist[r * C + t] = ok ? sd[t] : self ? kSelf : INFINITY;
     }
 }
 
@@ -686,7 +702,8 @@ extern "C" {
 int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C) {
     const int Cs = screen_count(C, n, x_dtype, dim);
     const int cap = use_mfma(dim) ? sweep_mfma_cap(Cs) : sweep_cap(C);
-    int64_t b = align256(n * 4) + align256(n * (int64_t)cap * 4) * 2 + align256(n * 4);
+    const int64_t G = use_mfma(dim) ? sweep_mfma_splits(n, dim) : 1;
+    int64_t b = align256(n * 4) + align256(n * G * cap * 4) * 2 + align256(n * G * 4);
     if (Cs != C) b += align256(n * (int64_t)Cs * 4) * 2;
     if (use_mfma(dim)) b += sweep_mfma_extra_bytes(n, dim, x_dtype);
     return b;
@@ -709,11 +726,12 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     const int Cs = screen_count(C, n, x_dtype, dim);
     SWANN_REQUIRE(Cs == C || dim * 4 <= 64 * 1024, "sweep: dimension too large for the re-rank");
     const int cap = mf ? sweep_mfma_cap(Cs) : sweep_cap(C);
+    const int G = mf ? sweep_mfma_splits(n, dim) : 1;
     char* ws = (char*)workspace;
     float* xn = (float*)ws; ws += align256(n * 4);
-    float* bkey = (float*)ws; ws += align256(n * (int64_t)cap * 4);
-    int32_t* bid = (int32_t*)ws; ws += align256(n * (int64_t)cap * 4);
-    int32_t* bcnt = (int32_t*)ws; ws += align256(n * 4);
+    float* bkey = (float*)ws; ws += align256(n * (int64_t)G * cap * 4);
+    int32_t* bid = (int32_t*)ws; ws += align256(n * (int64_t)G * cap * 4);
+    int32_t* bcnt = (int32_t*)ws; ws += align256(n * (int64_t)G * 4);
     int32_t* scand = nullptr;
     float* scd = nullptr;
     if (Cs != C) {
@@ -722,8 +740,10 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     }
     char* extra = ws;
     int rc;
+    int Gu = 1;                      // lists per row the sweep filled
     if (mf) {
-        rc = sweep_mfma_run(X, x_dtype, n, dim, metric, Cs, cap, bkey, bid, bcnt, extra, st);
+        rc = sweep_mfma_run(X, x_dtype, n, dim, metric, Cs, cap, G, bkey, bid, bcnt, extra, st,
+                            &Gu);
     } else {
         const unsigned nb = (unsigned)((n + 3) / 4);
         if (metric == SWANN_METRIC_L2)
@@ -738,15 +758,17 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
         rc = launch_status("sweep");
     }
     if (rc) return rc;
+    // one list holds up to cap; G > 1 lists were each cut to Cs by the sweep
+    const int most = Gu > 1 ? Gu * Cs : cap;
     int np = 2;
-    while (np < cap) np <<= 1;
+    while (np < most) np <<= 1;
     if (Cs == C) {
         hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
-                           bcnt, n, cap, C, cand, cdist);
+                           bcnt, n, cap, Gu, C, mf ? 1 : 0, cand, cdist);
         return launch_status("sweep final");
     }
     hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
-                       bcnt, n, cap, Cs, scand, scd);
+                       bcnt, n, cap, Gu, Cs, mf ? 1 : 0, scand, scd);
     rc = launch_status("sweep final");
     if (rc) return rc;
     // exact fp32 re-rank of the screened lists; the norms are the sweep's

@@ -16,6 +16,7 @@
 #include <float.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -29,6 +30,7 @@ constexpr int kBK = 32;
 constexpr int kPad = 8;                       // fp16 elements of padding per LDS row
 constexpr int kLdsRow = kBK + kPad;           // 40 halves = 80 bytes
 constexpr float kSelf = 3.4e38f;
+constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;   // workgroup tile rows, columns; threads
 
 __device__ __forceinline__ uint32_t fkey(float f) {
     const uint32_t b = __float_as_uint(f);
@@ -100,6 +102,7 @@ struct MfmaSweepArgs {
     int64_t n; int dim; int metric; int C; int cap;
     float* bkey; int32_t* bid; int32_t* bcnt;
     int scaled;                  // rows carry a power-of-two scale (fp32 corpus)
+    int splits;                  // column splits G: row r's buffer s is (r * G + s) * cap
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -159,52 +162,76 @@ __device__ void compact_row_w(float* key, int32_t* id, int cnt, int C, float* th
 
 
 // Epilogue for one 32 x 32 accumulator block: lane holds column c and the 16
-// rows rbase + (e/4)*8 + (e%4).  Thresholds and row norms are read as four
-// 16-byte LDS vectors, all 16 distances are tested into a mask, and only a
-// wave with a survivor takes the append path.  Rows past n carry a -inf
-// threshold, so they never pass.
+// rows rbase + (e/4)*8 + (e%4).  The common case -- no score of the block
+// beats its row's threshold -- costs the distance formula and one compare per
+// score, the "any" kept as a lane mask, one row group (4 rows: threshold,
+// norms, scales) live at a time; only a block with a survivor recomputes its
+// distances from fresh LDS reads and appends.  Rows past n carry a -inf
+// threshold, so they never pass.  Self scores were set to -inf in the
+// accumulator (self_out), so their distance is +inf and never passes; the
+// merge adds self back at kSelf where a row has fewer than C others.
 template <int METRIC>
 __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64_t r0, int64_t c,
-                                               bool cok, bool diag, float cn, float sc,
-                                               const float* rs, const float* thr,
-                                               const float* rnorm, int* cnt,
-                                               const MfmaSweepArgs& a, int nterm_scale,
-                                               const f32x16* vx) {
-    float4 th[4], rn[4], rsc[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        th[g] = *reinterpret_cast<const float4*>(thr + rbase + g * 8);
-        if (METRIC == SWANN_METRIC_L2) rn[g] = *reinterpret_cast<const float4*>(rnorm + rbase + g * 8);
-        if (nterm_scale) rsc[g] = *reinterpret_cast<const float4*>(rs + rbase + g * 8);
-    }
-    unsigned mask = 0;
-    float dv[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int g = e >> 2, q = e & 3;
+                                               bool cok, float cn, float sc, const float* rs,
+                                               const float* thr, const float* rnorm, int* cnt,
+                                               const MfmaSweepArgs& a, int split, int nterm_scale,
+                                               const f32x16* vx, int* needf = nullptr) {
+    auto dist = [&](int e, const float4& r4, const float4& s4) {
+        const int q = e & 3;
         float dot;
         if (nterm_scale == 1)
-            dot = rsc[g][q] * sc * (v[e] + (*vx)[e] * (1.0f / 2048.0f));
+            dot = s4[q] * sc * (v[e] + (*vx)[e] * (1.0f / 2048.0f));
         else if (nterm_scale == 2)
-            dot = rsc[g][q] * sc * v[e];
+            dot = s4[q] * sc * v[e];
         else
             dot = v[e];
-        float d = dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? rn[g][q] : 0.f, cn);
-        if (diag && c == r0 + rbase + g * 8 + q) d = kSelf;
-        dv[e] = d;
-        mask |= (d < th[g][q]) ? (1u << e) : 0u;
+        return dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? r4[q] : 0.f, cn);
+    };
+    auto group = [&](int g, float4& t4, float4& r4, float4& s4) {
+        t4 = *reinterpret_cast<const float4*>(thr + rbase + g * 8);
+        r4 = METRIC == SWANN_METRIC_L2 ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        s4 = nterm_scale ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                         : make_float4(1.f, 1.f, 1.f, 1.f);
+    };
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float4 t4, r4, s4;
+        group(g, t4, r4, s4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) any = any || (dist(g * 4 + q, r4, s4) < t4[q]);
     }
-    if (!cok) mask = 0;
-    if (__ballot(mask != 0) == 0ull) return;
-    while (mask) {
-        const int e = __builtin_ctz(mask);
-        mask &= mask - 1;
-        const int rl = rbase + (e >> 2) * 8 + (e & 3);
-        const int p = atomicAdd(&cnt[rl], 1);
-        const int64_t o = (r0 + rl) * (int64_t)a.cap + p;
-        a.bkey[o] = dv[e];
-        a.bid[o] = (int32_t)c;
+    any = any && cok;
+    if (__ballot(any) == 0ull) return;
+    asm volatile("" ::: "memory");           // rare path: reload rather than keep live
+    if (!any) return;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float4 t4, r4, s4;
+        group(g, t4, r4, s4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float d = dist(g * 4 + q, r4, s4);
+            if (!(d < t4[q])) continue;
+            const int rl = rbase + g * 8 + q;
+            const int p = atomicAdd(&cnt[rl], 1);
+            // the append that leaves less than a tile of room flags a compaction
+            if (needf && p == a.cap - kBN2) *needf = 1;
+            const int64_t o = ((r0 + rl) * a.splits + split) * (int64_t)a.cap + p;
+            a.bkey[o] = d;
+            a.bid[o] = (int32_t)c;
+        }
     }
+}
+
+// On the diagonal tile, the score of each row against itself becomes -inf
+// (its distance +inf), so the epilogue never takes it.  Lane holds column
+// ccol (offset in the tile) and rows rbase + (e/4)*8 + (e%4).
+__device__ __forceinline__ void self_out(f32x16& v, int rbase, int ccol) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        if (ccol == rbase + (e >> 2) * 8 + (e & 3)) v[e] = -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -214,7 +241,6 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
 // workgroup's work is one stream of (column tile, K tile) steps: global loads
 // run two steps ahead in two register stages, LDS is double-buffered with one
 // barrier per step, and a column tile's epilogue overlaps the next tile's loads.
-constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;
 
 struct Stage { f16x8 a[2], b[2]; };
 
@@ -356,8 +382,9 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
                 for (int i = 0; i < 4; ++i) {
                     int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
                     asm volatile("" : "+v"(rbase));
-                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], cs[j],
-                                           rscale, thr, rnorm, cnt, a, SCALED ? 2 : 0, nullptr);
+                    if (diag) self_out(acc[i][j], rbase, wn * 64 + j * 32 + (lane & 31));
+                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j], rscale,
+                                           thr, rnorm, cnt, a, 0, SCALED ? 2 : 0, nullptr);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -368,7 +395,7 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
                 for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
                     const int64_t r = r0 + rl;
                     if (r < n && cnt[rl] > a.cap - kBN2)
-                        compact_row_w(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C,
+                        compact_row_w(a.bkey + r * a.splits * a.cap, a.bid + r * a.splits * a.cap, cnt[rl], a.C,
                                       &thr[rl], &cnt[rl]);
                 }
                 __syncthreads();
@@ -381,7 +408,7 @@ __global__ __launch_bounds__(512, 1) void sweep_mfma256_kernel(MfmaSweepArgs a) 
         step(t, S1);
         if (t + 1 < nsteps) step(t + 1, S0);
     }
-    if (tid < kBM2 && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
+    if (tid < kBM2 && r0 + tid < n) a.bcnt[(r0 + tid) * a.splits] = cnt[tid];
 }
 
 // ---------------------------------------------------------------------------
@@ -421,7 +448,7 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     __shared__ int cnt[kBM2];
     __shared__ __align__(16) float rnorm[kBM2];
     __shared__ __align__(16) float rscale[kBM2];
-    __shared__ int need;
+    __shared__ int need[2];      // set by the appends of column tiles of that parity
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -429,7 +456,13 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     const int64_t n = a.n;
     const int dim = a.dim;
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
-    const int64_t r0 = xcd_remap(blockIdx.x, ntile) * kBM2;
+    // G workgroups share a row panel, each taking 1/G of the column tiles;
+    // xcd_remap gives consecutive logical ids to one XCD, so the G readers of
+    // a panel run together on one L2
+    const int G = a.splits;
+    const int64_t lid = xcd_remap(blockIdx.x, ntile * G);
+    const int64_t r0 = (lid / G) * kBM2;
+    const int split = (int)(lid % G);
 
     if (tid < kBM2) {
         thr[tid] = r0 + tid < n ? INFINITY : -INFINITY;
@@ -437,7 +470,7 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
         if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
     }
-    if (tid == 0) need = 0;
+    if (tid < 2) need[tid] = 0;
 
     // direct-load assignment: instruction j of this wave fills rows
     // 8 (4 wave + j) .. + 7 of the stage; this lane fetches one 16-byte chunk
@@ -452,7 +485,8 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     }
     const int nk = dim / kBK3;
     const int64_t nct = (n + kBN2 - 1) / kBN2;
-    const int64_t nsteps = nct * nk;
+    const int64_t ct0 = nct * split / G, ct1 = nct * (split + 1) / G;
+    const int64_t nsteps = (ct1 - ct0) * nk;
     const _Float16* X = a.hi;
 
     auto issue = [&](int64_t t, int kt, int64_t cb) {
@@ -478,11 +512,12 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     for (int j = 0; j < 2; ++j) bro[j] = (wn * 64 + j * 32 + (lane & 31)) * kRowBytes;
 
     int kt_c = 0, kt_f = 0;
-    int64_t cb_c = 0, cb_f = 0;
+    int64_t cb_c = ct0 * kBN2, cb_f = ct0 * kBN2;
     auto adv = [&](int& kt, int64_t& cb) {
         if (++kt == nk) { kt = 0; cb += kBN2; }
     };
     f32x16 acc[4][2];
+    int tpar = 0;                    // parity of the current column tile (its need flag)
     issue(0, kt_f, cb_f);
     adv(kt_f, cb_f);
 
@@ -506,6 +541,23 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         __syncthreads();                                // every wave's stage-t loads have landed
         issue(t + 1, kt_f, cb_f);
         adv(kt_f, cb_f);
+        if (kt == 0 && t > 0) {
+            // compaction flagged by the previous column tile's appends; the
+            // flag was set before the barrier above, so every wave reads the
+            // same value, and it is cleared only after every wave has read it
+            const int par = tpar ^ 1;    // the tile that just ended
+            if (need[par]) {
+                for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+                    const int64_t r = r0 + rl;
+                    if (r < n && cnt[rl] > a.cap - kBN2)
+                        compact_row_w(a.bkey + (r * G + split) * a.cap,
+                                      a.bid + (r * G + split) * a.cap, cnt[rl], a.C, &thr[rl],
+                                      &cnt[rl]);
+                }
+                __syncthreads();
+                if (tid == 0) need[par] = 0;
+            }
+        }
         if (kt == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -548,29 +600,30 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
                 for (int i = 0; i < 4; ++i) {
                     int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
                     asm volatile("" : "+v"(rbase));
-                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, diag, cn[j], cs[j],
-                                           rscale, thr, rnorm, cnt, a, SCALED ? 2 : 0, nullptr);
+                    if (diag) self_out(acc[i][j], rbase, wn * 64 + j * 32 + (lane & 31));
+                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j], rscale,
+                                           thr, rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
+                                           &need[tpar]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            __syncthreads();
-            if (tid < kBM2 && cnt[tid] > a.cap - kBN2) atomicOr(&need, 1);
-            __syncthreads();
-            if (need) {
-                for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
-                    const int64_t r = r0 + rl;
-                    if (r < n && cnt[rl] > a.cap - kBN2)
-                        compact_row_w(a.bkey + r * a.cap, a.bid + r * a.cap, cnt[rl], a.C,
-                                      &thr[rl], &cnt[rl]);
-                }
-                __syncthreads();
-                if (tid == 0) need = 0;
-            }
+            tpar ^= 1;
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (tid < kBM2 && r0 + tid < n) a.bcnt[r0 + tid] = cnt[tid];
+    if (G > 1) {
+        // each split leaves at most C per row, so the merge of the G lists
+        // sorts at most G * C
+        for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+            const int64_t r = r0 + rl;
+            if (r < n && cnt[rl] > a.C)
+                compact_row_w(a.bkey + (r * G + split) * a.cap, a.bid + (r * G + split) * a.cap,
+                              cnt[rl], a.C, &thr[rl], &cnt[rl]);
+        }
+        __syncthreads();
+    }
+    if (tid < kBM2 && r0 + tid < n) a.bcnt[(r0 + tid) * G + split] = cnt[tid];
 }
 
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
@@ -580,8 +633,12 @@ inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 // Runs the MFMA sweep into the row buffers (bkey/bid/bcnt); the caller sorts.
 // fp16 rows: exact products, one term.  fp32 rows: one fp16 term of the
 // power-of-two-scaled rows (a screen; the caller re-ranks the survivors in fp32).
+// The buffers hold `splits` lists of `cap` per row (sweep_mfma_splits); *used
+// returns how many the launched kernel filled (the register-staged kernel
+// fills one), which is what the merge must read.
 int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
-                   float* bkey, int32_t* bid, int32_t* bcnt, char* extra, hipStream_t st) {
+                   int splits, float* bkey, int32_t* bid, int32_t* bcnt, char* extra,
+                   hipStream_t st, int* used) {
     float* xn = (float*)extra; extra += al256(n * 4);
     float* scale = (float*)extra; extra += al256(n * 4);
     const _Float16* hi;
@@ -596,10 +653,14 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                            (const float*)X, n, dim, h, (_Float16*)nullptr, scale, xn);
         hi = h;
     }
-    MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled};
+    MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled, 1};
     const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
     const bool ip = metric == SWANN_METRIC_IP;
+    *used = 1;
     if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
+        a.splits = splits;
+        *used = splits;
+        const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2 * splits);
         if (scaled) {
             if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
             else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
@@ -623,6 +684,25 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
     return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2);
+}
+
+// Column splits of the direct-load sweep: enough workgroups to give every
+// CU one (small n), and at least kMinSplits so that row panels are read from
+// L2 more than once.  SWANN_SWEEP_SPLIT=1|2|4|8 pins it.
+#ifndef SWANN_SWEEP_MIN_SPLITS
+#define SWANN_SWEEP_MIN_SPLITS 2
+#endif
+int sweep_mfma_splits(int64_t n, int dim) {
+    if (dim % kBK3 != 0) return 1;
+    const char* e = getenv("SWANN_SWEEP_SPLIT");
+    if (e && *e) {
+        const int g = atoi(e);
+        return g == 2 || g == 4 || g == 8 ? g : 1;
+    }
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    int g = SWANN_SWEEP_MIN_SPLITS;
+    while (g < 8 && ntile * g < 512) g *= 2;
+    return g;
 }
 
 int sweep_mfma_cap(int C) {

@@ -201,6 +201,29 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
 
 
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_mfma_sweep_self_is_last_when_candidates_cover_the_corpus(metric, dtype):
+    """C = n: every other row is a candidate and self comes last at 3.4e38
+    (build.py:39 sets the self score so).  n = 48 is one row panel, so most
+    of the sweep's column splits receive no column tile."""
+    n, d = 48, 64
+    X = gaussian(n, d, 411 + metric, metric == 0)
+    if dtype == "f16":
+        X = X.astype(np.float16)
+    Xg = torch.from_numpy(X).cuda()
+    note("mfma sweep C = n", dtype, metric)
+    cand, cdist = B.knn_candidates(Xg, n, metric="ip" if metric == 0 else "l2")
+    oc, od = O.knn_candidates(X.astype(np.float32), n, metric, nthreads=8)
+    c = cand.cpu().numpy()
+    assert (c[:, -1] == np.arange(n)).all()
+    assert (cdist.cpu().numpy()[:, -1] == np.float32(3.4e38)).all()
+    assert (oc[:, -1] == np.arange(n)).all()
+    for r in range(n):
+        assert sorted(c[r, :-1].tolist()) == sorted(set(range(n)) - {r})
+    assert (c == oc).mean() > 0.99
+
+
 def test_captured_search_replays_exactly():
     """The whole search path under hipGraph capture (selection, seed gather,
     init, advance, top-k, merge, overflow count), in a deterministic
