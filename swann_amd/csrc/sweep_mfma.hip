@@ -440,8 +440,17 @@ __device__ __forceinline__ void dma16(const _Float16* g, unsigned char* lds) {
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_vptr)lds, 16, 0, 0);
 }
 
-template <int METRIC, int SCALED>
-__global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
+// WAVES = 8: two waves per SIMD with 128 x 64 wave tiles (128 accumulators);
+// WAVES = 16: four waves per SIMD with 64 x 64 wave tiles (64 accumulators),
+// which leaves the registers to keep fragment reads ahead of their MFMAs and
+// twice the waves to cover one another's LDS and barrier waits.
+template <int METRIC, int SCALED, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
+    constexpr int WR = WAVES == 16 ? 4 : 2;    // waves down the 256 rows
+    constexpr int WN = WAVES / WR;             // waves across the 256 columns
+    constexpr int RW = kBM2 / WR, CW = kBN2 / WN;   // wave tile
+    constexpr int BI = RW / 32, BJ = CW / 32;  // 32 x 32 blocks per wave
+    constexpr int NQ = 32 / WAVES;             // 1 KB direct loads per wave per operand
     __shared__ __align__(16) unsigned char sA[2][kStage];
     __shared__ __align__(16) unsigned char sB[2][kStage];
     __shared__ __align__(16) float thr[kBM2];
@@ -452,7 +461,7 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;           // rows wm*128.., cols wn*64..
+    const int wm = wave / WN, wn = wave % WN;          // rows wm*RW.., cols wn*CW..
     const int64_t n = a.n;
     const int dim = a.dim;
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
@@ -474,11 +483,11 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
 
     // direct-load assignment: instruction j of this wave fills rows
     // 8 (4 wave + j) .. + 7 of the stage; this lane fetches one 16-byte chunk
-    int lrow[4], lchunk[4];
-    int64_t aoff[4];
+    int lrow[NQ], lchunk[NQ];
+    int64_t aoff[NQ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        lrow[j] = (wave * 4 + j) * 8 + (lane >> 3);
+    for (int j = 0; j < NQ; ++j) {
+        lrow[j] = (wave * NQ + j) * 8 + (lane >> 3);
         lchunk[j] = ((lane & 7) ^ swz(lrow[j])) * 8;
         const int64_t r = r0 + lrow[j] < n ? r0 + lrow[j] : n - 1;
         aoff[j] = r * (int64_t)dim + lchunk[j];
@@ -494,8 +503,8 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         const int buf = (int)(t & 1);
         const int k0 = kt * kBK3;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int q = wave * 4 + j;
+        for (int j = 0; j < NQ; ++j) {
+            const int q = wave * NQ + j;
             dma16(X + aoff[j] + k0, &sA[buf][q * 1024]);
             const int64_t rb = cb + lrow[j] < n ? cb + lrow[j] : n - 1;
             dma16(X + rb * (int64_t)dim + lchunk[j] + k0, &sB[buf][q * 1024]);
@@ -505,18 +514,18 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     // fragment addresses: row r's logical chunk c sits at r*128 + ((c ^ swz(r)) * 16);
     // the fragment rows are (multiple of 32) + lane % 32, so swz is per lane
     const int fsw = swz(lane & 31);
-    int aro[4], bro[2];
+    int aro[BI], bro[BJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) aro[i] = (wm * 128 + i * 32 + (lane & 31)) * kRowBytes;
+    for (int i = 0; i < BI; ++i) aro[i] = (wm * RW + i * 32 + (lane & 31)) * kRowBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bro[j] = (wn * 64 + j * 32 + (lane & 31)) * kRowBytes;
+    for (int j = 0; j < BJ; ++j) bro[j] = (wn * CW + j * 32 + (lane & 31)) * kRowBytes;
 
     int kt_c = 0, kt_f = 0;
     int64_t cb_c = ct0 * kBN2, cb_f = ct0 * kBN2;
     auto adv = [&](int& kt, int64_t& cb) {
         if (++kt == nk) { kt = 0; cb += kBN2; }
     };
-    f32x16 acc[4][2];
+    f32x16 acc[BI][BJ];
     int tpar = 0;                    // parity of the current column tile (its need flag)
     issue(0, kt_f, cb_f);
     adv(kt_f, cb_f);
@@ -528,11 +537,13 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         const int buf = (int)(t & 1);
         // column norms/scales of a finishing tile, issued before the next
         // stage's loads so the epilogue's wait does not include them
-        float cn[2] = {0.f, 0.f}, cs[2] = {1.f, 1.f};
+        float cn[BJ], cs[BJ];
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) { cn[j] = 0.f; cs[j] = 1.f; }
         if (kt == nk - 1) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int64_t c = cbt + wn * 64 + j * 32 + (lane & 31);
+            for (int j = 0; j < BJ; ++j) {
+                const int64_t c = cbt + wn * CW + j * 32 + (lane & 31);
                 if (METRIC == SWANN_METRIC_L2) cn[j] = c < n ? a.xn[c] : 0.f;
                 if (SCALED) cs[j] = c < n ? a.scale[c] : 1.f;
             }
@@ -547,7 +558,7 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
             // same value, and it is cleared only after every wave has read it
             const int par = tpar ^ 1;    // the tile that just ended
             if (need[par]) {
-                for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+                for (int rl = wave; rl < kBM2; rl += WAVES) {
                     const int64_t r = r0 + rl;
                     if (r < n && cnt[rl] > a.cap - kBN2)
                         compact_row_w(a.bkey + (r * G + split) * a.cap,
@@ -560,20 +571,20 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         }
         if (kt == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < BI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
+                for (int j = 0; j < BJ; ++j) acc[i][j] = (f32x16){};
         }
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
-        f16x8 fa[2][4], fb[2][2];
+        f16x8 fa[2][BI], fb[2][BJ];
         auto fload = [&](int sub, int slot) {
             const int co = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < BI; ++i)
                 fa[slot][i] = *reinterpret_cast<const f16x8*>(pA + aro[i] + co);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < BJ; ++j)
                 fb[slot][j] = *reinterpret_cast<const f16x8*>(pB + bro[j] + co);
         };
         fload(0, 0);
@@ -581,9 +592,9 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
         for (int sub = 0; sub < 4; ++sub) {
             if (sub < 3) fload(sub + 1, (sub + 1) & 1);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < BI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < BJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[sub & 1][i],
                                                                       fb[sub & 1][j], acc[i][j],
                                                                       0, 0, 0);
@@ -593,14 +604,14 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
             const int64_t cb = cbt;
             const bool diag = (cb == r0);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int64_t c = cb + wn * 64 + j * 32 + (lane & 31);
+            for (int j = 0; j < BJ; ++j) {
+                const int64_t c = cb + wn * CW + j * 32 + (lane & 31);
                 const bool cok = c < n;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    int rbase = wm * 128 + i * 32 + (lane >> 5) * 4;
+                for (int i = 0; i < BI; ++i) {
+                    int rbase = wm * RW + i * 32 + (lane >> 5) * 4;
                     asm volatile("" : "+v"(rbase));
-                    if (diag) self_out(acc[i][j], rbase, wn * 64 + j * 32 + (lane & 31));
+                    if (diag) self_out(acc[i][j], rbase, wn * CW + j * 32 + (lane & 31));
                     epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j], rscale,
                                            thr, rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
                                            &need[tpar]);
@@ -615,7 +626,7 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
     if (G > 1) {
         // each split leaves at most C per row, so the merge of the G lists
         // sorts at most G * C
-        for (int rl = wave; rl < kBM2; rl += kT2 / 64) {
+        for (int rl = wave; rl < kBM2; rl += WAVES) {
             const int64_t r = r0 + rl;
             if (r < n && cnt[rl] > a.C)
                 compact_row_w(a.bkey + (r * G + split) * a.cap, a.bid + (r * G + split) * a.cap,
@@ -627,6 +638,17 @@ __global__ __launch_bounds__(512, 1) void sweep_dma_kernel(MfmaSweepArgs a) {
 }
 
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
+
+// Waves per direct-load workgroup: 8 (128 x 64 wave tiles) or 16 (64 x 64).
+// SWANN_SWEEP_WAVES=8|16 pins it.
+#ifndef SWANN_SWEEP_WAVES
+#define SWANN_SWEEP_WAVES 16
+#endif
+inline int sweep_waves() {
+    const char* e = getenv("SWANN_SWEEP_WAVES");
+    if (e && *e) return atoi(e) == 16 ? 16 : 8;
+    return SWANN_SWEEP_WAVES;
+}
 
 }  // namespace
 
@@ -661,12 +683,20 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         a.splits = splits;
         *used = splits;
         const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2 * splits);
-        if (scaled) {
-            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
-            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
+        if (sweep_waves() == 16) {
+            if (scaled) {
+                if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(grid), dim3(1024), 0, st, a);
+                else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(grid), dim3(1024), 0, st, a);
+            } else {
+                if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(grid), dim3(1024), 0, st, a);
+                else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(grid), dim3(1024), 0, st, a);
+            }
+        } else if (scaled) {
+            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 8>), dim3(grid), dim3(kT2), 0, st, a);
+            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 8>), dim3(grid), dim3(kT2), 0, st, a);
         } else {
-            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0>), dim3(grid), dim3(kT2), 0, st, a);
-            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0>), dim3(grid), dim3(kT2), 0, st, a);
+            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 8>), dim3(grid), dim3(kT2), 0, st, a);
+            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 8>), dim3(grid), dim3(kT2), 0, st, a);
         }
         return launch_status("sweep (mfma, direct loads)");
     }
