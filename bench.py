@@ -55,6 +55,7 @@ LADDER = ((64, 32, 64, 0.3), (64, 48, 64, 0.2), (96, 32, 64, 0.3), (64, 48, 128,
           (128, 24, 128, 0.2), (128, 32, 64, 0.3), (64, 64, 128, 0.3), (128, 48, 128, 0.3))
 TARGET_RECALL = 0.95
 HBM_PEAK = 8.0e12
+MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # HBM bytes per advance launch measured by rocprofv3 --pmc (FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000, the factors a 2 GiB device copy reads; see
 # profiles/advance_kernel_c3_hbm_traffic.md).  Valid only for the kernel source it
@@ -131,6 +132,38 @@ def ground_truth(X32, Q, k, metric):
                 best_i = torch.gather(ii, 1, j)
         out[a:a + 1024] = best_i
     return out
+
+
+def timed_build(X, cfg):
+    """Index.build's three stages (swann/build.py:153-171) with a sync after
+    each: (graph, total seconds, per-stage seconds)."""
+    from swann_amd import build as B
+    Xg = B._rows(X)
+    t = [time.perf_counter()]
+    cand, cdist = B.knn_candidates(Xg, cfg["cand"], metric=cfg["metric"])
+    torch.cuda.synchronize()
+    t.append(time.perf_counter())
+    G = B.robust_prune(Xg, cand, cdist, cfg["D"], alpha=1.2, metric=cfg["metric"])
+    torch.cuda.synchronize()
+    t.append(time.perf_counter())
+    G = B.add_reverse(Xg, G, cfg["D"], alpha=1.2, metric=cfg["metric"]).to(torch.int32).contiguous()
+    torch.cuda.synchronize()
+    t.append(time.perf_counter())
+    del cand, cdist
+    stages = dict(candidates=round(t[1] - t[0], 3), prune=round(t[2] - t[1], 3),
+                  reverse=round(t[3] - t[2], 3))
+    return G, t[3] - t[0], stages
+
+
+def build_roofline(n, d, stages):
+    """The candidate sweep against the dense fp16 MFMA peak: 2 n^2 d FLOP over
+    the candidate stage's time (sweep + list merge, + the exact re-rank for an
+    fp32 corpus)."""
+    flop = 2.0 * n * n * d
+    ach = flop / stages["candidates"]
+    return {"bound": "mfma", "achieved": round(ach / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
+            "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK, 4), "kernel": "sweep_dma_kernel",
+            "flop": flop, "stage_s": stages["candidates"]}
 
 
 def recall(ids, truth, k=10):
@@ -430,7 +463,6 @@ def main():
         return
 
     import swann_amd
-    from swann_amd.build import build_graph
     cfg = dict(CONFIGS[a.config])
     cfg.update(queue=12, budget=64)
     n = a.n or cfg["n"]
@@ -452,11 +484,8 @@ def main():
     del X32
     torch.cuda.empty_cache()
     torch.cuda.synchronize()
-    tb = time.perf_counter()
-    G = build_graph(X, metric=cfg["metric"], degree=cfg["D"], candidates=cfg["cand"], alpha=1.2)
-    torch.cuda.synchronize()
-    build_s = time.perf_counter() - tb
-    log(f"graph built in {build_s:.1f}s")
+    G, build_s, stages = timed_build(X, cfg)
+    log(f"graph built in {build_s:.1f}s {stages}")
     index = swann_amd.Index(X, G, metric=cfg["metric"])
     srch = Searcher(index, Q, k, cfg)
 
@@ -613,6 +642,8 @@ def main():
         "phase_ms": ph_mean,
         "build_s": round(build_s, 2),
         "build_s_per_1M_rows": round(build_s * 1e6 / n, 2),
+        "build_stages_s": stages,
+        "build_roofline": build_roofline(n, cfg["d"], stages),
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1),
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
