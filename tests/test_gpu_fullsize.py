@@ -1,0 +1,213 @@
+"""Config C3 at its full size on one GPU (1M x 1536 fp16, inner product, D=64,
+C=128), checked through properties that do not depend on the size: the
+candidate lists of sampled rows against a brute-force product of those rows
+with the whole corpus, the prune of sampled nodes against the oracle on the
+rows it reads, the final graph's invariants, and the search's answers
+against exact recomputation and exact ground truth."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+swann = pytest.importorskip("swann_amd")
+from swann_amd import build as B  # noqa: E402
+
+N, DIM, RANK, C, DEG = 1_000_000, 1536, 256, 128, 64
+
+
+def note(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def lowrank(m, W, g):
+    """x = z W / 16 + 0.1 e, rows normalised (the C3 generator's shape)."""
+    z = torch.randn((m, RANK), generator=g, device="cuda")
+    x = z @ W / 16.0 + 0.1 * torch.randn((m, DIM), generator=g, device="cuda")
+    return x / x.norm(dim=1, keepdim=True)
+
+
+@pytest.fixture(scope="module")
+def c3():
+    g = torch.Generator(device="cuda")
+    g.manual_seed(33)
+    W = torch.randn((RANK, DIM), generator=g, device="cuda")
+    X16 = lowrank(N, W, g).half()
+    Q = lowrank(1000, W, g)
+    note("c3 full size: sweep")
+    cand, cdist = B.knn_candidates(X16, C, metric="ip")
+    note("c3 full size: prune")
+    Gp = B.robust_prune(X16, cand, cdist, DEG, alpha=1.2, metric="ip")
+    note("c3 full size: reverse")
+    G = B.add_reverse(X16, Gp, DEG, alpha=1.2, metric="ip")
+    torch.cuda.synchronize()
+    return dict(X16=X16, Q=Q, cand=cand, cdist=cdist, Gp=Gp, G=G)
+
+
+def test_candidate_lists_are_exact_on_sampled_rows(c3):
+    X16, cand, cdist = c3["X16"], c3["cand"], c3["cdist"]
+    rows = torch.from_numpy(np.random.default_rng(1).choice(N, 256, replace=False)).cuda()
+    A = X16[rows].float()
+    best_d, best_i = None, None
+    for s in range(0, N, 200_000):                  # brute force in fp32 (exact products)
+        d = 1.0 - A @ X16[s:s + 200_000].float().T
+        cols = torch.arange(s, min(N, s + 200_000), device="cuda")
+        d[rows[:, None] == cols[None, :]] = 3.4e38          # self, as build.py:39
+        v, i = torch.topk(d, C, dim=1, largest=False)
+        i = i + s
+        if best_d is None:
+            best_d, best_i = v, i
+        else:
+            dd, ii = torch.cat([best_d, v], 1), torch.cat([best_i, i], 1)
+            best_d, j = torch.topk(dd, C, dim=1, largest=False)
+            best_i = torch.gather(ii, 1, j)
+    got = cand[rows].long()
+    agree = np.mean([len(set(a) & set(b)) / C
+                     for a, b in zip(got.cpu().tolist(), best_i.cpu().tolist())])
+    note("sampled candidate agreement", agree)
+    assert agree > 0.995
+    # returned distances against an fp64 recomputation from the stored rows
+    xa = X16[rows].double()
+    xb = X16[got.reshape(-1)].double().reshape(256, C, DIM)
+    exact = 1.0 - (xb @ xa[:, :, None])[..., 0]
+    assert torch.allclose(cdist[rows].double(), exact, rtol=0, atol=1e-5)
+    # invariants of every row
+    cc, cd = cand.cpu().numpy(), cdist.cpu().numpy()
+    assert ((cc >= 0) & (cc < N)).all()
+    assert not (cc == np.arange(N)[:, None]).any()
+    assert (np.diff(cd, axis=1) >= 0).all()
+
+
+def test_prune_of_sampled_nodes_matches_oracle(c3):
+    """The oracle prunes each sampled node on the corpus rows it reads (the
+    node and its candidates), with the sweep's own lists and distances."""
+    X16, cand, cdist, Gp = c3["X16"], c3["cand"], c3["cdist"], c3["Gp"]
+    nodes = np.random.default_rng(2).choice(N, 48, replace=False)
+    same = 0
+    for u in nodes:
+        ids = np.concatenate([[u], cand[u].cpu().numpy()]).astype(np.int64)
+        Xs = X16[torch.from_numpy(ids).cuda()].float().cpu().numpy()
+        cs = np.full((len(ids), C), -1, np.int32)
+        ds = np.full((len(ids), C), np.inf, np.float32)
+        cs[0] = np.arange(1, C + 1, dtype=np.int32)
+        ds[0] = cdist[u].cpu().numpy()
+        row = O.robust_prune(Xs, cs, ds, DEG, 1.2, O.METRIC_IP, nthreads=8)[0]
+        want = np.where(row >= 0, ids[np.clip(row, 0, None)], -1)
+        same += int(np.array_equal(want, Gp[u].cpu().numpy()))
+    note("sampled prune rows equal to the oracle", same, "of", len(nodes))
+    assert same >= len(nodes) - 1                     # a near-tie may flip one row
+
+
+def test_final_graph_invariants(c3):
+    G = c3["G"].cpu().numpy()
+    assert G.shape == (N, DEG) and G.dtype == np.int32
+    assert ((G >= -1) & (G < N)).all()
+    assert not (G == np.arange(N)[:, None]).any()
+    live = G >= 0
+    srt = np.sort(np.where(live, G, -1 - np.arange(DEG)[None, :]), axis=1)
+    assert (np.diff(srt, axis=1) != 0).all()          # no id twice in a row
+    deg = live.sum(1)
+    note("out-degree min/mean", int(deg.min()), float(deg.mean()))
+    assert deg.min() >= 1
+
+
+def test_search_answers_are_exact_and_recall_meets_the_target(c3):
+    X16, Q, G = c3["X16"], c3["Q"], c3["G"]
+    index = swann.Index(X16, G, metric="ip")
+    ids, dist = index.search(Q, k=10, branches=64, queue=48, budget=64, stop_eps=0.2, team=16)
+    ids_t = torch.from_numpy(ids.astype(np.int64)).cuda()
+    assert (ids >= 0).all()
+    assert all(len(set(r)) == 10 for r in ids.tolist())
+    exact = 1.0 - (X16[ids_t.reshape(-1)].double().reshape(1000, 10, DIM)
+                   @ Q.double()[:, :, None])[..., 0]
+    assert torch.allclose(torch.from_numpy(dist).cuda().double(), exact, rtol=0, atol=1e-5)
+    truth = torch.topk(Q @ X16.float().T, 10, dim=1).indices.cpu().numpy()
+    r = np.mean([len(set(a) & set(b)) / 10 for a, b in zip(ids.tolist(), truth.tolist())])
+    note("full-size C3 recall@10", r)
+    assert r >= 0.95
+
+
+# ---------------------------------------------------------------------------
+# Config C5: the build target, 1M x 1024 fp32 L2 (a 1000-centre mixture)
+
+D5 = 1024
+
+
+def gmm(m, centres, g):
+    lab = torch.randint(0, centres.shape[0], (m,), generator=g, device="cuda")
+    return centres[lab] + 0.3 * torch.randn((m, D5), generator=g, device="cuda")
+
+
+@pytest.fixture(scope="module")
+def c5():
+    g = torch.Generator(device="cuda")
+    g.manual_seed(55)
+    centres = torch.randn((1000, D5), generator=g, device="cuda")
+    X = gmm(N, centres, g)
+    Q = gmm(1000, centres, g)
+    note("c5 full size: sweep")
+    cand, cdist = B.knn_candidates(X, C, metric="l2")
+    note("c5 full size: prune + reverse")
+    G = B.add_reverse(X, B.robust_prune(X, cand, cdist, DEG, alpha=1.2, metric="l2"), DEG,
+                      alpha=1.2, metric="l2")
+    torch.cuda.synchronize()
+    return dict(X=X, Q=Q, cand=cand, cdist=cdist, G=G)
+
+
+def test_c5_candidates_are_exact_on_sampled_rows(c5):
+    """fp32 rows go through the fp16 screen and the exact fp32 re-rank: the
+    lists of sampled rows equal a brute-force fp64 top-C up to near-ties and
+    carry distances equal to an fp64 recomputation to fp32 rounding."""
+    X, cand, cdist = c5["X"], c5["cand"], c5["cdist"]
+    rows = torch.from_numpy(np.random.default_rng(3).choice(N, 128, replace=False)).cuda()
+    A = X[rows].double()
+    an = (A * A).sum(1, keepdim=True)
+    best_d, best_i = None, None
+    for s in range(0, N, 100_000):
+        Y = X[s:s + 100_000].double()
+        d = an - 2.0 * A @ Y.T + (Y * Y).sum(1)[None, :]
+        cols = torch.arange(s, min(N, s + 100_000), device="cuda")
+        d[rows[:, None] == cols[None, :]] = 3.4e38
+        v, i = torch.topk(d, C, dim=1, largest=False)
+        if best_d is None:
+            best_d, best_i = v, i + s
+        else:
+            dd, ii = torch.cat([best_d, v], 1), torch.cat([best_i, i + s], 1)
+            best_d, j = torch.topk(dd, C, dim=1, largest=False)
+            best_i = torch.gather(ii, 1, j)
+    got = cand[rows].long()
+    agree = np.mean([len(set(a) & set(b)) / C
+                     for a, b in zip(got.cpu().tolist(), best_i.cpu().tolist())])
+    note("c5 sampled candidate agreement", agree)
+    assert agree > 0.995
+    xb = X[got.reshape(-1)].double().reshape(128, C, D5)
+    exact = ((xb - A[:, None, :]) ** 2).sum(-1)
+    assert torch.allclose(cdist[rows].double(), exact, rtol=2e-5, atol=0)
+    cc, cd = cand.cpu().numpy(), cdist.cpu().numpy()
+    assert ((cc >= 0) & (cc < N)).all()
+    assert not (cc == np.arange(N)[:, None]).any()
+    assert (np.diff(cd, axis=1) >= 0).all()
+
+
+def test_c5_graph_and_search(c5):
+    X, Q, G = c5["X"], c5["Q"], c5["G"]
+    Gc = G.cpu().numpy()
+    assert Gc.shape == (N, DEG) and ((Gc >= -1) & (Gc < N)).all()
+    assert not (Gc == np.arange(N)[:, None]).any()
+    index = swann.Index(X, G, metric="l2")
+    ids, dist = index.search(Q, k=10, branches=32, queue=12, budget=64, stop_eps=0.05, team=16)
+    assert (ids >= 0).all() and all(len(set(r)) == 10 for r in ids.tolist())
+    ids_t = torch.from_numpy(ids.astype(np.int64)).cuda()
+    exact = ((X[ids_t.reshape(-1)].double().reshape(1000, 10, D5) - Q.double()[:, None, :]) ** 2
+             ).sum(-1)
+    assert torch.allclose(torch.from_numpy(dist).cuda().double(), exact, rtol=1e-5, atol=0)
+    xn = (X * X).sum(1)
+    truth = torch.topk(xn[None, :] - 2.0 * Q @ X.T, 10, dim=1, largest=False).indices
+    r = np.mean([len(set(a) & set(b)) / 10 for a, b in zip(ids.tolist(), truth.cpu().tolist())])
+    note("full-size C5 recall@10", r)
+    assert r >= 0.94        # bench.py --config c5 measures 0.955 at these knobs on its seed
