@@ -339,6 +339,69 @@ __device__ void gram_mfma(const _Float16* __restrict__ X, int64_t n, int dim, co
     }
 }
 
+// The same Gram for fp32 rows on v_mfma_f32_32x32x2_f32 (fp32 products and
+// sums, as the SIMT Gram, in another order).  One MFMA takes two K per lane
+// group: lane l supplies row l%32 at k = k0 + 4*(l/32) + s for s = 0..3, so a
+// lane's four operands are one 16-byte load and four MFMAs cover K = 8 (the
+// Gram is a sum over k; the order of the k is free).  dim % 8 == 0.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__device__ void gram_mfma_f32(const float* __restrict__ X, int64_t n, int dim, const int* cid,
+                              int C, float* gram, float* vn) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (w * 32 >= C) return;
+    const int quad = (lane >> 5) * 4;
+    auto rowp = [&](int i) -> const float* {
+        const int c = (i < C) ? cid[i] : -1;
+        return (c >= 0 && c < n) ? X + (int64_t)c * dim + quad : nullptr;
+    };
+    const float* pa = rowp(w * 32 + (lane & 31));
+    const float* pb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pb[j] = (j >= w) ? rowp(j * 32 + (lane & 31)) : nullptr;
+    f32x16v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+    const f32x4v z = {};
+    constexpr int kU = 4;                               // K = 8 steps in flight
+    for (int k0 = 0; k0 < dim; k0 += 8 * kU) {
+        f32x4v a[kU], b[kU][4];
+#pragma unroll
+        for (int s = 0; s < kU; ++s) {
+            const int k = k0 + s * 8;
+            const bool kin = k < dim;
+            a[s] = (pa && kin) ? *reinterpret_cast<const f32x4v*>(pa + k) : z;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                b[s][j] = (j >= w && pb[j] && kin) ? *reinterpret_cast<const f32x4v*>(pb[j] + k) : z;
+        }
+#pragma unroll
+        for (int s = 0; s < kU; ++s)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (j >= w)
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][q], b[s][j][q], acc[j],
+                                                                      0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < w) continue;
+        const int cc = j * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            if (r < C && cc < C) {
+                if (r < cc) gram[tri(r, cc)] = acc[j][e];
+                else if (r == cc) vn[r] = acc[j][e];
+            }
+        }
+    }
+}
+
 template <typename XT, bool MFMA>
 __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
@@ -361,8 +424,10 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
         cdu[i] = cdist[u * C + i];
     }
     __syncthreads();
-    if constexpr (MFMA) {
+    if constexpr (MFMA && sizeof(XT) == 2) {
         gram_mfma(reinterpret_cast<const _Float16*>(X), n, dim, cid, C, gram, vn);
+    } else if constexpr (MFMA) {
+        gram_mfma_f32(reinterpret_cast<const float*>(X), n, dim, cid, C, gram, vn);
     } else {
     // thread (ty, tx) accumulates Gram rows ty*8.., columns tx*8.. (C <= 128)
     float acc[8][8] = {};
@@ -799,12 +864,18 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
     SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
     SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
-    // fp16 rows with 16-byte aligned 16-wide K steps: the Gram on MFMA
-    const bool mfma = x_dtype == SWANN_DTYPE_F16 && dim % 16 == 0 && (uintptr_t)X % 16 == 0 &&
-                      !getenv_flag("SWANN_PRUNE_SIMT");
-    if (mfma)
+    // the Gram on MFMA: fp16 rows with 16-byte aligned 16-wide K steps, fp32
+    // rows with 16-byte aligned 8-wide K steps
+    const bool simt = getenv_flag("SWANN_PRUNE_SIMT");
+    const bool mfma16 = x_dtype == SWANN_DTYPE_F16 && dim % 16 == 0 && (uintptr_t)X % 16 == 0;
+    const bool mfma32 = x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 && (uintptr_t)X % 16 == 0;
+    if (!simt && mfma16)
         hipLaunchKernelGGL((prune_kernel<_Float16, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                           deg_per_node, protect, out);
+    else if (!simt && mfma32)
+        hipLaunchKernelGGL((prune_kernel<float, true>), dim3((unsigned)n), dim3(256), 0, st,
+                           (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
                            deg_per_node, protect, out);
     else
         SWANN_BY_DTYPE(x_dtype,

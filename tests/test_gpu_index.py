@@ -354,16 +354,18 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
     assert same > 0.97
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
 @pytest.mark.parametrize("metric", [0, 1])
-def test_prune_mfma_gram_matches_simt_and_oracle(metric, monkeypatch):
-    """fp16 corpora prune on an MFMA Gram (exact products, fp32 sums); the
-    fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle (double dots) on the
-    same inputs keep the same rows up to near-ties.  d = 80 leaves a ragged
-    last K group; per-node caps and protect ride along."""
+def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, monkeypatch):
+    """The prune's Gram on MFMA -- fp16 rows: exact products, fp32 sums
+    (32x32x16 f16); fp32 rows: fp32 products and sums (32x32x2 f32) -- keeps
+    the same rows as the fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle
+    (double dots) up to near-ties.  d = 80 leaves a ragged last K group for
+    fp16; per-node caps and protect ride along."""
     X = gaussian(3000, 80, 71 + metric, metric == 0)
     if metric == 1:
         X = X * 2.0 + 0.5
-    X16 = X.astype(np.float16)
+    X16 = X.astype(np.float16) if dtype == "f16" else X.astype(np.float32)
     m = "ip" if metric == 0 else "l2"
     Xg = torch.from_numpy(X16).cuda()
     cand, cdist = B.knn_candidates(Xg, 48, metric=m)
@@ -378,5 +380,5 @@ def test_prune_mfma_gram_matches_simt_and_oracle(metric, monkeypatch):
     ora = O.robust_prune(X16.astype(np.float32), cand.cpu().numpy(), cdist.cpu().numpy(), 24,
                          1.2, metric, nthreads=8, deg_per_node=dpn, protect=prot)
     a, b = (g_mfma == g_simt).all(1).mean(), (g_mfma == ora).all(1).mean()
-    note("prune mfma vs simt / oracle", m, a, b)
+    note("prune mfma vs simt / oracle", dtype, m, a, b)
     assert a > 0.99 and b > 0.99
