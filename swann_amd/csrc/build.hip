@@ -402,6 +402,97 @@ __device__ void gram_mfma_f32(const float* __restrict__ X, int64_t n, int dim, c
     }
 }
 
+// The Gram with the candidate rows staged through LDS, 128 bytes of each
+// row at a time (64 halves or 32 floats), so every row is read from memory
+// once per node instead of once per wave that needs it.  Each 16-byte chunk c
+// of row r sits at chunk c ^ swz(r) (the 32 rows of a fragment read fall in
+// distinct banks).  A K chunk is four steps; in step t lane l reads chunk
+// 2t + l/32 of its row: fp16 -- 8 halves, one 32x32x16 MFMA; fp32 -- 4
+// floats, four 32x32x2 MFMAs (k = 4*(l/32) + s of the step's 8, a
+// permutation of the K order, which a sum over k does not see).  Products
+// are exact (fp16) or fp32 (fp32), sums fp32.  dim % 8 (fp16: % 16) == 0.
+constexpr int kStgRow = 128;                       // bytes of a row per K chunk
+
+__device__ __forceinline__ int pswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <typename XT>
+__device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, const int* cid,
+                                 int C, float* gram, float* vn, unsigned char* stg) {
+    constexpr int EPC = 16 / sizeof(XT);           // elements per 16-byte chunk
+    constexpr int KC = kStgRow / sizeof(XT);       // elements of a row per K chunk
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const bool busy = w * 32 < C;                  // C: one past the last valid candidate
+    f32x16v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+    const int ar = w * 32 + (lane & 31);
+    const int half = lane >> 5;
+    for (int k0 = 0; k0 < dim; k0 += KC) {
+        // stage: 128 rows x 8 chunks, 4 per thread
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = q * 256 + tid;
+            const int r = e >> 3, c = e & 7;
+            if (r >= ((C + 31) & ~31)) continue;     // rows no tile reads
+            const int id = r < C ? cid[r] : -1;
+            const int k = k0 + c * EPC;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (id >= 0 && id < n && k < dim)
+                v = *reinterpret_cast<const uint4*>(X + (int64_t)id * dim + k);
+            *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = v;
+        }
+        __syncthreads();
+        if (busy) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int ch = 2 * t + half;
+                const uint4 ra = *reinterpret_cast<const uint4*>(stg + ar * kStgRow +
+                                                                 ((ch ^ pswz(ar)) << 4));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j < w || j * 32 >= C) continue;
+                    const int br = j * 32 + (lane & 31);
+                    const uint4 rb = *reinterpret_cast<const uint4*>(stg + br * kStgRow +
+                                                                     ((ch ^ pswz(br)) << 4));
+                    if constexpr (sizeof(XT) == 2) {
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(h16x8, ra), __builtin_bit_cast(h16x8, rb), acc[j],
+                            0, 0, 0);
+                    } else {
+                        const f32x4v fa = __builtin_bit_cast(f32x4v, ra);
+                        const f32x4v fb = __builtin_bit_cast(f32x4v, rb);
+#pragma unroll
+                        for (int s2 = 0; s2 < 4; ++s2)
+                            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[s2], fb[s2], acc[j],
+                                                                          0, 0, 0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (!busy) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < w) continue;
+        const int cc = j * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            if (r < C && cc < C) {
+                if (r < cc) gram[tri(r, cc)] = acc[j][e];
+                else if (r == cc) vn[r] = acc[j][e];
+            }
+        }
+    }
+}
+
+#ifndef SWANN_PRUNE_STAGED
+#define SWANN_PRUNE_STAGED 1
+#endif
+
 template <typename XT, bool MFMA>
 __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
@@ -424,7 +515,17 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
         cdu[i] = cdist[u * C + i];
     }
     __syncthreads();
-    if constexpr (MFMA && sizeof(XT) == 2) {
+    if constexpr (MFMA && SWANN_PRUNE_STAGED) {
+        // candidates past the last valid one are never read: the Gram stops there
+        __shared__ __align__(16) unsigned char stg[kPruneMaxC * kStgRow];
+        __shared__ int s_nv;
+        if (tid == 0) s_nv = 0;
+        __syncthreads();
+        for (int i = tid; i < C; i += 256)
+            if (cid[i] >= 0 && cid[i] < n) atomicMax(&s_nv, i + 1);
+        __syncthreads();
+        gram_mfma_staged<XT>(X, n, dim, cid, s_nv, gram, vn, stg);
+    } else if constexpr (MFMA && sizeof(XT) == 2) {
         gram_mfma(reinterpret_cast<const _Float16*>(X), n, dim, cid, C, gram, vn);
     } else if constexpr (MFMA) {
         gram_mfma_f32(reinterpret_cast<const float*>(X), n, dim, cid, C, gram, vn);
