@@ -281,126 +281,7 @@ __device__ __forceinline__ int tri(int w, int i) { return i * (i - 1) / 2 + w; }
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16v __attribute__((ext_vector_type(16)));
 
-// The Gram of a node's candidates on MFMA (fp16 rows: products exact, sums
-// in fp32).  Wave w owns candidate rows [32w, 32w + 32) and the 32x32 tiles
-// j >= w of the upper triangle; fragments come straight from the rows in
-// HBM/L2 as 16-byte loads (A: row l%32, halves (l/32)*8..+7 of each 16-wide
-// K step; B likewise), four K steps in flight.  Output tile element e of lane
-// l is <row (e/4)*8 + (l/32)*4 + e%4 of the strip, row l%32 of tile j>.
-__device__ void gram_mfma(const _Float16* __restrict__ X, int64_t n, int dim, const int* cid,
-                          int C, float* gram, float* vn) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (w * 32 >= C) return;
-    const int half = (lane >> 5) * 8;
-    auto rowp = [&](int i) -> const _Float16* {
-        const int c = (i < C) ? cid[i] : -1;
-        return (c >= 0 && c < n) ? X + (int64_t)c * dim + half : nullptr;
-    };
-    const _Float16* pa = rowp(w * 32 + (lane & 31));
-    const _Float16* pb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pb[j] = (j >= w) ? rowp(j * 32 + (lane & 31)) : nullptr;
-    f32x16v acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
-    const h16x8 z = {};
-    constexpr int kU = 4;
-    for (int k0 = 0; k0 < dim; k0 += 16 * kU) {
-        h16x8 a[kU], b[kU][4];
-#pragma unroll
-        for (int s = 0; s < kU; ++s) {
-            const int k = k0 + s * 16;
-            const bool kin = k < dim;
-            a[s] = (pa && kin) ? *reinterpret_cast<const h16x8*>(pa + k) : z;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                b[s][j] = (j >= w && pb[j] && kin) ? *reinterpret_cast<const h16x8*>(pb[j] + k) : z;
-        }
-#pragma unroll
-        for (int s = 0; s < kU; ++s)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j >= w) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s], b[s][j], acc[j], 0, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (j < w) continue;
-        const int cc = j * 32 + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-            if (r < C && cc < C) {
-                if (r < cc) gram[tri(r, cc)] = acc[j][e];
-                else if (r == cc) vn[r] = acc[j][e];
-            }
-        }
-    }
-}
-
-// The same Gram for fp32 rows on v_mfma_f32_32x32x2_f32 (fp32 products and
-// sums, as the SIMT Gram, in another order).  One MFMA takes two K per lane
-// group: lane l supplies row l%32 at k = k0 + 4*(l/32) + s for s = 0..3, so a
-// lane's four operands are one 16-byte load and four MFMAs cover K = 8 (the
-// Gram is a sum over k; the order of the k is free).  dim % 8 == 0.
 typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-__device__ void gram_mfma_f32(const float* __restrict__ X, int64_t n, int dim, const int* cid,
-                              int C, float* gram, float* vn) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (w * 32 >= C) return;
-    const int quad = (lane >> 5) * 4;
-    auto rowp = [&](int i) -> const float* {
-        const int c = (i < C) ? cid[i] : -1;
-        return (c >= 0 && c < n) ? X + (int64_t)c * dim + quad : nullptr;
-    };
-    const float* pa = rowp(w * 32 + (lane & 31));
-    const float* pb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pb[j] = (j >= w) ? rowp(j * 32 + (lane & 31)) : nullptr;
-    f32x16v acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
-    const f32x4v z = {};
-    constexpr int kU = 4;                               // K = 8 steps in flight
-    for (int k0 = 0; k0 < dim; k0 += 8 * kU) {
-        f32x4v a[kU], b[kU][4];
-#pragma unroll
-        for (int s = 0; s < kU; ++s) {
-            const int k = k0 + s * 8;
-            const bool kin = k < dim;
-            a[s] = (pa && kin) ? *reinterpret_cast<const f32x4v*>(pa + k) : z;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                b[s][j] = (j >= w && pb[j] && kin) ? *reinterpret_cast<const f32x4v*>(pb[j] + k) : z;
-        }
-#pragma unroll
-        for (int s = 0; s < kU; ++s)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (j >= w)
-                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][q], b[s][j][q], acc[j],
-                                                                      0, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (j < w) continue;
-        const int cc = j * 32 + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-            if (r < C && cc < C) {
-                if (r < cc) gram[tri(r, cc)] = acc[j][e];
-                else if (r == cc) vn[r] = acc[j][e];
-            }
-        }
-    }
-}
 
 // The Gram with the candidate rows staged through LDS, 128 bytes of each
 // row at a time (64 halves or 32 floats), so every row is read from memory
@@ -489,10 +370,6 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
     }
 }
 
-#ifndef SWANN_PRUNE_STAGED
-#define SWANN_PRUNE_STAGED 1
-#endif
-
 template <typename XT, bool MFMA>
 __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
@@ -515,7 +392,7 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
         cdu[i] = cdist[u * C + i];
     }
     __syncthreads();
-    if constexpr (MFMA && SWANN_PRUNE_STAGED) {
+    if constexpr (MFMA) {
         // candidates past the last valid one are never read: the Gram stops there
         __shared__ __align__(16) unsigned char stg[kPruneMaxC * kStgRow];
         __shared__ int s_nv;
@@ -525,10 +402,6 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
             if (cid[i] >= 0 && cid[i] < n) atomicMax(&s_nv, i + 1);
         __syncthreads();
         gram_mfma_staged<XT>(X, n, dim, cid, s_nv, gram, vn, stg);
-    } else if constexpr (MFMA && sizeof(XT) == 2) {
-        gram_mfma(reinterpret_cast<const _Float16*>(X), n, dim, cid, C, gram, vn);
-    } else if constexpr (MFMA) {
-        gram_mfma_f32(reinterpret_cast<const float*>(X), n, dim, cid, C, gram, vn);
     } else {
     // thread (ty, tx) accumulates Gram rows ty*8.., columns tx*8.. (C <= 128)
     float acc[8][8] = {};

@@ -29,7 +29,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBK = 32;
 constexpr int kPad = 8;                       // fp16 elements of padding per LDS row
 constexpr int kLdsRow = kBK + kPad;           // 40 halves = 80 bytes
-constexpr float kSelf = 3.4e38f;
 constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;   // workgroup tile rows, columns; threads
 
 __device__ __forceinline__ uint32_t fkey(float f) {
@@ -169,7 +168,7 @@ __device__ void compact_row_w(float* key, int32_t* id, int cnt, int C, float* th
 // distances from fresh LDS reads and appends.  Rows past n carry a -inf
 // threshold, so they never pass.  Self scores were set to -inf in the
 // accumulator (self_out), so their distance is +inf and never passes; the
-// merge adds self back at kSelf where a row has fewer than C others.
+// merge adds self back at 3.4e38 where a row has fewer than C others.
 template <int METRIC>
 __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64_t r0, int64_t c,
                                                bool cok, float cn, float sc, const float* rs,
