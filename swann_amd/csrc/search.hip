@@ -46,9 +46,6 @@ constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in 
 #ifndef SWANN_TABLE_SCOPE
 #define SWANN_TABLE_SCOPE __HIP_MEMORY_SCOPE_AGENT
 #endif
-#ifndef SWANN_CAS_FIRST
-#define SWANN_CAS_FIRST 0
-#endif
 constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
 constexpr size_t kMaxLds = 64 * 1024;
 
@@ -263,18 +260,6 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int ts, int key, int
     const unsigned mask = (unsigned)(Hc - 1);
     unsigned pos = (2654435761u * (unsigned)key) & mask;
     for (int probe = 0; probe < kCprobe; ++probe) {
-#if SWANN_CAS_FIRST
-        // The compare-and-swap returns the slot's value: one round trip
-        // decides found / claimed / occupied.
-        int expected = 0;
-        if (__hip_atomic_compare_exchange_strong(&cid[pos * ts], &expected, key + 1,
-                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 SWANN_TABLE_SCOPE)) {
-            *claimed = 1;
-            return (int)pos;
-        }
-        if (expected == key + 1) return (int)pos;
-#else
         int cur = __hip_atomic_load(&cid[pos * ts], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
         if (cur == key + 1) return (int)pos;
         if (cur == 0) {
@@ -287,7 +272,6 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int ts, int key, int
             }
             if (expected == key + 1) return (int)pos;
         }
-#endif
         pos = (pos + 1) & mask;
     }
     return -1;
@@ -301,9 +285,6 @@ __device__ __forceinline__ int cache_slot(int* cid, int Hc, int ts, int key, int
 // key comes back with its distance in the same round trip.  Reading the id
 // and the distance in one access is one of the orders the word-by-word probe
 // allows (id, then distance).
-#ifndef SWANN_PAIR_PROBE
-#define SWANN_PAIR_PROBE 2
-#endif
 __device__ __forceinline__ int cache_slot_pair(unsigned long long* tab, int Hc, int key,
                                                int* claimed, float* d) {
     const unsigned mask = (unsigned)(Hc - 1);
@@ -311,19 +292,12 @@ __device__ __forceinline__ int cache_slot_pair(unsigned long long* tab, int Hc, 
     const unsigned long long empty = (unsigned long long)__float_as_uint(FLT_MAX) << 32;
     const unsigned long long mine = empty | (unsigned)(key + 1);
     for (int probe = 0; probe < kCprobe; ++probe) {
-        unsigned long long cur;
-#if SWANN_PAIR_PROBE == 1
-        cur = __hip_atomic_load(&tab[pos], __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
-        if ((unsigned)cur == 0u)
-#endif
-        {
-            cur = empty;
-            if (__hip_atomic_compare_exchange_strong(&tab[pos], &cur, mine, __ATOMIC_RELAXED,
-                                                     __ATOMIC_RELAXED, SWANN_TABLE_SCOPE)) {
-                *claimed = 1;
-                *d = FLT_MAX;
-                return (int)pos;
-            }
+        unsigned long long cur = empty;
+        if (__hip_atomic_compare_exchange_strong(&tab[pos], &cur, mine, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, SWANN_TABLE_SCOPE)) {
+            *claimed = 1;
+            *d = FLT_MAX;
+            return (int)pos;
         }
         if ((unsigned)cur == (unsigned)(key + 1)) {
             *d = __uint_as_float((unsigned)(cur >> 32));
@@ -675,7 +649,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (!isnew) { ++cov; continue; }
             int slot = -1, claimed = 0;
             float d = FLT_MAX;
-            if (a.Hc > 0 && SWANN_PAIR_PROBE && ts == 2) {
+            if (a.Hc > 0 && ts == 2) {
                 slot = cache_slot_pair(reinterpret_cast<unsigned long long*>(cid), a.Hc, v,
                                        &claimed, &d);
             } else if (a.Hc > 0) {
