@@ -598,12 +598,28 @@ __global__ __launch_bounds__(256) void rev_assemble(const XT* __restrict__ X, in
         if (mark[t]) row[i] = kBig;
     for (int t = tid; t < dim && t < 4096; t += 256) xu[t] = ld(X + u * dim + t);
     __syncthreads();
-    // exact distances, 16 lanes per candidate
+    // exact distances, 16 lanes per candidate; with 16-byte aligned rows a
+    // lane reads 16-byte chunks (8 halves or 4 floats) c = tl, tl + 16, ...
+    constexpr int VEC = 16 / (int)sizeof(XT);
+    const bool vec = dim <= 4096 && dim % VEC == 0 &&
+                     (reinterpret_cast<uintptr_t>(X) & 15) == 0;
     const int team = tid >> 4, tl = tid & 15;
     for (int i = team; i < W; i += 16) {
         const int v = row[i];
         float s = 0.f;
-        if (v < kBig) {
+        if (v < kBig && vec) {
+            const uint4* xv = reinterpret_cast<const uint4*>(X + (int64_t)v * dim);
+            for (int c = tl; c * VEC < dim; c += 16) {
+                const uint4 raw = xv[c];
+                const XT* e = reinterpret_cast<const XT*>(&raw);
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    const float xt = xu[c * VEC + k], xvt = (float)e[k];
+                    if (metric == SWANN_METRIC_IP) s = __builtin_fmaf(xvt, xt, s);
+                    else { const float df = xvt - xt; s = __builtin_fmaf(df, df, s); }
+                }
+            }
+        } else if (v < kBig) {
             const XT* xv = X + (int64_t)v * dim;
             for (int t = tl; t < dim; t += 16) {
                 const float xt = dim <= 4096 ? xu[t] : ld(X + u * dim + t);
