@@ -517,6 +517,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
 
     __shared__ int s_ctr[kNctr];
     __shared__ int s_slot, s_p, s_plin, s_nkeep, s_nwork, s_nbr, s_cov, s_stall, s_crowd_run;
+    __shared__ int s_npass;
     __shared__ unsigned s_retired[8];
     __shared__ float s_best_k, s_rad, s_qmu, s_qsum;
 
@@ -626,7 +627,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                 } else {
                     s_ctr[3] = 1;
                 }
-                s_nwork = 0; s_nkeep = 0; s_nbr = 0; s_cov = 0;
+                s_nwork = 0; s_nkeep = 0; s_nbr = 0; s_cov = 0; s_npass = 0;
             }
         }
         for (int i = tid; i < nsort; i += BLOCK) { c_id[i] = -1; c_d[i] = FLT_MAX; c_l[i] = 0; }
@@ -690,7 +691,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         } else {
             // decide from the code before reading the row (:560-575); a
             // skipped neighbour stays a candidate at FLT_MAX, unscored, with
-            // its table slot claimed but never filled
+            // its table slot claimed but never filled.  Two passes: every
+            // item is estimated and the ones to read are listed (in u_id,
+            // free until the keep step), then the teams score only those,
+            // so no team waits on a row that another team's item needs.
             const float rad = s_rad;
             for (int w = team; w < nw; w += NT) {
                 const int v = w_v[w];
@@ -699,14 +703,21 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                 float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords, head,
                                                a.calpha[v], s_qmu, s_qsum, a.dim, a.cwords, tl);
                 est = __shfl(est, 0, TEAM);
-                if (rad != FLT_MAX && est > rad + a.cmargin) {
-                    if (tl == 0) {
+                if (tl == 0) {
+                    if (rad != FLT_MAX && est > rad + a.cmargin) {
                         const int nidx = w_nidx[w] & 0xffff;
                         atomicAdd(&s_ctr[3], 1);
                         c_id[nidx] = v; c_d[nidx] = FLT_MAX; c_l[nidx] = plin;
+                    } else {
+                        u_id[atomicAdd(&s_npass, 1)] = w;
                     }
-                    continue;
                 }
+            }
+            __syncthreads();
+            const int npass = s_npass;
+            for (int k = team; k < npass; k += NT) {
+                const int w = u_id[k];
+                const int v = w_v[w];
                 const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
                                                      a.vec_ok, a.metric);
                 if (tl == 0) record(w, v, d);
