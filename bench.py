@@ -59,13 +59,11 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # HBM bytes per advance launch measured by rocprofv3 --pmc (FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000, the factors a 2 GiB device copy reads; see
 # profiles/advance_kernel_c3_hbm_traffic.md).  Valid only for the kernel source it
-# was measured on (SHA-256 prefix of swann_amd/csrc/search.hip) and the same
-# workload and knobs; otherwise `traffic` is reported as null.
+# was measured on (kernel_source_key of swann_amd/csrc/search.hip: SHA-256 prefix of
+# the source without comments) and the same workload and knobs; otherwise
+# `traffic` is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 48, 128, 0.3, "6d609080657bb8e5"): 5.620e12,
-    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "6d609080657bb8e5"): 5.635e12,
-    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "5f8609651dd61c31"): 5.640e12,
-    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "88261fdb3ebbf2da"): 5.410e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "c3193a44dd261467"): 5.410e12,
 }
 
 
@@ -132,6 +130,20 @@ def ground_truth(X32, Q, k, metric):
                 best_i = torch.gather(ii, 1, j)
         out[a:a + 1024] = best_i
     return out
+
+
+def kernel_source_key(path):
+    """SHA-256 prefix of a kernel source with its // comments and blank lines
+    removed, so that a measured figure stays attached to the code it was
+    measured on through comment edits."""
+    import hashlib
+    import re
+    lines = []
+    for line in Path(path).read_text().splitlines():
+        line = re.sub(r"//.*$", "", line).rstrip()
+        if line:
+            lines.append(line)
+    return hashlib.sha256("\n".join(lines).encode()).hexdigest()[:16]
 
 
 def timed_build(X, cfg):
@@ -582,8 +594,7 @@ def main():
     adv_s = float(np.mean(adv_ms)) / 1e3
     achieved = adv_bytes / adv_s
     ph_mean = {k2: round(float(np.mean([p[k2] for p in phases])), 3) for k2 in phases[0]}
-    import hashlib
-    src_sha = hashlib.sha256((ROOT / "swann_amd" / "csrc" / "search.hip").read_bytes()).hexdigest()[:16]
+    src_sha = kernel_source_key(ROOT / "swann_amd" / "csrc" / "search.hip")
     traffic = PMC_TRAFFIC.get((a.config, n, nq, cfg["branches"], cfg["queue"], cfg["budget"],
                                eps, src_sha))
 
