@@ -14,7 +14,7 @@ import torch
 
 import oracle as O
 from conftest import gaussian, golden, regen
-from test_oracle_helpers import exact_topk, knn_graph, recall
+from test_oracle_helpers import crowd_case, exact_topk, knn_graph, recall, stall_case
 
 pytestmark = pytest.mark.gpu
 
@@ -290,6 +290,39 @@ def test_stall_and_crowd_match_oracle():
         O.advance_branch(X, G, Qv[q], br, budget, budget, policy=1, stall_patience=3,
                          crowd_frac=0.5)
         assert_queue(st, q, 0, br, q)
+
+
+@pytest.mark.parametrize("patience", [1, 4])
+def test_stall_hand_case(patience, block):
+    """The stall rule's hand case on the GPU: exactly patience + 1 expansions,
+    counter 6 set, and the queue equal to the oracle's."""
+    X, G, q = stall_case()
+    Xg, Gg, Qg = to_gpu(X, G, q[None, :])
+    st = E.init_states(Xg, Qg, torch.tensor([[0]], dtype=torch.int32), L=16, B=64, D=8,
+                       metric=1, team_size=4, stop_eps=-1.0, kstop=1, stall_patience=patience)
+    E.advance(Xg, Gg, Qg, st, 64)
+    br = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=1,
+                     stall_patience=patience)
+    assert int(st.counters[0, 0, 0]) == patience + 1 and int(st.counters[0, 0, 6]) == 1
+    assert_queue(st, 0, 0, br, ("stall", patience))
+
+
+def test_crowd_hand_case(block):
+    """The crowd rule's hand case on the GPU: the seed's lineage is retired
+    after the third expansion (counter 7) and the branch then finds no slot
+    (counter 3); the queue equals the oracle's."""
+    X, G, q = crowd_case()
+    Xg, Gg, Qg = to_gpu(X, G, q[None, :])
+    st = E.init_states(Xg, Qg, torch.tensor([[0]], dtype=torch.int32), L=16, B=64, D=8,
+                       metric=1, team_size=4, stop_eps=-1.0, kstop=10, crowd_frac=1.0)
+    E.advance(Xg, Gg, Qg, st, 64)
+    br = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=10,
+                     crowd_frac=1.0)
+    c = st.counters[0, 0].cpu().numpy()
+    assert c[0] == 3 and c[7] == 1 and c[3] == 1
+    assert_queue(st, 0, 0, br, "crowd")
 
 
 def test_shared_state_beats_split_branches_on_work():

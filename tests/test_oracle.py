@@ -15,6 +15,7 @@ import pytest
 
 import oracle as O
 from conftest import gaussian, golden, regen
+from test_oracle_helpers import crowd_case, stall_case
 
 F32MAX = np.finfo(np.float32).max
 
@@ -604,3 +605,43 @@ def test_fill_rules_closed_forms():
     for u in range(n):
         two = set(G[G[u, 0]]) if G[u, 0] >= 0 else set()
         assert not (set(br[u, 1:]) - {-1}) & two
+
+
+# -- stall and crowd retirement (local_search.cu:659-682): hand cases whose
+#    counts follow from the rule alone (stall_case / crowd_case)
+
+@pytest.mark.parametrize("patience", [1, 2, 4, 6])
+def test_stall_stops_after_patience_expansions_without_progress(patience):
+    """s_best_k starts at FLT_MAX each call: the first expansion moves it to 0
+    and resets the count, each later one adds 1; the branch stops when the
+    count reaches the patience, so it expands exactly patience + 1 nodes and
+    sets counter 6."""
+    X, G, q = stall_case()
+    br = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=1,
+                     stall_patience=patience)
+    assert br.counters[0] == patience + 1
+    assert br.counters[6] == 1
+    # patience 0 disables the rule: the branch runs until its queue is spent
+    br0 = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br0, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=1)
+    assert br0.counters[0] == 9 and br0.counters[6] == 0
+
+
+def test_crowd_retires_a_lineage_after_two_covered_expansions():
+    """crowd_frac = 1: expansion 1 (the seed) sees four new nodes; expansions
+    2 and 3 see only covered ones, so after the third the seed's lineage is
+    retired (counter 7) and, every queued node being of that lineage, the
+    next pick finds nothing (counter 3)."""
+    X, G, q = crowd_case()
+    br = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=10,
+                     crowd_frac=1.0)
+    assert br.counters[0] == 3
+    assert br.counters[7] == 1
+    assert br.counters[3] == 1
+    # a fraction no expansion reaches leaves the lineage alone: all 5 nodes expand
+    br2 = O.init_branch(X, q, [0], L=16, B=64, D=8, metric=O.METRIC_L2, team=4)
+    O.advance_branch(X, G, q, br2, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=10,
+                     crowd_frac=1.5)
+    assert br2.counters[0] == 5 and br2.counters[7] == 0
