@@ -717,17 +717,21 @@ int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
 
 // Column splits of the direct-load sweep: enough workgroups to give every
 // CU one (small n), and at least kMinSplits so that row panels are read from
-// L2 more than once.  SWANN_SWEEP_SPLIT=1|2|4|8 pins it.
+// L2 more than once.  SWANN_SWEEP_SPLIT=1|2|4|8 pins it (read at the first call).
 #ifndef SWANN_SWEEP_MIN_SPLITS
 #define SWANN_SWEEP_MIN_SPLITS 2
 #endif
 int sweep_mfma_splits(int64_t n, int dim) {
     if (dim % kBK3 != 0) return 1;
-    const char* e = getenv("SWANN_SWEEP_SPLIT");
-    if (e && *e) {
+    // read once per process: the workspace a caller sized with one value
+    // must not meet a launch that uses another
+    static const int pinned = [] {
+        const char* e = getenv("SWANN_SWEEP_SPLIT");
+        if (!e || !*e) return 0;
         const int g = atoi(e);
         return g == 2 || g == 4 || g == 8 ? g : 1;
-    }
+    }();
+    if (pinned) return pinned;
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     int g = SWANN_SWEEP_MIN_SPLITS;
     while (g < 8 && ntile * g < 512) g *= 2;
