@@ -160,6 +160,19 @@ __device__ void compact_row_w(float* key, int32_t* id, int cnt, int C, float* th
 }
 
 
+// A row's threshold in score space, for the epilogue's first test.  ip keeps
+// a score s when 1 - s < thr, so s > (1 - thr) - slack lets every such s
+// through (and a few more); l2 keeps when (nb - 2s) + na < thr, so
+// s > ((na - thr) - slack) / 2 + (nb - slack') / 2 does.  The slacks are 1e-5
+// relative to the magnitudes, far above the rounding of either form, and the
+// survivors are then tested exactly.  thr = +inf gives -inf (every finite
+// score passes); a row past n (thr = -inf) gives +inf or NaN (none passes).
+template <int METRIC>
+__device__ __forceinline__ float screen_thr(float thr, float na) {
+    if (METRIC == SWANN_METRIC_IP) return (1.0f - thr) - 1e-5f * (1.0f + fabsf(thr));
+    return 0.5f * ((na - thr) - 1e-5f * (fabsf(na) + fabsf(thr)));
+}
+
 // Epilogue for one 32 x 32 accumulator block: lane holds column c and the 16
 // rows rbase + (e/4)*8 + (e%4).  The common case -- no score of the block
 // beats its row's threshold -- costs the distance formula and one compare per
@@ -174,7 +187,8 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
                                                bool cok, float cn, float sc, const float* rs,
                                                const float* thr, const float* rnorm, int* cnt,
                                                const MfmaSweepArgs& a, int split, int nterm_scale,
-                                               const f32x16* vx, int* needf = nullptr) {
+                                               const f32x16* vx, int* needf = nullptr,
+                                               const float* sthr = nullptr) {
     auto dist = [&](int e, const float4& r4, const float4& s4) {
         const int q = e & 3;
         float dot;
@@ -194,12 +208,28 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
                          : make_float4(1.f, 1.f, 1.f, 1.f);
     };
     bool any = false;
+    if (sthr && nterm_scale != 1) {
+        // one compare per score against the row's screen threshold
+        const float ch = METRIC == SWANN_METRIC_L2 ? 0.5f * (cn - 1e-5f * fabsf(cn)) : 0.f;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        float4 t4, r4, s4;
-        group(g, t4, r4, s4);
+        for (int g = 0; g < 4; ++g) {
+            const float4 h4 = *reinterpret_cast<const float4*>(sthr + rbase + g * 8);
+            const float4 s4 = nterm_scale ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                          : make_float4(1.f, 1.f, 1.f, 1.f);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) any = any || (dist(g * 4 + q, r4, s4) < t4[q]);
+            for (int q = 0; q < 4; ++q) {
+                const float dot = nterm_scale ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+                any = any || (METRIC == SWANN_METRIC_IP ? dot > h4[q] : dot > ch + h4[q]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float4 t4, r4, s4;
+            group(g, t4, r4, s4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) any = any || (dist(g * 4 + q, r4, s4) < t4[q]);
+        }
     }
     any = any && cok;
     if (__ballot(any) == 0ull) return;
@@ -453,6 +483,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     __shared__ __align__(16) unsigned char sA[2][kStage];
     __shared__ __align__(16) unsigned char sB[2][kStage];
     __shared__ __align__(16) float thr[kBM2];
+    // thr in score space (screen_thr), for l2 only: there it saves the
+    // distance formula's four operations per score; ip's formula is one
+    // subtraction and the screen measured no faster
+    __shared__ __align__(16) float sthr[kBM2];
     __shared__ int cnt[kBM2];
     __shared__ __align__(16) float rnorm[kBM2];
     __shared__ __align__(16) float rscale[kBM2];
@@ -477,6 +511,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         cnt[tid] = 0;
         rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
         if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
+        if (METRIC == SWANN_METRIC_L2) sthr[tid] = screen_thr<METRIC>(thr[tid], rnorm[tid]);
     }
     if (tid < 2) need[tid] = 0;
 
@@ -559,10 +594,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             if (need[par]) {
                 for (int rl = wave; rl < kBM2; rl += WAVES) {
                     const int64_t r = r0 + rl;
-                    if (r < n && cnt[rl] > a.cap - kBN2)
+                    if (r < n && cnt[rl] > a.cap - kBN2) {
                         compact_row_w(a.bkey + (r * G + split) * a.cap,
                                       a.bid + (r * G + split) * a.cap, cnt[rl], a.C, &thr[rl],
                                       &cnt[rl]);
+                        if (METRIC == SWANN_METRIC_L2 && lane == 0)
+                            sthr[rl] = screen_thr<METRIC>(thr[rl], rnorm[rl]);
+                    }
                 }
                 __syncthreads();
                 if (tid == 0) need[par] = 0;
@@ -613,7 +651,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                     if (diag) self_out(acc[i][j], rbase, wn * CW + j * 32 + (lane & 31));
                     epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j], rscale,
                                            thr, rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
-                                           &need[tpar]);
+                                           &need[tpar],
+                                           METRIC == SWANN_METRIC_L2 ? sthr : nullptr);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
