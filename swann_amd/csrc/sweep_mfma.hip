@@ -465,8 +465,18 @@ typedef __attribute__((address_space(3))) void* lds_vptr;
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-__device__ __forceinline__ void dma16(const _Float16* g, unsigned char* lds) {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_vptr)lds, 16, 0, 0);
+// One wave-wide direct load global -> LDS of 16 bytes a lane: lane i's 16
+// bytes at base + voff (a wave-uniform base, a 32-bit byte offset per lane)
+// land at lds + 16 i.  Written as assembly so that the compiler does not
+// track it: it cannot tell the stage being read from the stage being filled
+// (they alternate at run time), and would make every fragment read wait for
+// the loads in flight.  The kernel waits for them itself: vmcnt(0) and a
+// barrier before a stage is read.  m0 carries the LDS address (one wait
+// state before the load reads it).
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, unsigned char* lds) {
+    const unsigned m = (unsigned)(uintptr_t)(lds_vptr)lds;
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(base), "s"(m) : "memory", "m0");
 }
 
 // WAVES = 8: two waves per SIMD with 128 x 64 wave tiles (128 accumulators);
@@ -516,15 +526,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     if (tid < 2) need[tid] = 0;
 
     // direct-load assignment: instruction j of this wave fills rows
-    // 8 (4 wave + j) .. + 7 of the stage; this lane fetches one 16-byte chunk
-    int lrow[NQ], lchunk[NQ];
-    int64_t aoff[NQ];
+    // 8 (NQ wave + j) .. + 7 of the stage; this lane fetches one 16-byte
+    // chunk, at byte offset voff from the stage's first row (rows past n
+    // read row n - 1: clamped for the panel here, for a column tile at issue)
+    const int64_t rowb = (int64_t)dim * 2;
+    uint32_t voffA[NQ], voffB[NQ];
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
-        lrow[j] = (wave * NQ + j) * 8 + (lane >> 3);
-        lchunk[j] = ((lane & 7) ^ swz(lrow[j])) * 8;
-        const int64_t r = r0 + lrow[j] < n ? r0 + lrow[j] : n - 1;
-        aoff[j] = r * (int64_t)dim + lchunk[j];
+        const int lrow = (wave * NQ + j) * 8 + (lane >> 3);
+        const int lchunk = ((lane & 7) ^ swz(lrow)) * 8;
+        const int64_t ra = r0 + lrow < n ? lrow : n - 1 - r0;
+        voffA[j] = (uint32_t)(ra * rowb + lchunk * 2);
+        voffB[j] = (uint32_t)(lrow * rowb + lchunk * 2);
     }
     const int nk = dim / kBK3;
     const int64_t nct = (n + kBN2 - 1) / kBN2;
@@ -536,12 +549,21 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         if (t >= nsteps) return;
         const int buf = (int)(t & 1);
         const int k0 = kt * kBK3;
+        const _Float16* ba = X + r0 * dim + k0;
+        const _Float16* bb = X + cb * dim + k0;
+        const bool part = cb + kBN2 > n;           // the last, partial column tile
 #pragma unroll
         for (int j = 0; j < NQ; ++j) {
             const int q = wave * NQ + j;
-            dma16(X + aoff[j] + k0, &sA[buf][q * 1024]);
-            const int64_t rb = cb + lrow[j] < n ? cb + lrow[j] : n - 1;
-            dma16(X + rb * (int64_t)dim + lchunk[j] + k0, &sB[buf][q * 1024]);
+            dma16(ba, voffA[j], &sA[buf][q * 1024]);
+            uint32_t vb = voffB[j];
+            if (part) {
+                const int lrow = (wave * NQ + j) * 8 + (lane >> 3);
+                const int lchunk = ((lane & 7) ^ swz(lrow)) * 8;
+                const int64_t rb = cb + lrow < n ? lrow : n - 1 - cb;
+                vb = (uint32_t)(rb * rowb + lchunk * 2);
+            }
+            dma16(bb, vb, &sB[buf][q * 1024]);
         }
     };
 
@@ -602,6 +624,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                             sthr[rl] = screen_thr<METRIC>(thr[rl], rnorm[rl]);
                     }
                 }
+                // let the compaction's stores finish here: left pending, the
+                // compiler's count of them reaches the join below and makes
+                // every stage's first fragment read wait for all loads in
+                // flight, the next stage's direct loads included
+                __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
                 if (tid == 0) need[par] = 0;
             }
@@ -636,6 +663,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                                                                       fb[sub & 1][j], acc[i][j],
                                                                       0, 0, 0);
         }
+        // interleave the next substep's fragment reads with this one's MFMAs
+        // (the scheduler otherwise reads each fragment just before its use)
+        __builtin_amdgcn_iglp_opt(1);
         if (kt == nk - 1) {
             // ---- epilogue of this column tile: distance, threshold, append ----
             const int64_t cb = cbt;
@@ -717,7 +747,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
     const bool ip = metric == SWANN_METRIC_IP;
     *used = 1;
-    if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
+    // the direct loads address a stage's 256 rows with 32-bit byte offsets
+    const bool off32 = (int64_t)dim * 2 * kBM2 < (int64_t(1) << 32);
+    if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && off32 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
         a.splits = splits;
         *used = splits;
         const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2 * splits);
