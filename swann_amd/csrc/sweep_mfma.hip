@@ -105,52 +105,63 @@ struct MfmaSweepArgs {
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
-// threshold by bitwise search, ties kept in index order).
-__device__ void compact_row_w(float* key, int32_t* id, int cnt, int C, float* thr_out,
-                              int* cnt_out) {
+// threshold by bitwise search, ties kept in index order).  Every key and id is
+// loaded before any is used (lanes past cnt read the last entry and are
+// masked; cnt >= 1 here), so a row costs one memory round trip; the search counts with
+// ballots and scalar popcounts, no cross-lane shuffles; the kept entries are
+// written back from registers (funkey inverts fkey bit for bit).
+__device__ __forceinline__ void compact_row_w(float* key, int32_t* id, int cnt, int C,
+                                              float* thr_out, int* cnt_out) {
     const int lane = threadIdx.x & 63;
     constexpr int R = 16;                      // cap <= 1024
+    cnt = __builtin_amdgcn_readfirstlane(cnt);
+    // lanes of word t that hold an entry: l < cnt - 64 t
+    auto valid = [&](int t) -> uint64_t {
+        const int rem = cnt - t * 64;
+        return rem >= 64 ? ~0ull : rem <= 0 ? 0ull : ((1ull << rem) - 1);
+    };
     uint32_t u[R];
+    int32_t v[R];
+    float kf[R];
 #pragma unroll
-    for (int t = 0; t < R; ++t) {
-        const int i = t * 64 + lane;
-        u[t] = i < cnt ? fkey(key[i]) : 0xffffffffu;
+    for (int t = 0; t < R; ++t) {           // no branch between the loads
+        const int i = min(t * 64 + lane, cnt - 1);
+        kf[t] = key[i];
+        v[t] = id[i];
     }
+#pragma unroll
+    for (int t = 0; t < R; ++t) u[t] = fkey(kf[t]);
     uint32_t lo = 0, hi = 0xffffffffu;
     while (lo < hi) {
         const uint32_t mid = lo + ((hi - lo) >> 1);
         int c = 0;
 #pragma unroll
-        for (int t = 0; t < R; ++t) c += (t * 64 + lane < cnt && u[t] <= mid) ? 1 : 0;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+        for (int t = 0; t < R; ++t)
+            if (t * 64 < cnt) c += __popcll(__ballot(u[t] <= mid) & valid(t));
         if (c >= C) hi = mid; else lo = mid + 1;
     }
     const uint32_t T = lo;
     int nlt = 0;
 #pragma unroll
-    for (int t = 0; t < R; ++t) nlt += (t * 64 + lane < cnt && u[t] < T) ? 1 : 0;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) nlt += __shfl_xor(nlt, off, 64);
+    for (int t = 0; t < R; ++t)
+        if (t * 64 < cnt) nlt += __popcll(__ballot(u[t] < T) & valid(t));
     int eq_left = C - nlt;
     int w = 0;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
     for (int t = 0; t < R; ++t) {
-        const int i = t * 64 + lane;
-        const bool in = i < cnt;
+        if (t * 64 >= cnt) break;
+        const bool in = (valid(t) >> lane) & 1ull;
         const bool is_lt = in && u[t] < T;
         const bool is_eq = in && u[t] == T;
         const uint64_t meq = __ballot(is_eq);
         const int eq_rank = __popcll(meq & below);
         const bool keep = is_lt || (is_eq && eq_rank < eq_left);
         const uint64_t mk = __ballot(keep);
-        const int kid = in ? id[i] : 0;
-        const float kk = in ? key[i] : 0.f;
         if (keep) {
             const int dst = w + __popcll(mk & below);
-            key[dst] = kk;
-            id[dst] = kid;
+            key[dst] = funkey(u[t]);
+            id[dst] = v[t];
         }
         w += __popcll(mk);
         const int used = __popcll(meq);
@@ -471,12 +482,13 @@ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // track it: it cannot tell the stage being read from the stage being filled
 // (they alternate at run time), and would make every fragment read wait for
 // the loads in flight.  The kernel waits for them itself: vmcnt(0) and a
-// barrier before a stage is read.  m0 carries the LDS address (one wait
-// state before the load reads it).
+// barrier before a stage is read.  m0 carries the LDS address: an input
+// operand, so the compiler writes m0 and knows it holds this value; the
+// s_nop is the one wait state the load needs after that write.
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, unsigned char* lds) {
     const unsigned m = (unsigned)(uintptr_t)(lds_vptr)lds;
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :: "v"(voff), "s"(base), "s"(m) : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(base), "{m0}"(m) : "memory");
 }
 
 // WAVES = 8: two waves per SIMD with 128 x 64 wave tiles (128 accumulators);
@@ -608,10 +620,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         __syncthreads();                                // every wave's stage-t loads have landed
         issue(t + 1, kt_f, cb_f);
         adv(kt_f, cb_f);
-        if (kt == 0 && t > 0) {
+        if (kt == 0) {
+          if (t > 0) {
             // compaction flagged by the previous column tile's appends; the
             // flag was set before the barrier above, so every wave reads the
-            // same value, and it is cleared only after every wave has read it
+            // same value, and it is cleared only after every wave has read it.
+            // The accumulators are dead here (the tile's epilogue used them,
+            // and they are zeroed at the end of this branch, where the
+            // compiler can see it), so the compaction may use their registers.
             const int par = tpar ^ 1;    // the tile that just ended
             if (need[par]) {
                 for (int rl = wave; rl < kBM2; rl += WAVES) {
@@ -632,8 +648,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                 __syncthreads();
                 if (tid == 0) need[par] = 0;
             }
-        }
-        if (kt == 0) {
+          }
 #pragma unroll
             for (int i = 0; i < BI; ++i)
 #pragma unroll
