@@ -203,6 +203,41 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
 
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_mfma_sweep_with_duplicate_rows_matches_oracle(metric, dtype):
+    """A larger sweep (n = 12,000: 47 row panels, 47 column tiles, several
+    compactions per row) with rows 0..999 duplicated at 6000..6999, so many
+    rows hold exact ties, some of them at the C-th place: the lists must be
+    the oracle's, and each duplicated row must find its twin."""
+    n, d, C = 12000, 64, 16
+    X = gaussian(n, d, 421 + metric, metric == 0)
+    if metric == 1:
+        X = X * 2.0 + 0.5
+    X[6000:7000] = X[0:1000]
+    if dtype == "f16":
+        X = X.astype(np.float16)
+    Xg = torch.from_numpy(X).cuda()
+    m = "ip" if metric == 0 else "l2"
+    note("mfma sweep with duplicates", dtype, m)
+    cand, cdist = B.knn_candidates(Xg, C, metric=m)
+    oc, od = O.knn_candidates(X.astype(np.float32), C, metric, nthreads=8)
+    cc, cd = cand.cpu().numpy(), cdist.cpu().numpy()
+    same = (cc == oc).mean()
+    note("mfma sweep with duplicates agreement", dtype, m, same)
+    assert same > 0.995
+    scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    assert np.allclose(cd, od, rtol=2e-5, atol=2e-6 * scale)
+    assert ((cc >= 0) & (cc < n)).all()
+    assert not (cc == np.arange(n)[:, None]).any()
+    assert (np.diff(cd, axis=1) >= 0).all()
+    # each duplicated row finds its twin first (distance 0 for l2)
+    twin = np.where(np.arange(n) < 1000, np.arange(n) + 6000,
+                    np.where((np.arange(n) >= 6000) & (np.arange(n) < 7000), np.arange(n) - 6000, -1))
+    rows = np.nonzero(twin >= 0)[0]
+    assert (cc[rows] == twin[rows][:, None]).any(axis=1).all()
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_self_is_last_when_candidates_cover_the_corpus(metric, dtype):
     """C = n: every other row is a candidate and self comes last at 3.4e38
     (build.py:39 sets the self score so).  n = 48 is one row panel, so most
