@@ -131,20 +131,34 @@ __device__ __forceinline__ void compact_row_w(float* key, int32_t* id, int cnt, 
     }
 #pragma unroll
     for (int t = 0; t < R; ++t) u[t] = fkey(kf[t]);
-    uint32_t lo = 0, hi = 0xffffffffu;
+    // search over the list's own key range; the words past cnt count
+    // nothing (their valid mask is 0), so the counting runs without branches
+    uint32_t mn = 0xffffffffu, mx = 0;
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const bool in = (valid(t) >> lane) & 1ull;
+        mn = in && u[t] < mn ? u[t] : mn;
+        mx = in && u[t] > mx ? u[t] : mx;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t x = __shfl_xor(mn, off, 64), y = __shfl_xor(mx, off, 64);
+        mn = x < mn ? x : mn;
+        mx = y > mx ? y : mx;
+    }
+    uint32_t lo = __builtin_amdgcn_readfirstlane(mn), hi = __builtin_amdgcn_readfirstlane(mx);
+    if (cnt < C) lo = hi = 0xffffffffu;
     while (lo < hi) {
         const uint32_t mid = lo + ((hi - lo) >> 1);
         int c = 0;
 #pragma unroll
-        for (int t = 0; t < R; ++t)
-            if (t * 64 < cnt) c += __popcll(__ballot(u[t] <= mid) & valid(t));
+        for (int t = 0; t < R; ++t) c += __popcll(__ballot(u[t] <= mid) & valid(t));
         if (c >= C) hi = mid; else lo = mid + 1;
     }
     const uint32_t T = lo;
     int nlt = 0;
 #pragma unroll
-    for (int t = 0; t < R; ++t)
-        if (t * 64 < cnt) nlt += __popcll(__ballot(u[t] < T) & valid(t));
+    for (int t = 0; t < R; ++t) nlt += __popcll(__ballot(u[t] < T) & valid(t));
     int eq_left = C - nlt;
     int w = 0;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
