@@ -107,7 +107,7 @@ def test_corpus_layout_and_offline_cli(tmp_path, metric):
     # candidates from an existing graph
     OF.main(["--data", str(d), "--D", "24", "--cand", "24", "--cand-graph", "G_knn.npy",
              "--out", "G_cg.npy"])
-    index = swann.Index(torch.from_numpy(np.ascontiguousarray(Xs)).cuda(),
+    index = swann.Index(torch.from_numpy(np.array(Xs, dtype=Xs.dtype, copy=True)).cuda(),
                         torch.from_numpy(np.load(d / "G_cg.npy")).cuda(), metric=metric)
     got, _ = index.search(Qs, k=10, branches=16, queue=24)
     r = np.mean([len(set(a) & set(b)) / 10 for a, b in zip(got, ids)])
