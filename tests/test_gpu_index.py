@@ -201,6 +201,33 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
 
 
+@pytest.mark.parametrize("switch", [("SWANN_SWEEP_WAVES", "8"), ("SWANN_SWEEP_REGSTAGE", "1")])
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtype):
+    """The direct-load sweep's 8-wave layout (128 x 64 wave tiles) and the
+    register-staged kernel, both chosen by environment at each call, keep
+    the oracle's lists like the default layout."""
+    monkeypatch.setenv(*switch)
+    n, d = 3001, 64
+    X = gaussian(n, d, 431 + metric, metric == 0)
+    if metric == 1:
+        X = X * 3.0 + 1.5
+    if dtype == "f16":
+        X = X.astype(np.float16)
+    Xg = torch.from_numpy(X).cuda()
+    m = "ip" if metric == 0 else "l2"
+    note("mfma sweep layout", switch, dtype, m)
+    cand, cdist = B.knn_candidates(Xg, 40, metric=m)
+    oc, od = O.knn_candidates(X.astype(np.float32), 40, metric, nthreads=8)
+    same = (cand.cpu().numpy() == oc).mean()
+    note("mfma sweep layout agreement", switch, dtype, m, same)
+    assert same > 0.995
+    scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
+    assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
+
+
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_with_duplicate_rows_matches_oracle(metric, dtype):
