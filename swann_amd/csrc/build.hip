@@ -301,52 +301,83 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
                                  int C, float* gram, float* vn, unsigned char* stg) {
     constexpr int EPC = 16 / sizeof(XT);           // elements per 16-byte chunk
     constexpr int KC = kStgRow / sizeof(XT);       // elements of a row per K chunk
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const bool busy = w * 32 < C;                  // C: one past the last valid candidate
-    f32x16v acc[4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the 10 upper-triangle 32 x 32 tiles (i <= j) of the 128 x 128 Gram,
+    // three or two per wave (a wave per row block would give wave 0 four
+    // and wave 3 one); tiles past C (one past the last valid candidate)
+    // are skipped
+    constexpr int kTI[4][3] = {{0, 0, 0}, {0, 1, 1}, {1, 2, -1}, {2, 3, -1}};
+    constexpr int kTJ[4][3] = {{0, 1, 2}, {3, 1, 2}, {3, 2, -1}, {3, 3, -1}};
+    int ti[3], tj[3];
+    bool on[3];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int x = 0; x < 3; ++x) {
+        ti[x] = kTI[w][x];
+        tj[x] = kTJ[w][x];
+        on[x] = ti[x] >= 0 && ti[x] * 32 < C && tj[x] * 32 < C;
+    }
+    const bool busy = on[0] || on[1] || on[2];
+    f32x16v acc[3];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
-    const int ar = w * 32 + (lane & 31);
+    for (int x = 0; x < 3; ++x)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[x][e] = 0.f;
     const int half = lane >> 5;
+    // staging: 128 rows x 8 chunks, 4 per thread; the next K chunk's loads
+    // go out before this chunk's MFMAs, so their latency hides behind them
+    const int rows = (C + 31) & ~31;               // rows some tile reads
+    int sid[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = (q * 256 + tid) >> 3;
+        const int id = r < C ? cid[r] : -1;
+        sid[q] = r < rows && id >= 0 && id < n ? id : -1;
+    }
+    uint4 nxt[4];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int k = k0 + ((q * 256 + tid) & 7) * EPC;
+            nxt[q] = make_uint4(0u, 0u, 0u, 0u);
+            if (sid[q] >= 0 && k < dim)
+                nxt[q] = *reinterpret_cast<const uint4*>(X + (int64_t)sid[q] * dim + k);
+        }
+    };
+    fetch(0);
     for (int k0 = 0; k0 < dim; k0 += KC) {
-        // stage: 128 rows x 8 chunks, 4 per thread
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = q * 256 + tid;
             const int r = e >> 3, c = e & 7;
-            if (r >= ((C + 31) & ~31)) continue;     // rows no tile reads
-            const int id = r < C ? cid[r] : -1;
-            const int k = k0 + c * EPC;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (id >= 0 && id < n && k < dim)
-                v = *reinterpret_cast<const uint4*>(X + (int64_t)id * dim + k);
-            *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = v;
+            if (r < rows)
+                *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = nxt[q];
         }
         __syncthreads();
+        if (k0 + KC < dim) fetch(k0 + KC);
         if (busy) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int ch = 2 * t + half;
-                const uint4 ra = *reinterpret_cast<const uint4*>(stg + ar * kStgRow +
-                                                                 ((ch ^ pswz(ar)) << 4));
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j < w || j * 32 >= C) continue;
-                    const int br = j * 32 + (lane & 31);
+                for (int x = 0; x < 3; ++x) {
+                    if (!on[x]) continue;
+                    const int ar = ti[x] * 32 + (lane & 31);
+                    const int br = tj[x] * 32 + (lane & 31);
+                    const uint4 ra = *reinterpret_cast<const uint4*>(stg + ar * kStgRow +
+                                                                     ((ch ^ pswz(ar)) << 4));
                     const uint4 rb = *reinterpret_cast<const uint4*>(stg + br * kStgRow +
                                                                      ((ch ^ pswz(br)) << 4));
                     if constexpr (sizeof(XT) == 2) {
-                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(h16x8, ra), __builtin_bit_cast(h16x8, rb), acc[j],
+                        acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(h16x8, ra), __builtin_bit_cast(h16x8, rb), acc[x],
                             0, 0, 0);
                     } else {
                         const f32x4v fa = __builtin_bit_cast(f32x4v, ra);
                         const f32x4v fb = __builtin_bit_cast(f32x4v, rb);
 #pragma unroll
                         for (int s2 = 0; s2 < 4; ++s2)
-                            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[s2], fb[s2], acc[j],
+                            acc[x] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[s2], fb[s2], acc[x],
                                                                           0, 0, 0);
                     }
                 }
@@ -356,15 +387,15 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
     }
     if (!busy) return;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (j < w) continue;
-        const int cc = j * 32 + (lane & 31);
+    for (int x = 0; x < 3; ++x) {
+        if (!on[x]) continue;
+        const int cc = tj[x] * 32 + (lane & 31);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const int r = w * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            const int r = ti[x] * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
             if (r < C && cc < C) {
-                if (r < cc) gram[tri(r, cc)] = acc[j][e];
-                else if (r == cc) vn[r] = acc[j][e];
+                if (r < cc) gram[tri(r, cc)] = acc[x][e];
+                else if (r == cc) vn[r] = acc[x][e];
             }
         }
     }
