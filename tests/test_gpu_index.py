@@ -416,24 +416,27 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
     assert same > 0.97
 
 
+@pytest.mark.parametrize("C", [48, 100])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 @pytest.mark.parametrize("metric", [0, 1])
-def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, monkeypatch):
+def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
     """The prune's Gram on MFMA -- fp16 rows: exact products, fp32 sums
     (32x32x16 f16); fp32 rows: fp32 products and sums (32x32x2 f32) -- keeps
     the same rows as the fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle
     (double dots) up to near-ties.  d = 80 leaves a ragged last K group for
-    fp16; per-node caps and protect ride along."""
+    fp16; C = 48 fills two of the four 32-row blocks (three of the ten Gram
+    tiles), C = 100 all four with a ragged last (every tile, every wave);
+    per-node caps and protect ride along."""
     X = gaussian(3000, 80, 71 + metric, metric == 0)
     if metric == 1:
         X = X * 2.0 + 0.5
     X16 = X.astype(np.float16) if dtype == "f16" else X.astype(np.float32)
     m = "ip" if metric == 0 else "l2"
     Xg = torch.from_numpy(X16).cuda()
-    cand, cdist = B.knn_candidates(Xg, 48, metric=m)
+    cand, cdist = B.knn_candidates(Xg, C, metric=m)
     rng = np.random.default_rng(8)
     dpn = np.where(rng.random(3000) < 0.2, 32, 20).astype(np.int32)
-    prot = rng.random((3000, 48)) < 0.1
+    prot = rng.random((3000, C)) < 0.1
     kw = dict(alpha=1.2, metric=m, deg_per_node=torch.from_numpy(dpn).cuda(),
               protect=torch.from_numpy(prot).cuda())
     g_mfma = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
