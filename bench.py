@@ -63,7 +63,7 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # the source without comments) and the same workload and knobs; otherwise
 # `traffic` is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "c3193a44dd261467"): 5.410e12,
+    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "85fab237a8f76b62"): 5.410e12,
 }
 
 

@@ -41,8 +41,9 @@ constexpr int kCprobe = 32;            // bounded probe into the shared table
 #endif
 constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in flight
 // Scope of the per-query table and bound operations.  A query's branches are
-// placed on one XCD (xcd_remap), whose L2 is the coherence point for all of
-// them; workgroup-scope accesses are served there, agent scope goes past it.
+// placed on one XCD (xcd_remap) when they all fit there at once, and spread
+// over the XCDs otherwise (remap_branches), so these must be agent scope,
+// which is coherent across the XCDs' separate L2s.
 #ifndef SWANN_TABLE_SCOPE
 #define SWANN_TABLE_SCOPE __HIP_MEMORY_SCOPE_AGENT
 #endif
@@ -476,6 +477,7 @@ struct AdvArgs {
     const int32_t* active; int64_t nblocks, nbranch, n;
     int vec_ok;
     const int32_t* codes; const float* calpha; const float* cmu; int cwords; float cmargin;
+    int remap;                   // xcd_remap the blocks (a query's branches on one XCD)
 };
 
 template <int TEAM, typename XT, int BLOCK>
@@ -484,7 +486,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     constexpr int NT = BLOCK / TEAM;
     const int tid = threadIdx.x, team = tid / TEAM, tl = tid % TEAM;
     const int lane = tid & 63, wave = tid >> 6;
-    const int64_t pos = xcd_remap(blockIdx.x, a.nblocks);
+    const int64_t pos = a.remap ? xcd_remap(blockIdx.x, a.nblocks) : (int64_t)blockIdx.x;
     const int64_t flat = a.active ? (int64_t)a.active[pos] : pos;
     if (flat < 0 || flat >= a.nbranch) return;          // a bad active entry: no work
     const int64_t q = flat / a.J;
@@ -964,6 +966,55 @@ bool rows_vec_ok(const void* X, int dim, int x_dtype) {
         }                                                                                 \
     } while (0)
 
+// Workgroups of one advance_kernel instance a CU holds at once (registers
+// and LDS), from the runtime's occupancy query; 0 if the query fails.
+template <int TEAM, typename XT>
+int advance_occupancy(int block, size_t lds) {
+    int v = 0;
+    hipError_t e;
+    if (block == 64)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 64>, 64, lds);
+    else if (block == 256)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 256>, 256, lds);
+    else
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 1024>, 1024,
+                                                         lds);
+    return e == hipSuccess ? v : 0;
+}
+
+// Whether the advance puts a query's branches on one XCD (xcd_remap), where
+// they share an L2: only when all J of them fit among the workgroups one XCD
+// holds at once.  Otherwise they would run in successive rounds, and the
+// late ones find the early ones' nodes claimed and their bound set (at 128
+// branches a query, 256 or 1024 threads a branch, recall@10 fell from 0.79 to
+// 0.72 and 0.53), so the blocks keep their dispatch order instead, which
+// spreads a query's branches over the XCDs; the visited table's atomics are
+// agent scope and stay coherent across XCDs.
+bool remap_branches(int J, int team, int x_dtype, int block, size_t lds) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    int per_cu = 0;
+    const bool f32 = x_dtype == SWANN_DTYPE_F32;
+    switch (team) {
+        case 4: per_cu = f32 ? advance_occupancy<4, float>(block, lds)
+                             : advance_occupancy<4, _Float16>(block, lds); break;
+        case 8: per_cu = f32 ? advance_occupancy<8, float>(block, lds)
+                             : advance_occupancy<8, _Float16>(block, lds); break;
+        case 16: per_cu = f32 ? advance_occupancy<16, float>(block, lds)
+                              : advance_occupancy<16, _Float16>(block, lds); break;
+        case 32: per_cu = f32 ? advance_occupancy<32, float>(block, lds)
+                              : advance_occupancy<32, _Float16>(block, lds); break;
+        default: per_cu = f32 ? advance_occupancy<64, float>(block, lds)
+                              : advance_occupancy<64, _Float16>(block, lds); break;
+    }
+    if (per_cu <= 0) (void)hipGetLastError();
+    return (int64_t)J <= (int64_t)(cus / kNumXcd) * per_cu;
+}
+
 }  // namespace
 }  // namespace swann
 
@@ -1087,6 +1138,7 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
               codes, codes ? alpha : nullptr, codes ? cmu : nullptr, codes ? cwords : 0,
               code_margin};
     const int block = search_block_for(nb);
+    a.remap = remap_branches(J, team_size, x_dtype, block, advance_lds(dim, D, L)) ? 1 : 0;
     SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
                    advance_lds(dim, D, L), (hipStream_t)stream, a);
     return launch_status("advance");
