@@ -621,3 +621,25 @@ def test_nan_distances_never_enter_a_queue():
         assert not np.isin(ids[live], bad).any()
         assert (ids[3] == -1).all()
         assert live[0].any() and live[2].any()
+
+
+def test_branches_spread_over_xcds_match_oracle(monkeypatch):
+    """48 branches a query of 1024 threads do not fit the 32 workgroups one XCD
+    holds, so the advance keeps dispatch order instead of grouping a query's
+    branches on one XCD: every branch must still find its own (query,
+    branch) state.  Independent branches, queues bit-exact against the
+    oracle."""
+    monkeypatch.setenv("SWANN_SEARCH_BLOCK", "1024")
+    X, G = toy(seed=131)
+    rng = np.random.default_rng(132)
+    nq, J = 3, 48
+    Qv = gaussian(nq, 64, 133, True)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg = to_gpu(X, G, Qv)
+    st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=12, B=30, D=32, team_size=16,
+                       stop_eps=0.05)
+    E.advance(Xg, Gg, Qg, st, 30)
+    for qi in range(nq):
+        for j in range(0, J, 5):
+            br = O.run(X, G, Qv[qi], int(seeds[qi, j]), L=12, B=30, team=16, stop_eps=0.05)
+            assert_queue(st, qi, j, br, (qi, j))
