@@ -51,7 +51,7 @@ C4_BATCHES = (1, 8, 64, 512)
 EPS_SWEEP = (0.02, 0.05, 0.1, 0.2)
 # If no stop_eps reaches the target at the configured knobs, the search effort
 # is raised along this ladder (branches, queue, budget, stop_eps), cheapest first.
-LADDER = ((64, 32, 64, 0.3), (64, 48, 64, 0.2), (96, 32, 64, 0.3), (64, 48, 128, 0.3),
+LADDER = ((64, 32, 64, 0.3), (64, 44, 64, 0.3), (64, 48, 64, 0.2), (96, 32, 64, 0.3), (64, 48, 128, 0.3),
           (128, 24, 128, 0.2), (128, 32, 64, 0.3), (64, 64, 128, 0.3), (128, 48, 128, 0.3))
 TARGET_RECALL = 0.95
 HBM_PEAK = 8.0e12
@@ -64,6 +64,7 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # `traffic` is reported as null.
 PMC_TRAFFIC = {
     ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "85fab237a8f76b62"): 5.410e12,
+    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "85fab237a8f76b62"): 5.045e12,
 }
 
 
