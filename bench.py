@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+from types import SimpleNamespace
 import os
 import sys
 import time
@@ -60,11 +61,10 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # WRITE_SIZE x 1.000, the factors a 2 GiB device copy reads; see
 # profiles/advance_kernel_c3_hbm_traffic.md).  Valid only for the kernel source it
 # was measured on (kernel_source_key of swann_amd/csrc/search.hip: SHA-256 prefix of
-# the source without comments) and the same workload and knobs; otherwise
-# `traffic` is reported as null.
+# the source without comments), the same workload and knobs and the same per-query
+# table size (Index._table_slots); otherwise `traffic` is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 48, 64, 0.2, "85fab237a8f76b62"): 5.410e12,
-    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "85fab237a8f76b62"): 5.045e12,
+    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, 524_288, "85fab237a8f76b62"): 4.994e12,
 }
 
 
@@ -214,7 +214,9 @@ class Searcher:
         st = E.init_states(ix.X, self.Q, seeds, L=cfg["queue"], B=cfg["budget"], D=ix.G.shape[1],
                            metric=ix._m, team_size=cfg["team"], stop_eps=eps, kstop=self.k,
                            shared_cache=True, shared_bound=True, exclusive=True,
-                           elide_visited=True)
+                           elide_visited=True,
+                           cache_slots=ix._table_slots(self.Q.shape[0], SimpleNamespace(
+                               branches=cfg["branches"], budget=cfg["budget"])))
         if record:
             ev[2].record()
         E.advance(ix.X, ix.G, self.Q, st, cfg["budget"], codes=self.codes)
@@ -596,8 +598,10 @@ def main():
     achieved = adv_bytes / adv_s
     ph_mean = {k2: round(float(np.mean([p[k2] for p in phases])), 3) for k2 in phases[0]}
     src_sha = kernel_source_key(ROOT / "swann_amd" / "csrc" / "search.hip")
+    slots = index._table_slots(nq, SimpleNamespace(branches=cfg["branches"],
+                                                   budget=cfg["budget"]))
     traffic = PMC_TRAFFIC.get((a.config, n, nq, cfg["branches"], cfg["queue"], cfg["budget"],
-                               eps, src_sha))
+                               eps, slots, src_sha))
 
     cpu = None
     if not a.no_cpu and a.cpu_sample > 0:

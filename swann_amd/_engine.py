@@ -171,7 +171,7 @@ def _check_corpus(X, Qv):
 def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32,
                 policy=POLICY_BEST, stop_eps=-1.0, kstop=10, shared_cache=False,
                 shared_bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0,
-                elide_visited=False) -> SearchState:
+                elide_visited=False, cache_slots=None) -> SearchState:
     """One state per (query, branch); swann/_engine.py:219-278.
 
     `seeds` is int32 [Q, J] (one entry per branch) or [Q, J, V] (V entries
@@ -199,7 +199,10 @@ def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32
         stop_eps=float(stop_eps), kstop=int(kstop), stall_patience=int(stall_patience),
         crowd_frac=float(crowd_frac))
     if shared_cache and J > 1:
-        Hc = cache_size(J, B, D)
+        # cache_slots (a power of two) replaces the closed-form size
+        Hc = int(cache_slots) if cache_slots else cache_size(J, B, D)
+        if Hc & (Hc - 1):
+            raise ValueError(f"cache_slots must be a power of two, got {Hc}")
         # one allocation of (id, d) pairs: a claim and the distance later
         # stored into it share a cache line; cache_id / cache_d are views
         tab = torch.empty((Q, Hc, 2), dtype=torch.int32, device=dev)
@@ -352,7 +355,7 @@ def advance_chunked(X, G, Qv, state: SearchState, total: int, chunk: int, codes=
 def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
            policy=POLICY_BEST, stop_eps=-1.0, shared_cache=False, shared_bound=False,
            exclusive=False, stall_patience=0, crowd_frac=0.0, elide_visited=False, chunk=0,
-           codes=None, check=None):
+           codes=None, check=None, cache_slots=None):
     """init -> advance(budget) -> per-branch best-k -> merged top-k
     (swann/_engine.py:428-447).  `check` overrides the global overflow guard:
     True checks synchronously, False skips it."""
@@ -360,7 +363,7 @@ def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
                      policy=policy, stop_eps=stop_eps, kstop=k, shared_cache=shared_cache,
                      shared_bound=shared_bound, exclusive=exclusive,
                      stall_patience=stall_patience, crowd_frac=crowd_frac,
-                     elide_visited=elide_visited)
+                     elide_visited=elide_visited, cache_slots=cache_slots)
     if chunk:
         advance_chunked(X, G, Qv, st, B, chunk, codes=codes)
     else:
