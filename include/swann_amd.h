@@ -165,8 +165,10 @@ int swann_enforce_min_in(int32_t* G, int64_t n, int W, const int32_t* cand, int 
                          int rounds, void* workspace, void* stream);
 
 /* Per-query dedup top-k of branch results (merge_branches_kernel,
- * local_search.cu:863-919).  bids/bdist [Q, V, kk] -> out [Q, k]; missing
- * entries are (-1, +inf).  Needs V*kk <= 8192. */
+ * local_search.cu:863-919).  bids/bdist [Q, V, kk] -> out [Q, k], 1 <= k <=
+ * V*kk: entries in (distance, id) order, invalid ids (< 0) last, an entry
+ * dropped when its id equals its predecessor's in that order; missing entries
+ * are (-1, +inf).  Any V*kk (no shared-memory limit). */
 int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk,
                          int k, int32_t* out_ids, float* out_dist, void* stream);
 

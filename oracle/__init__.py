@@ -31,6 +31,8 @@ LIB = HERE / "_build" / "libswann_oracle.so"
 
 METRIC_IP, METRIC_L2 = 0, 1
 POLICY_BEST, POLICY_ROUND_ROBIN = 0, 1
+# when a branch's step reads the shared bound (so_search_query)
+SCHEDULES = {"serial": 0, "rounds": 1}
 NCTR = 10
 F32, F16 = 0, 1
 
@@ -77,10 +79,10 @@ def _declare(L):
     L.so_merge.argtypes = [P, P, I64, I, I, I, P, P]
     L.so_search_query.restype = None
     L.so_search_query.argtypes = [P, I, I, P, I, P, P, I, I, I, I, I, I, I, I, F, I,
-                                  I, I, I, I, F, P, P, P, P, P, P, P, P, P, P, I, P, P, F]
+                                  I, I, I, I, F, P, P, P, P, P, P, P, P, P, P, I, P, P, F, I]
     L.so_search_batch.restype = None
     L.so_search_batch.argtypes = [P, I, I, P, I, P, I64, P, I, I, I, I, I, I, I, I,
-                                  F, I, I, I, I, I, P, P, P, I]
+                                  F, I, I, I, I, I, P, P, P, I, I]
     L.so_topk_rows.restype = None
     L.so_topk_rows.argtypes = [P, I64, P, I64, I, I, I, I64, P, P, I]
     L.so_robust_prune.restype = None
@@ -226,9 +228,13 @@ def cache_size(J, B, D, share=4.0, cap=1 << 20):
 def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                  policy=POLICY_BEST, stop_eps=-1.0, kstop=10, H=None, Hc=0,
                  bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0,
-                 codes=None):
+                 codes=None, schedule="serial"):
     """All J branches of one query, stepped in turn (every step atomic).
-    seeds: [J] or [J, V].  Returns a dict of [J, ...] arrays."""
+    seeds: [J] or [J, V].  Returns a dict of [J, ...] arrays.
+
+    schedule "serial": a step reads the bound as the steps before it left it;
+    "rounds": every step of round s reads the bound as it was when the round
+    began (a concurrent launch's shape: a query's branches start together)."""
     X, dt = _corpus(X)
     cp, cw, ap, mp, mg, _keep = _codes(codes)
     G = np.ascontiguousarray(G, dtype=np.int32)
@@ -249,14 +255,14 @@ def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                           int(kstop), int(Hc), int(bool(bound)), int(bool(exclusive)),
                           int(stall_patience), float(crowd_frac),
                           _p(ids), _p(dist), _p(expd), _p(lin), _p(vis), _p(ctr),
-                          _p(cid), _p(cdd), _p(bnd), cp, cw, ap, mp, mg)
+                          _p(cid), _p(cdd), _p(bnd), cp, cw, ap, mp, mg, SCHEDULES[schedule])
     return dict(ids=ids, dist=dist, expanded=expd, lineage=lin, visited=vis,
                 counters=ctr, cache_id=cid[:Hc], cache_d=cdd[:Hc], bound=bnd[0])
 
 
 def search_batch(X, G, Q, seeds, k=10, L=16, B=16, metric=METRIC_IP, team=32,
                  policy=POLICY_BEST, stop_eps=-1.0, H=None, Hc=0, bound=False,
-                 exclusive=False, nthreads=0, counters=False):
+                 exclusive=False, nthreads=0, counters=False, schedule="serial"):
     """search_query + merge for every query (OpenMP over queries).
     seeds: [nq, J] or [nq, J, V]."""
     X, dt = _corpus(X)
@@ -274,7 +280,7 @@ def search_batch(X, G, Q, seeds, k=10, L=16, B=16, metric=METRIC_IP, team=32,
                           J, V, L, B, H, int(metric), int(team), int(policy),
                           float(stop_eps), int(k), int(Hc), int(bool(bound)),
                           int(bool(exclusive)), int(k), _p(oi), _p(od), _p(oc),
-                          int(nthreads))
+                          int(nthreads), SCHEDULES[schedule])
     return (oi, od, oc) if counters else (oi, od)
 
 

@@ -42,6 +42,8 @@
 
 #define SO_NCTR 10
 #define SO_CPROBE 32
+#define SO_SCHED_SERIAL 0   /* so_search_query: bound read as the previous step left it */
+#define SO_SCHED_ROUNDS 1   /* ... as it was when the round began */
 #define SO_MAXD 128
 #define SO_MAXL 512
 
@@ -231,6 +233,9 @@ typedef struct {
     int max_exp, policy, V;
     float stop_eps; int kstop;
     int32_t* cid; float* cdd; int Hc; float* bound; int exclusive;
+    /* where a step reads the bound (NULL: *bound itself).  The rounds
+     * schedule points it at the value the bound had when the round began. */
+    const float* bound_rd;
     int stall_patience; float crowd_frac;
     /* sign-code filter (local_search.cu:205-243, :560-575); codes == NULL: off */
     const int32_t* codes; int cwords; const float* calpha; float qmu, qsum, cmargin;
@@ -293,7 +298,7 @@ static int so_step(const so_cfg* c, int32_t* ids, float* dist, uint8_t* expd, ui
     const int kr = (c->kstop < L) ? c->kstop : L;
     float radius = (kr > 0 && ids[kr - 1] >= 0) ? dist[kr - 1] : FLT_MAX;
     if (c->bound) {
-        const float gb = *c->bound;
+        const float gb = c->bound_rd ? *c->bound_rd : *c->bound;
         if (gb < radius) radius = gb;
     }
     const float limit = (radius == FLT_MAX) ? FLT_MAX : radius * (1.0f + c->stop_eps);
@@ -501,12 +506,22 @@ void so_merge(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk,
 }
 
 /* ------------------------------------------------------------------ */
-/* A whole search of one query with J branches in one legal serial
- * schedule of the kernel: init every branch, then step the branches in
- * turn (branch 0 step s, branch 1 step s, ...).  Shared cache, bound and
- * claims behave as in local_search.cu with every step atomic.  With the
- * cache, bound and claims off the branches are independent and the result
- * equals J separate branch runs. */
+/* A whole search of one query with J branches in one legal schedule of the
+ * kernel: init every branch, then step the branches in turn (branch 0 step s,
+ * branch 1 step s, ...).  Shared cache, bound and claims behave as in
+ * local_search.cu with every step atomic.  With the cache, bound and claims
+ * off the branches are independent and the result equals J separate branch
+ * runs.
+ *
+ * sched SO_SCHED_SERIAL: each step reads the bound as the steps before it
+ * left it.  SO_SCHED_ROUNDS: every step of round s reads the bound as it was
+ * when round s began (updates still land at once, claims are still seen at
+ * once).  Both are interleavings the kernel allows -- a branch's bound read
+ * (local_search.cu:466-469) may come before another branch's lowering
+ * (:655-658) and its claims after them.  Rounds is the concurrent launch's
+ * shape, where a query's branches start together and a step sees the
+ * others' previous steps; serial lets branch 0's first expansion set the
+ * bound before any other branch has expanded its seed. */
 void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
                      const float* q, const int32_t* seeds /* [J][V] */, int J, int V,
                      int L, int B, int H, int metric, int team, int policy,
@@ -516,7 +531,7 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
                      int32_t* visited, int32_t* counters,
                      int32_t* cache_id, float* cache_d, float* bound_out,
                      const int32_t* codes, int cwords, const float* calpha, const float* cmu,
-                     float cmargin) {
+                     float cmargin, int sched) {
     for (int t = 0; t < Hc; ++t) { cache_id[t] = 0; cache_d[t] = FLT_MAX; }
     float bound = FLT_MAX;
     for (int j = 0; j < J; ++j)
@@ -542,6 +557,8 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
     for (int j = 0; j < J; ++j) so_locals_reset(&lo[j]);
     for (int s = 0; s < B; ++s) {
         int alive = 0;
+        const float snap = bound;
+        c.bound_rd = (sched == SO_SCHED_ROUNDS) ? &snap : NULL;
         for (int j = 0; j < J; ++j) {
             if (lo[j].done) continue;
             if (!so_step(&c, ids + (int64_t)j * L, dist + (int64_t)j * L,
@@ -564,7 +581,7 @@ void so_search_batch(const void* X, int dt, int dim, const int32_t* G, int D,
                      int L, int B, int H, int metric, int team, int policy,
                      float stop_eps, int kstop, int Hc, int use_bound, int exclusive,
                      int k, int32_t* out_ids, float* out_dist, int32_t* out_counters,
-                     int nthreads) {
+                     int nthreads, int sched) {
     const int kk = k < L ? k : L;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -588,7 +605,7 @@ void so_search_batch(const void* X, int dt, int dim, const int32_t* G, int D,
             so_search_query(X, dt, dim, G, D, Qv + qi * dim, seeds + qi * (int64_t)J * V, J, V,
                             L, B, H, metric, team, policy, stop_eps, kstop, Hc, use_bound,
                             exclusive, 0, 0.0f, ids, dist, expd, lin, vis, ctr, cid, cdd, NULL,
-                            NULL, 0, NULL, NULL, 0.0f);
+                            NULL, 0, NULL, NULL, 0.0f, sched);
             for (int j = 0; j < J; ++j)
                 for (int t = 0; t < kk; ++t) {
                     bi[j * kk + t] = ids[j * L + t];

@@ -148,15 +148,19 @@ def ctypes_ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-# Whether `search` checks, synchronously, that no visited table overflowed.
+# `search` and `Index.search` read the branches' failed-insert counters after
+# every search and raise if any is nonzero.  A caller whose table sizes are
+# known to fit can switch that off and read `state.overflow()` when it likes.
 _OVERFLOW_GUARD = True
 
 
 def overflow_guard(on: bool) -> bool:
-    """Turn the per-search overflow check on or off. Returns the old setting."""
+    """Enable or disable the overflow check made after every search; the
+    previous setting is returned (swann/_engine.py:203-216)."""
     global _OVERFLOW_GUARD
-    was, _OVERFLOW_GUARD = _OVERFLOW_GUARD, bool(on)
-    return was
+    previous = _OVERFLOW_GUARD
+    _OVERFLOW_GUARD = bool(on)
+    return previous
 
 
 def _check_corpus(X, Qv):
@@ -275,22 +279,27 @@ def advance(X, G, Qv, state: SearchState, delta_expansions: int, active=None,
     return state
 
 
+_CODE_FILES = ("codes", "alpha", "mu")
+
+
 def load_codes(data, name=None, margin=0.20, device="cuda"):
-    """The sign code, its per-node scale and the corpus mean, as `advance`
-    wants them (swann/_engine.py:320-337): codes_<name>.npy, alpha_<name>.npy
-    and mu_<name>.npy under `data`; `name` defaults from manifest.json's
-    metric ("1bit" for ip).  `margin` is in the corpus's distance units."""
+    """`(codes, alpha, mu, margin)` for `advance(codes=...)`, read from
+    codes_<name>.npy, alpha_<name>.npy and mu_<name>.npy in the corpus
+    directory `data` (swann/_engine.py:320-337).  Without `name`, the corpus's
+    manifest.json decides: "1bit" for an ip metric, "int8" otherwise.
+    `margin` is in the corpus's distance units."""
     import json
     from pathlib import Path
     import numpy as np
-    d = Path(data)
+    root = Path(data)
     if name is None:
-        man = json.loads((d / "manifest.json").read_text())
-        name = "1bit" if man["metric"].startswith("ip") else "int8"
-    cd = torch.from_numpy(np.load(d / f"codes_{name}.npy")).to(device)
-    al = torch.from_numpy(np.load(d / f"alpha_{name}.npy")).to(device)
-    cm = torch.from_numpy(np.load(d / f"mu_{name}.npy")).to(device)
-    return cd.contiguous(), al.contiguous(), cm.contiguous(), margin
+        metric = json.loads((root / "manifest.json").read_text())["metric"]
+        name = "1bit" if metric.startswith("ip") else "int8"
+    codes, alpha, mu = (
+        torch.as_tensor(np.ascontiguousarray(np.load(root / f"{stem}_{name}.npy",
+                                                     allow_pickle=False)), device=device)
+        for stem in _CODE_FILES)
+    return codes, alpha, mu, margin
 
 
 def branch_topk(state: SearchState, k: int):
@@ -300,54 +309,43 @@ def branch_topk(state: SearchState, k: int):
 
 
 def merge_branches(ids: torch.Tensor, dist: torch.Tensor, k: int, fused: bool = True):
-    """Branch results -> one top-k per query, duplicates removed by id
-    (swann/_engine.py:358-374).  The fused path is one kernel; the tensor path
-    serves shapes the kernel refuses (more than 8192 candidates per query)."""
-    if fused and ids.is_cuda and ids.dim() == 3 and ids.shape[1] * ids.shape[2] <= 8192:
-        ids = ids.contiguous().to(torch.int32)
-        dist = dist.contiguous().float()
-        Q, V, kk = ids.shape
-        oi = torch.empty((Q, k), dtype=torch.int32, device=ids.device)
-        od = torch.empty((Q, k), dtype=torch.float32, device=ids.device)
-        with torch.cuda.device(ids.device):
-            call("swann_merge_branches", ptr(ids), ptr(dist), Q, V, kk, int(k), ptr(oi), ptr(od),
-                 stream_of(ids.device))
-        return oi, od
-    return _merge_branches_tensor(ids, dist, k)
+    """Branch results [Q, V, kk] -> one top-k per query in (distance, id) order,
+    duplicates removed by id (swann/_engine.py:358-374).  One kernel serves
+    every shape (a successor walk over (distance, id) keys, no V*kk limit);
+    `fused` is accepted for the reference's signature and changes nothing."""
+    if not (ids.is_cuda and dist.is_cuda) or ids.dim() != 3 or tuple(dist.shape) != tuple(ids.shape):
+        raise RuntimeError("merge_branches: ids and dist must be cuda tensors of shape [Q, V, kk]")
+    ids = ids.contiguous().to(torch.int32)
+    dist = dist.contiguous().float()
+    Q, V, kk = ids.shape
+    oi = torch.empty((Q, k), dtype=torch.int32, device=ids.device)
+    od = torch.empty((Q, k), dtype=torch.float32, device=ids.device)
+    with torch.cuda.device(ids.device):
+        call("swann_merge_branches", ptr(ids), ptr(dist), Q, V, kk, int(k), ptr(oi), ptr(od),
+             stream_of(ids.device))
+    return oi, od
 
 
-def _merge_branches_tensor(ids: torch.Tensor, dist: torch.Tensor, k: int):
-    """The merge as tensor operations (swann/_engine.py:377-402)."""
-    Q = ids.shape[0]
-    flat_i = ids.reshape(Q, -1).to(torch.int64)
-    flat_d = dist.reshape(Q, -1).clone()
-    flat_d[flat_i < 0] = float("inf")
-    order = torch.argsort(flat_i, dim=1, stable=True)
-    sd = torch.gather(flat_d, 1, order)
-    si = torch.gather(flat_i, 1, order)
-    dup = torch.zeros_like(si, dtype=torch.bool)
-    dup[:, 1:] = (si[:, 1:] == si[:, :-1]) & (si[:, 1:] >= 0)
-    sd = sd.masked_fill(dup, float("inf"))
-    si = si.masked_fill(dup, -1)
-    kk = min(k, sd.shape[1])
-    best_d, pos = torch.topk(sd, kk, dim=1, largest=False, sorted=True)
-    best_i = torch.gather(si, 1, pos)
-    best_i = best_i.masked_fill(torch.isinf(best_d), -1)
-    return best_i.to(torch.int32), best_d
+def _live_branches(state: SearchState) -> torch.Tensor:
+    """Flattened indices q*J + j (int32, on the state's device) of the branches
+    that still have an unexpanded candidate and budget left."""
+    done = state.exhausted.ne(0) | state.expansions.ge(state.B)
+    return torch.nonzero(done.logical_not().flatten()).flatten().to(torch.int32)
 
 
 def advance_chunked(X, G, Qv, state: SearchState, total: int, chunk: int, codes=None) -> int:
-    """Advance in chunks over the branches still running (swann/_engine.py:405-425).
-    Returns the number of launches."""
-    launches, spent = 0, 0
-    while spent < total:
-        alive = ((state.exhausted == 0) &
-                 (state.expansions < state.B)).reshape(-1).nonzero().squeeze(1)
-        if alive.numel() == 0:
+    """Spend up to `total` expansions per branch in launches of `chunk`, each
+    over only the branches still live, so a finished branch gives its slot on
+    the GPU to one that is not (swann/_engine.py:405-425).  Stops early once
+    no branch is live; returns the number of launches."""
+    if chunk < 1:
+        raise ValueError(f"chunk must be >= 1, got {chunk}")
+    launches = 0
+    for start in range(0, total, chunk):
+        live = _live_branches(state)
+        if live.numel() == 0:
             break
-        step = min(chunk, total - spent)
-        advance(X, G, Qv, state, step, active=alive.to(torch.int32).contiguous(), codes=codes)
-        spent += step
+        advance(X, G, Qv, state, min(chunk, total - start), active=live, codes=codes)
         launches += 1
     return launches
 

@@ -27,6 +27,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "lanes.h"
 
 namespace swann {
 namespace {
@@ -47,7 +48,6 @@ constexpr int kMaxChunks = SWANN_MAX_CHUNKS;   // 16-byte loads a lane keeps in 
 #ifndef SWANN_TABLE_SCOPE
 #define SWANN_TABLE_SCOPE __HIP_MEMORY_SCOPE_AGENT
 #endif
-constexpr int kMergeMax = 8192;        // merge_branches: V*kk limit (64 KB of LDS)
 constexpr size_t kMaxLds = 64 * 1024;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -137,8 +137,7 @@ __device__ __forceinline__ float team_dist(const float* __restrict__ sq,
             }
         }
     }
-#pragma unroll
-    for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
+    acc = team_fold_add<TEAM>(acc);      // DPP row shifts, no LDS round trip
     return METRIC == SWANN_METRIC_IP ? 1.f - acc : acc;
 }
 
@@ -225,8 +224,7 @@ __device__ __forceinline__ float team_code_ip(const float* __restrict__ sq,
         code_fetch<TEAM>(code, w0, cwords, wb);
         acc = code_chunk<TEAM>(sq, wb, w0, cwords, dim, acc);
     }
-#pragma unroll
-    for (int off = TEAM / 2; off > 0; off >>= 1) acc = acc + __shfl_down(acc, off, TEAM);
+    acc = team_fold_add<TEAM>(acc);
     return 1.f - (alpha * (2.f * acc - qsum) + qmu);
 }
 
@@ -553,11 +551,8 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             m = m + qt * a.cmu[t];
             s = s + qt;
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            m = m + __shfl_down(m, off, 64);
-            s = s + __shfl_down(s, off, 64);
-        }
+        m = team_fold_add<64>(m);
+        s = team_fold_add<64>(s);
         if (lane == 0) { s_qmu = m; s_qsum = s; }
     }
     if (a.codes) __syncthreads();
@@ -702,10 +697,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                 const int v = w_v[w];
                 unsigned head[kCodeWords];
                 code_fetch<TEAM>(a.codes + (int64_t)v * a.cwords, tl, a.cwords, head);
-                float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords, head,
-                                               a.calpha[v], s_qmu, s_qsum, a.dim, a.cwords, tl);
-                est = __shfl(est, 0, TEAM);
-                if (tl == 0) {
+                const float est = team_code_ip<TEAM>(sq, a.codes + (int64_t)v * a.cwords,
+                                                     head, a.calpha[v], s_qmu, s_qsum, a.dim,
+                                                     a.cwords, tl);
+                if (tl == 0) {                   // the team's total is in its lane 0
                     if (rad != FLT_MAX && est > rad + a.cmargin) {
                         const int nidx = w_nidx[w] & 0xffff;
                         atomicAdd(&s_ctr[3], 1);
@@ -824,52 +819,113 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// merge: local_search.cu:863-919
-constexpr int kMergeBlock = 256;
+// merge (semantics of local_search.cu:863-919): a query's n = V*kk branch
+// results in (distance, id) order with invalid ids after everything; an entry
+// whose id equals its predecessor's in that order is dropped; the first k
+// kept, padded with (-1, +inf).
+//
+// Each entry becomes one 64-bit key ordered as (distance, id) is: the high
+// word is the distance's bit pattern made monotone (+0 and -0 share a value,
+// as the float comparison has them equal), the low word 2*id plus 1 for a
+// distance of -0, so keys of different ids order by id and a zero's sign
+// rides along.  An invalid id is the key (+inf, INT32_MAX), where the walk
+// ends.  The walk through the sorted order is a chain of successor queries --
+// the least key >= lo, then lo = that key + 1 -- each one wave-wide minimum
+// over keys held in registers; nothing is sorted.  Equal keys are visited
+// once, which drops their later copies as the predecessor rule does.
+constexpr int kMergeWaveMax = 32;      // keys per lane in the one-wave kernel
+constexpr int kMergeBlockThreads = 1024;
 
-__global__ __launch_bounds__(kMergeBlock) void merge_kernel(const int32_t* __restrict__ bids,
-                                                           const float* __restrict__ bdist,
-                                                           int32_t* __restrict__ oi,
-                                                           float* __restrict__ od, int64_t Q,
-                                                           int n, int k, int padded) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    float* sd = reinterpret_cast<float*>(smem);
-    int* si = reinterpret_cast<int*>(sd + padded);
-    const int64_t q = xcd_remap(blockIdx.x, Q);
+__device__ __forceinline__ uint64_t merge_key(int32_t id, float d) {
+    if (id < 0) id = INT32_MAX, d = INFINITY;
+    uint32_t b = __float_as_uint(d);
+    const uint32_t neg0 = b == 0x80000000u;
+    if (neg0) b = 0;
+    const uint32_t m = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)m << 32) | ((uint32_t)id << 1) | neg0;
+}
+
+__device__ __forceinline__ float merge_key_dist(uint64_t key) {
+    if (key & 1) return -0.0f;
+    const uint32_t m = (uint32_t)(key >> 32);
+    return __uint_as_float((m & 0x80000000u) ? (m & 0x7FFFFFFFu) : ~m);
+}
+
+// One step of the walk, shared by both kernels: `m` is the least key >= lo
+// (all ones when none is left).  Returns false when the walk is over.
+__device__ __forceinline__ bool merge_visit(uint64_t m, int& prev_id, int& w, uint64_t& lo,
+                                            int32_t* __restrict__ oi, float* __restrict__ od,
+                                            int64_t row, bool writer) {
+    const int id = (int)((uint32_t)m >> 1);
+    if (id == INT32_MAX) return false;       // invalid entries (or nothing) remain
+    if (id != prev_id) {
+        if (writer) { oi[row + w] = id; od[row + w] = merge_key_dist(m); }
+        ++w;
+    }
+    prev_id = id;
+    lo = m + 1;
+    return true;
+}
+
+// n <= 64*R: one wave per query, R keys per lane in registers.
+template <int R>
+__global__ __launch_bounds__(64) void merge_wave_kernel(const int32_t* __restrict__ bids,
+                                                        const float* __restrict__ bdist,
+                                                        int32_t* __restrict__ oi,
+                                                        float* __restrict__ od, int64_t q0,
+                                                        int n, int k) {
+    const int64_t q = q0 + blockIdx.x;
+    const int lane = threadIdx.x;
     const int64_t base = q * (int64_t)n;
-    for (int i = threadIdx.x; i < padded; i += kMergeBlock) {
-        const bool real = i < n;
-        const int id = real ? bids[base + i] : -1;
-        sd[i] = (real && id >= 0) ? bdist[base + i] : INFINITY;
-        si[i] = id >= 0 ? id : INT32_MAX;
+    uint64_t key[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = lane + 64 * r;
+        key[r] = i < n ? merge_key(bids[base + i], bdist[base + i]) : ~0ull;
     }
-    __syncthreads();
-    for (int size = 2; size <= padded; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < padded; i += kMergeBlock) {
-                const int jx = i ^ stride;
-                if (jx > i) {
-                    const bool up = ((i & size) == 0);
-                    const bool l = lt(sd[i], si[i], sd[jx], si[jx]);
-                    if (up != l) {
-                        const float td = sd[i]; sd[i] = sd[jx]; sd[jx] = td;
-                        const int ti = si[i]; si[i] = si[jx]; si[jx] = ti;
-                    }
-                }
-            }
-            __syncthreads();
-        }
+    const int64_t row = q * (int64_t)k;
+    uint64_t lo = 0;
+    int prev_id = -1, w = 0;
+    for (int step = 0; step < n && w < k; ++step) {     // each step passes one key
+        uint64_t m = ~0ull;
+#pragma unroll
+        for (int r = 0; r < R; ++r) m = key[r] >= lo ? umin64(m, key[r]) : m;
+        m = wave_min_u64(m);
+        if (!merge_visit(m, prev_id, w, lo, oi, od, row, lane == 0)) break;
     }
-    if (threadIdx.x == 0) {
-        int w = 0;
-        for (int i = 0; i < n && w < k; ++i) {
-            if (si[i] == INT32_MAX) break;
-            if (i > 0 && si[i] == si[i - 1]) continue;
-            oi[q * k + w] = si[i];
-            od[q * k + w] = sd[i];
-            ++w;
+    for (int t = w + lane; t < k; t += 64) { oi[row + t] = -1; od[row + t] = INFINITY; }
+}
+
+// Any n: one 1024-thread workgroup per query; each step re-reads the keys
+// (the query's n entries stay in L1/L2 after the first pass), the waves'
+// minima meet in LDS, double-buffered so one barrier per step suffices.
+__global__ __launch_bounds__(kMergeBlockThreads) void merge_block_kernel(
+    const int32_t* __restrict__ bids, const float* __restrict__ bdist, int32_t* __restrict__ oi,
+    float* __restrict__ od, int64_t q0, int64_t n, int k) {
+    constexpr int kWaves = kMergeBlockThreads / 64;
+    __shared__ uint64_t part[2][kWaves];
+    const int64_t q = q0 + blockIdx.x;
+    const int64_t base = q * n;
+    const int64_t row = q * (int64_t)k;
+    uint64_t lo = 0;
+    int prev_id = -1, w = 0;
+    for (int64_t step = 0; step < n && w < k; ++step) {
+        uint64_t m = ~0ull;
+        for (int64_t i = threadIdx.x; i < n; i += kMergeBlockThreads) {
+            const uint64_t x = merge_key(bids[base + i], bdist[base + i]);
+            m = x >= lo ? umin64(m, x) : m;
         }
-        for (; w < k; ++w) { oi[q * k + w] = -1; od[q * k + w] = INFINITY; }
+        m = wave_min_u64(m);
+        if ((threadIdx.x & 63) == 0) part[step & 1][threadIdx.x >> 6] = m;
+        __syncthreads();
+        m = ~0ull;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) m = umin64(m, part[step & 1][v]);
+        if (!merge_visit(m, prev_id, w, lo, oi, od, row, threadIdx.x == 0)) break;
+    }
+    for (int t = w + (int)threadIdx.x; t < k; t += kMergeBlockThreads) {
+        oi[row + t] = -1;
+        od[row + t] = INFINITY;
     }
 }
 
@@ -1150,17 +1206,43 @@ int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int
     SWANN_REQUIRE(V >= 1 && kk >= 1, "expected (Q, V, kk) branch results with V, kk >= 1");
     const int64_t n = (int64_t)V * kk;
     SWANN_REQUIRE(k > 0 && k <= n, "k must be in 1..V*kk");
-    SWANN_REQUIRE(n <= kMergeMax, "merge of %lld candidates exceeds %d; lower V or the per-branch k",
-                  (long long)n, kMergeMax);
-    SWANN_REQUIRE(Q >= 0 && Q <= INT32_MAX, "Q out of range");
+    SWANN_REQUIRE(Q >= 0, "Q out of range");
     if (Q == 0) return SWANN_OK;
     SWANN_REQUIRE(bids && bdist && out_ids && out_dist, "merge: a required pointer is NULL");
-    int padded = 1;
-    while (padded < n) padded <<= 1;
-    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)Q), dim3(kMergeBlock),
-                       (size_t)padded * 8, (hipStream_t)stream, bids, bdist, out_ids, out_dist, Q,
-                       (int)n, k, padded);
-    return launch_status("merge_branches");
+    const hipStream_t st = (hipStream_t)stream;
+    // one workgroup per query, launched in slices of at most 2^20 queries
+    constexpr int64_t kSlice = 1 << 20;
+    for (int64_t q0 = 0; q0 < Q; q0 += kSlice) {
+        const unsigned nq = (unsigned)(Q - q0 < kSlice ? Q - q0 : kSlice);
+        if (n <= 64 * kMergeWaveMax) {
+            const int r = (int)((n + 63) / 64);
+            const int ni = (int)n;
+            if (r <= 1)
+                hipLaunchKernelGGL(merge_wave_kernel<1>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+            else if (r <= 2)
+                hipLaunchKernelGGL(merge_wave_kernel<2>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+            else if (r <= 4)
+                hipLaunchKernelGGL(merge_wave_kernel<4>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+            else if (r <= 8)
+                hipLaunchKernelGGL(merge_wave_kernel<8>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+            else if (r <= 16)
+                hipLaunchKernelGGL(merge_wave_kernel<16>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+            else
+                hipLaunchKernelGGL(merge_wave_kernel<32>, dim3(nq), dim3(64), 0, st, bids, bdist,
+                                   out_ids, out_dist, q0, ni, k);
+        } else {
+            hipLaunchKernelGGL(merge_block_kernel, dim3(nq), dim3(kMergeBlockThreads), 0, st, bids,
+                               bdist, out_ids, out_dist, q0, n, k);
+        }
+        const int rc = launch_status("merge_branches");
+        if (rc) return rc;
+    }
+    return SWANN_OK;
 }
 
 int swann_overflow_async(const int32_t* counters, int64_t nbranch, int32_t* out, void* stream) {

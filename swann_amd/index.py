@@ -82,7 +82,7 @@ class Index:
               alpha: float = 1.2, **kw) -> "Index":
         """Build a graph over `vectors` on the GPU (sweep, prune, reverse)."""
         from .build import build_graph
-        X = _as_cuda(vectors)
+        X = _on_gpu(vectors)
         G = build_graph(X, metric=metric, degree=degree, candidates=candidates, alpha=alpha)
         return cls(X, G, metric=metric, **kw)
 
@@ -96,7 +96,7 @@ class Index:
             if not hasattr(cfg, key):
                 raise TypeError(f"unknown search option {key!r}")
             setattr(cfg, key, value)
-        Q = _as_cuda(queries).float().contiguous()
+        Q = _on_gpu(queries).float().contiguous()
         return self._search_device(Q, k, cfg)
 
     def _search_device(self, Q: torch.Tensor, k: int, cfg: SearchConfig):
@@ -179,7 +179,7 @@ class Index:
         meta = json.loads((path / "index.json").read_text())
         G = torch.from_numpy(np.load(path / "graph.npy", allow_pickle=False)).cuda()
         cat = torch.from_numpy(np.load(path / "catalogue.npy", allow_pickle=False)).cuda()
-        return cls(_as_cuda(vectors), G, metric=meta["metric"], catalogue=cat)
+        return cls(_on_gpu(vectors), G, metric=meta["metric"], catalogue=cat)
 
     def __repr__(self) -> str:
         n, d = self.X.shape
@@ -187,12 +187,13 @@ class Index:
                 f"metric={self.metric!r}, dtype={self.X.dtype})")
 
 
-def _as_cuda(a) -> torch.Tensor:
-    if isinstance(a, np.ndarray):
-        a = torch.from_numpy(np.ascontiguousarray(a))
-    if a.device.type != "cuda":
-        a = a.cuda()
-    return a.contiguous()
+def _on_gpu(a) -> torch.Tensor:
+    """`a` -- a numpy array, a nested list or a tensor on any device -- as a
+    contiguous tensor on the GPU (the current device unless it is already on
+    one)."""
+    if isinstance(a, torch.Tensor):
+        return (a if a.is_cuda else a.to("cuda")).contiguous()
+    return torch.as_tensor(np.ascontiguousarray(a), device="cuda")
 
 
 class CapturedSearch:
@@ -233,7 +234,7 @@ class CapturedSearch:
         """Copy `queries` (batch x d) into the graph's input and replay it on
         the current stream.  Returns the graph's (ids, dist) device tensors,
         overwritten by the next run."""
-        q = _as_cuda(queries)
+        q = _on_gpu(queries)
         if q.shape != self.queries.shape:
             raise ValueError(f"captured for queries of shape {tuple(self.queries.shape)}, "
                              f"got {tuple(q.shape)}")

@@ -195,16 +195,51 @@ def test_visited_overflow_is_reported():
 
 
 def test_merge_dedup_matches_oracle():
+    """Every kernel shape (one wave with 1..32 keys a lane, n up to 2048; the
+    1024-thread walk above that), C4's 128 branches x 10, k up to n, against
+    the oracle's sort-and-scan restatement of local_search.cu:863-919, bit
+    for bit."""
     rng = np.random.default_rng(37)
-    for Q, V, kk, k in ((6, 5, 10, 10), (50, 32, 10, 10), (9, 128, 12, 10), (3, 7, 3, 5)):
+    for Q, V, kk, k in ((6, 5, 10, 10), (50, 32, 10, 10), (9, 128, 12, 10), (3, 7, 3, 5),
+                        (4, 1, 1, 1), (5, 2, 40, 80), (7, 64, 10, 10), (11, 128, 10, 10),
+                        (3, 128, 16, 10), (2, 256, 10, 100), (2, 1000, 10, 10000),
+                        (300, 64, 10, 10)):
         note("merge", Q, V, kk, k)
-        ids = rng.integers(-1, 60, (Q, V, kk)).astype(np.int32)
-        base = rng.random(60).astype(np.float32)
+        pool = max(8, V * kk // 3)
+        ids = rng.integers(-1, pool, (Q, V, kk)).astype(np.int32)
+        base = rng.random(pool).astype(np.float32)
         dist = np.where(ids >= 0, base[np.clip(ids, 0, None)], np.float32(3e38)).astype(np.float32)
         gi, gd = E.merge_branches(*to_gpu(ids, dist), k)
         wi, wd = O.merge(ids, dist, k)
-        assert np.array_equal(gi.cpu().numpy(), wi)
-        assert np.array_equal(gd.cpu().numpy(), wd)
+        assert np.array_equal(gi.cpu().numpy(), wi), (Q, V, kk, k)
+        assert gd.cpu().numpy().tobytes() == wd.tobytes(), (Q, V, kk, k)
+
+
+def test_merge_keeps_the_reference_quirks():
+    """Hand cases of the (distance, id) walk with the predecessor rule of
+    local_search.cu:903-910: an id seen again at a larger distance is dropped
+    only when nothing lies between the two copies; equal distances go by id;
+    a valid id at +inf comes before the invalid ones; -0 keeps its sign; too
+    few distinct ids pad with (-1, +inf)."""
+    inf = np.float32(np.inf)
+    cases = [
+        ([7, 3, 7], [0.5, 0.55, 0.6], 3),          # 7 3 7: not adjacent, both kept
+        ([7, 7, 3], [0.5, 0.6, 0.7], 3),           # 7 3: the copies are adjacent
+        ([9, 4, 4, 2], [0.25, 0.25, 0.25, 0.25], 4),   # ties by id: 2 4 9
+        ([5, -1, 6, -1], [inf, 0.1, 0.2, 0.3], 4),     # 6, then 5 at +inf, then padding
+        ([1, 2, 3], [-0.0, 0.0, -1.0], 3),         # -1, then -0 (id 1) before +0 (id 2)
+        ([-1, -1, -1], [0.1, 0.2, 0.3], 2),        # nothing valid
+    ]
+    for ids_l, d_l, k in cases:
+        ids = np.array(ids_l, np.int32).reshape(1, 1, -1)
+        dist = np.array(d_l, np.float32).reshape(1, 1, -1)
+        gi, gd = E.merge_branches(*to_gpu(ids, dist), k)
+        wi, wd = O.merge(ids, dist, k)
+        assert np.array_equal(gi.cpu().numpy(), wi), ids_l
+        assert gd.cpu().numpy().tobytes() == wd.tobytes(), ids_l
+    gi, _ = E.merge_branches(*to_gpu(np.array([[[7, 3, 7]]], np.int32),
+                                     np.array([[[0.5, 0.55, 0.6]]], np.float32)), 3)
+    assert gi.cpu().numpy().tolist() == [[7, 3, 7]]
 
 
 def test_shared_cache_is_free_of_consequence(block):

@@ -112,22 +112,12 @@ def test_search_config_defaults():
     assert (c.branches, c.queue, c.budget, c.stop_eps, c.team, c.k) == (32, 12, 64, 0.05, 16, 10)
 
 
-def test_tensor_merge_matches_oracle():
-    rng = np.random.default_rng(3)
-    Q, V, kk, k = 30, 6, 10, 10
-    ids = rng.integers(-1, 50, (Q, V, kk)).astype(np.int32)
-    base = rng.random(50).astype(np.float32)
-    dist = np.where(ids >= 0, base[np.clip(ids, 0, None)], np.float32(3e38)).astype(np.float32)
-    oi, od = E._merge_branches_tensor(torch.from_numpy(ids), torch.from_numpy(dist), k)
-    wi, wd = O.merge(ids, dist, k)
-    assert np.array_equal(oi.numpy(), wi)
-    assert np.array_equal(od.numpy(), wd)
-
-
 def test_product_refuses_cpu_tensors():
     X = torch.zeros((10, 8))
     with pytest.raises(RuntimeError):
         E.init_states(X, X[:2].clone(), torch.zeros((2, 1), dtype=torch.int32), D=4)
+    with pytest.raises(RuntimeError):
+        E.merge_branches(torch.zeros((2, 3, 4), dtype=torch.int32), torch.zeros((2, 3, 4)), 4)
 
 
 def test_no_oracle_in_the_product():
@@ -157,3 +147,19 @@ def test_interleaved_table_must_be_8_byte_aligned():
         assert fn(base + 4, base + 8) != 0 and "8-byte aligned" in _err()
         assert fn(base, base + 4) == 0                       # aligned pairs
         assert fn(base + 4, base + 0x8000) == 0              # separate arrays
+
+
+def test_swann_is_the_drop_in_name():
+    """`import swann` gives the reference's public names and module paths
+    (swann/__init__.py:13-16), bound to this implementation's objects."""
+    import swann
+    import swann_amd
+    assert swann.Index is swann_amd.Index and swann.SearchConfig is swann_amd.SearchConfig
+    assert swann.overflow_guard is swann_amd.overflow_guard
+    assert sorted(swann.__all__) == ["Index", "SearchConfig", "overflow_guard"]
+    import swann._engine as E2
+    from swann.build import build_graph, knn_candidates  # noqa: F401
+    from swann._select import select_nearest  # noqa: F401
+    from swann.index import Index
+    assert E2 is E and Index is swann_amd.Index
+    assert E2.cache_size(32, 64, 64) == 131072

@@ -266,6 +266,83 @@ def test_claims_keep_branches_disjoint():
         assert r["cache_d"][slot] == O.team_distance(q, X, v, O.METRIC_IP, 32)
 
 
+@pytest.mark.parametrize("schedule", ["serial", "rounds"])
+@pytest.mark.parametrize("kstop", [1, 5, 10, 40])
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_bound_is_the_least_kth_distance_any_branch_reached(kstop, exclusive, schedule):
+    """The shared bound is lowered after every expansion to the branch's
+    kr-th distance, kr = min(kstop, L) (local_search.cu:655-658).  A queue
+    position only ever improves, so the final bound must equal, bit for bit,
+    the least final kr-th distance over the branches that expanded at least
+    once with that position filled -- and stay FLT_MAX when none did.  A bound
+    never lowered, lowered from the wrong position (L-th instead of kr-th) or
+    from a branch's seeds fails this.  L2 keeps every distance >= 0, where the
+    integer atomicMin on the bits is the float minimum."""
+    X = gaussian(2000, 64, 91, False)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 16, metric=1)
+    Q = gaussian(8, 64, 92, False)
+    rng = np.random.default_rng(93)
+    L = 12
+    kr = min(kstop, L)
+    for qi in range(8):
+        seeds = rng.integers(0, 2000, 12).astype(np.int32)
+        Hc = O.cache_size(12, 10, 16) if exclusive else 0
+        r = O.search_query(X, G, Q[qi], seeds, L=L, B=10, metric=O.METRIC_L2, H=None if not
+                           exclusive else 1, Hc=Hc, bound=True, exclusive=exclusive,
+                           stop_eps=0.1, kstop=kstop, schedule=schedule)
+        live = (r["counters"][:, 0] >= 1) & (r["ids"][:, kr - 1] >= 0)
+        want = r["dist"][live, kr - 1].min() if live.any() else F32MAX
+        assert np.float32(r["bound"]).tobytes() == np.float32(want).tobytes(), (qi, kstop)
+        assert live.any()
+
+
+def _bound_case():
+    """L2 on a line (dim 4, fp32).  Node 0 sits at distance 1 from the query
+    and its only neighbour, node 1, at 0.25.  Nodes 5, 6, 7, 8 form a chain
+    walking in from distance 100 (10, 9, 8, 7 along the axis); node 8 is a
+    dead end.  With kstop = 1 and stop_eps = 0 a branch expands only while its
+    best entry is unexpanded and within its radius."""
+    X = np.zeros((10, 4), np.float32)
+    X[0, 0], X[1, 0] = 1.0, 0.5
+    for i, x in zip((5, 6, 7, 8), (10.0, 9.0, 8.0, 7.0)):
+        X[i, 0] = x
+    G = np.full((10, 2), -1, np.int32)
+    G[0, 0], G[1, 0] = 1, 0
+    G[5, 0], G[6, 0], G[7, 0] = 6, 7, 8
+    return X, G, np.zeros(4, np.float32)
+
+
+@pytest.mark.parametrize("schedule", ["serial", "rounds"])
+@pytest.mark.parametrize("near_first", [True, False])
+def test_bound_stops_a_branch_its_own_radius_would_not(near_first, schedule):
+    """Two branches of one query, the near one seeded at node 0, the far one
+    at node 5.  Alone, the far branch walks the whole chain (4 expansions).
+    With the shared bound, the near branch's first expansion lowers the bound
+    to 0.25; the far branch's next pick (distance >= 49) then exceeds
+    min(own radius, bound) and it stops, exhausted.  The serial schedule
+    steps branch 0 then branch 1 and each step reads the bound as the one
+    before it left it: stepped after the near branch the far one expands
+    nothing; stepped before it, exactly one node.  In rounds, both branches'
+    first steps read the bound the round began with (FLT_MAX), so the far
+    branch expands exactly one node in either order.  A bound that is read
+    but ignored, or never lowered, gives 4."""
+    X, G, q = _bound_case()
+    seeds = np.array([0, 5] if near_first else [5, 0], np.int32)
+    far = 1 if near_first else 0
+    kw = dict(L=4, B=8, metric=O.METRIC_L2, team=4, stop_eps=0.0, kstop=1, schedule=schedule)
+    alone = O.search_query(X, G, q, seeds, bound=False, **kw)
+    assert alone["counters"][far, 0] == 4
+    r = O.search_query(X, G, q, seeds, bound=True, **kw)
+    want = (0 if near_first else 1) if schedule == "serial" else 1
+    assert r["counters"][far, 0] == want
+    assert r["counters"][far, 3] == 1
+    assert r["counters"][1 - far, 0] == 2          # node 0, then node 1
+    assert r["bound"] == np.float32(0.25)
+    # the near branch is untouched by the bound: it owns the bound's value
+    assert np.array_equal(r["ids"][1 - far], alone["ids"][1 - far])
+
+
 # -- merge ----------------------------------------------------------------------
 def test_merge_is_a_dedup_selection():
     rng = np.random.default_rng(37)
