@@ -186,6 +186,22 @@ int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, i
                          int E, int metric, int32_t* out_idx, float* out_dist,
                          void* workspace, void* stream);
 
+/* swann_select_nearest without a workspace argument and without allocating:
+ * no counterpart in the reference.  It is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Its workspace is the library's own
+ * fixed array of SWANN_SELECT_SCRATCH_BYTES per GPU (held from the first call
+ * on a GPU until the process ends); a call whose
+ * swann_select_workspace_size(nq, P) exceeds that is refused with
+ * SWANN_E_INVALID (32 MiB: e.g. 2,000 queries against a 4,096-row
+ * catalogue).  Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (concurrent streams or threads) race; calls ordered on
+ * one stream do not.  Results equal swann_select_nearest's. */
+#define SWANN_SELECT_SCRATCH_BYTES ((int64_t)32 << 20)
+int swann_select_nearest_noalloc(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P,
+                                 int E, int metric, int32_t* out_idx, float* out_dist,
+                                 void* stream);
+
 /* ---- graph build -------------------------------------------------------
  * X [n, dim] is fp32 or fp16 (x_dtype); an fp16 corpus is read as fp16 and
  * upcast exactly, which equals the reference's X.float() (build.py:167).

@@ -36,6 +36,7 @@ PROTOTYPES = {
     "swann_overflow_async": (I, [P, I64, P, P]),
     "swann_select_workspace_size": (I64, [I64, I64]),
     "swann_select_nearest": (I, [P, I64, I, P, I64, I, I, P, P, P, P]),
+    "swann_select_nearest_noalloc": (I, [P, I64, I, P, I64, I, I, P, P, P]),
     "swann_sweep_workspace_size": (I64, [I64, I, I, I]),
     "swann_build_sweep": (I, [P, I, I64, I, I, I, P, P, P, P]),
     "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P]),

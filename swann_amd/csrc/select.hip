@@ -18,6 +18,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 
 namespace swann {
@@ -312,23 +315,53 @@ __global__ __launch_bounds__(kTopBlock) void row_topk(const float* __restrict__ 
 
 using namespace swann;
 
-extern "C" {
+// ---- the fixed workspace of swann_select_nearest_noalloc -------------------
+// One array per GPU in the library's own device memory, reserved when the
+// code object loads on that device and held until the process ends, so the
+// no-alloc entry point never calls an allocator.  In host code `scratch` only
+// names the symbol; its address on a device comes from hipGetSymbolAddress,
+// looked up once per device (with that device current) and cached.
+constexpr int64_t kScratchBytes = SWANN_SELECT_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-int64_t swann_select_workspace_size(int64_t nq, int64_t P) {
-    // distance matrix + both norm vectors + (small batches) the split-K
-    // partials, each 256-byte aligned
-    const int64_t a = ((nq * P * 4 + 255) / 256) * 256;
-    const int64_t b = ((nq * 4 + 255) / 256) * 256;
-    const int64_t c = ((P * 4 + 255) / 256) * 256;
-    const int S = split_for(((P + kTN - 1) / kTN) * ((nq + kTM - 1) / kTM));
-    const int64_t d = S > 1 ? (int64_t)S * a : 0;
-    return a + b + c + d;
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("select (no-alloc): hipGetDevice failed: %s", hipGetErrorString(e));
+        return SWANN_E_NODEVICE;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("select (no-alloc): device %d out of range", dev);
+        return SWANN_E_UNSUPPORTED;
+    }
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) {
+                set_error("select (no-alloc): hipGetSymbolAddress(scratch) failed on device %d: %s",
+                          dev, hipGetErrorString(e));
+                return SWANN_E_LAUNCH;
+            }
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return SWANN_OK;
 }
+}  // namespace
 
-int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int E,
-                         int metric, int32_t* out_idx, float* out_dist, void* workspace,
-                         void* stream) {
-    clear_error();
+static int select_run(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int E,
+                      int metric, int32_t* out_idx, float* out_dist, void* workspace,
+                      void* stream) {
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
     SWANN_REQUIRE(nq >= 0 && P >= 1 && dim >= 1, "select: need nq >= 0, P >= 1, dim >= 1");
@@ -378,6 +411,46 @@ int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, i
         hipLaunchKernelGGL(row_topk, dim3((unsigned)nq), dim3(kTopBlock), 0, st, Dm, nq, P, E,
                            out_idx, out_dist);
     return launch_status("select top-E");
+}
+
+
+extern "C" {
+
+int64_t swann_select_workspace_size(int64_t nq, int64_t P) {
+    // distance matrix + both norm vectors + (small batches) the split-K
+    // partials, each 256-byte aligned
+    const int64_t a = ((nq * P * 4 + 255) / 256) * 256;
+    const int64_t b = ((nq * 4 + 255) / 256) * 256;
+    const int64_t c = ((P * 4 + 255) / 256) * 256;
+    const int S = split_for(((P + kTN - 1) / kTN) * ((nq + kTM - 1) / kTM));
+    const int64_t d = S > 1 ? (int64_t)S * a : 0;
+    return a + b + c + d;
+}
+
+int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int E,
+                         int metric, int32_t* out_idx, float* out_dist, void* workspace,
+                         void* stream) {
+    clear_error();
+    return select_run(Q, nq, dim, Vp, P, E, metric, out_idx, out_dist, workspace, stream);
+}
+
+int swann_select_nearest_noalloc(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P,
+                                 int E, int metric, int32_t* out_idx, float* out_dist,
+                                 void* stream) {
+    clear_error();
+    SWANN_REQUIRE(nq >= 0 && P >= 1, "select: need nq >= 0, P >= 1");
+    const int64_t need = swann_select_workspace_size(nq, P);
+    SWANN_REQUIRE(need <= kScratchBytes,
+                  "select (no-alloc): %lld queries x %lld catalogue rows need %lld bytes of "
+                  "workspace; the built-in scratch holds %lld (use swann_select_nearest with a "
+                  "workspace of swann_select_workspace_size bytes)",
+                  (long long)nq, (long long)P, (long long)need, (long long)kScratchBytes);
+    if (nq == 0) return select_run(Q, nq, dim, Vp, P, E, metric, out_idx, out_dist, nullptr,
+                                   stream);
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+    return select_run(Q, nq, dim, Vp, P, E, metric, out_idx, out_dist, ws, stream);
 }
 
 }  // extern "C"
