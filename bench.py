@@ -234,9 +234,13 @@ class Searcher:
                     advance=e[2].elapsed_time(e[3]), merge=e[3].elapsed_time(e[4]))
 
 
-def cpu_baseline(X, G, Q, seeds, cfg, eps, k, nsample, metric_id, elem_bytes):
+def cpu_baseline(X, G, Q, seeds, cfg, eps, k, nsample, metric_id, truth, gpu_ids):
     """The oracle's C restatement (a port of the reference algorithm) on this
-    host's cores, on a bounded sample of the same workload."""
+    host's cores, on a bounded sample of the same workload: the production
+    mode (shared table at the reference's size, bound, claims, no visited
+    table) in the rounds schedule, where every branch of a query starts
+    together as on the GPU.  Its answers are scored against the same ground
+    truth, beside the GPU's recall on the same queries from the timed run."""
     import oracle as O
     from swann_amd import _engine as E
     cores = len(os.sched_getaffinity(0))
@@ -247,14 +251,18 @@ def cpu_baseline(X, G, Q, seeds, cfg, eps, k, nsample, metric_id, elem_bytes):
     Hc = E.cache_size(cfg["branches"], cfg["budget"], G.shape[1])
     O.lib()
     t0 = time.perf_counter()
-    O.search_batch(Xh, Gh, Qh, Sh, k=k, L=cfg["queue"], B=cfg["budget"], metric=metric_id,
-                   team=cfg["team"], stop_eps=eps, H=1, Hc=Hc, bound=True, exclusive=True,
-                   nthreads=cores)
+    oi, _ = O.search_batch(Xh, Gh, Qh, Sh, k=k, L=cfg["queue"], B=cfg["budget"],
+                           metric=metric_id, team=cfg["team"], stop_eps=eps, H=1, Hc=Hc,
+                           bound=True, exclusive=True, nthreads=cores, schedule="rounds")
     dt = time.perf_counter() - t0
+    dev = truth.device
+    r_cpu = recall(torch.from_numpy(oi).to(dev), truth[:nsample], k)
+    r_gpu = recall(gpu_ids[:nsample], truth[:nsample], k)
     return dict(value=round(nsample / dt, 2), unit="queries/s", cores=cores, kind="port",
                 sample=f"{nsample} queries of the timed workload at the same knobs "
-                       f"(oracle/swann_oracle.c, OpenMP over queries, serial branch schedule)",
-                seconds=round(dt, 2))
+                       f"(oracle/swann_oracle.c, OpenMP over queries, rounds schedule)",
+                seconds=round(dt, 2), recall_at_10=round(r_cpu, 4),
+                gpu_recall_at_10_same_queries=round(r_gpu, 4))
 
 
 SWEEP_GRID = dict(branches=(16, 32, 64, 128), queue=(12, 24, 48), budget=(64, 128),
@@ -458,6 +466,8 @@ def main():
     ap.add_argument("--no-codes", action="store_true",
                     help="skip the sign-code pre-filter line reported beside the headline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c5-build", action="store_true",
+                    help="skip the C5 graph build reported beside the C3 headline")
     ap.add_argument("--sweep", action="store_true",
                     help="print the recall-QPS grid and its frontier instead of the headline")
     ap.add_argument("--sweep-codes", action="store_true",
@@ -609,7 +619,7 @@ def main():
                                                metric=index._m)
         seeds = index.catalogue[ent].to(torch.int32)
         try:
-            cpu = cpu_baseline(X, G, Q, seeds, cfg, eps, k, a.cpu_sample, index._m, elem)
+            cpu = cpu_baseline(X, G, Q, seeds, cfg, eps, k, a.cpu_sample, index._m, truth, ids)
             log(f"cpu baseline {cpu}")
         except Exception as e:                                   # noqa: BLE001
             log(f"cpu baseline failed: {e}")
@@ -640,13 +650,30 @@ def main():
         log(f"with codes {with_codes}")
         del cs, cd, al, mu
 
+    # the build target's own shape, C5 (1M x 1024 fp32 l2 mixture), built beside
+    # the headline: the candidate sweep's MFMA fraction is quoted on it
+    build_c5 = None
+    if a.config == "c3" and not a.no_c5_build:
+        c5 = dict(CONFIGS["c5"])
+        n5 = a.n or c5["n"]
+        X5, _ = generate(c5, n5, 1, dev)
+        torch.cuda.synchronize()
+        _, b5_s, st5 = timed_build(X5, c5)
+        build_c5 = {"workload": f"C5: n={n5:,} x d={c5['d']} fp32 l2 (gmm), D={c5['D']}, "
+                                f"C={c5['cand']}, alpha=1.2",
+                    "build_s": round(b5_s, 2), "build_s_per_1M_rows": round(b5_s * 1e6 / n5, 2),
+                    "build_stages_s": st5, "build_roofline": build_roofline(n5, c5["d"], st5)}
+        log(f"c5 build {build_c5}")
+        del X5
+        torch.cuda.empty_cache()
+
     out = {
         "metric": "QPS at recall@10=0.95 (1 GPU) + achieved HBM GB/s fraction; build s/1M rows",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (generated on the GPU from fixed seeds; random-init graph built "
-                "by this library)",
+        "data": "synthetic (generated on the GPU from fixed seeds; graph built by this "
+                "library's exact sweep, prune and reverse)",
         "config": {"workload": f"{a.config.upper()}: n={n:,} x d={cfg['d']} {cfg['dtype']} "
                                f"{cfg['metric']} ({cfg['gen']}), {nq:,} fp32 queries, D={cfg['D']}, "
                                f"k={k}, team={cfg['team']}",
@@ -667,6 +694,7 @@ def main():
                      "bytes_per_launch": adv_bytes, "launch_ms": round(adv_s * 1e3, 3)},
         "cpu_baseline": cpu,
         "with_codes": with_codes,
+        "build_c5": build_c5,
     }
     print(json.dumps(out), flush=True)
 

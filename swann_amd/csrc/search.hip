@@ -1039,13 +1039,13 @@ int advance_occupancy(int block, size_t lds) {
 }
 
 // Whether the advance puts a query's branches on one XCD (xcd_remap), where
-// they share an L2: only when all J of them fit among the workgroups one XCD
-// holds at once.  Otherwise they would run in successive rounds, and the
-// late ones find the early ones' nodes claimed and their bound set (at 128
-// branches a query, 256 or 1024 threads a branch, recall@10 fell from 0.79 to
-// 0.72 and 0.53), so the blocks keep their dispatch order instead, which
-// spreads a query's branches over the XCDs; the visited table's atomics are
-// agent scope and stay coherent across XCDs.
+// they share an L2: only when they are a small share of the workgroups one
+// XCD holds at once (below).  Otherwise they would start in successive
+// rounds, and the late ones find the early ones' nodes claimed and their
+// bound set (at 128 branches a query, 256 or 1024 threads a branch, recall@10
+// fell from 0.79 to 0.72 and 0.53), so the blocks keep their dispatch order
+// instead, which spreads a query's branches over the XCDs; the table's and
+// bound's atomics are agent scope and stay coherent across XCDs.
 bool remap_branches(int J, int team, int x_dtype, int block, size_t lds) {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1068,7 +1068,16 @@ bool remap_branches(int J, int team, int x_dtype, int block, size_t lds) {
                               : advance_occupancy<64, _Float16>(block, lds); break;
     }
     if (per_cu <= 0) (void)hipGetLastError();
-    return (int64_t)J <= (int64_t)(cus / kNumXcd) * per_cu;
+    // Grouped only while a query's branches take at most a quarter of the
+    // XCD's resident slots.  In steady state a new query's branches enter one
+    // freed slot at a time; when J is a large share of the XCD, the late ones
+    // start after the early ones have set the bound and claimed the nodes,
+    // and the search turns toward a serial schedule: C4 at 128 branches (J =
+    // 0.44 of an XCD's one-wave slots) fell to recall 0.773 grouped against
+    // 0.802 for branches that start together, while J = 0.11-0.17 of the
+    // slots (C2, C3, C4 at 32 branches) matched it within 0.002.  Spread over
+    // the eight XCDs, a query's branches are dispatched about together.
+    return 4 * (int64_t)J <= (int64_t)(cus / kNumXcd) * per_cu;
 }
 
 }  // namespace

@@ -426,12 +426,13 @@ def test_large_batch_one_wave_layout_matches_oracle():
 
 def test_claims_and_bound_multi_branch_statistics():
     """Claims, bound and the elided visited table are racy by design: judge
-    them by recall against the oracle's serial schedule, by distances that
-    equal exact recomputation, and by no duplicate ids in the answer."""
+    them by recall within 0.005 of the oracle's rounds schedule (every branch
+    of a query starts together, as on the GPU), by distances that equal exact
+    recomputation, and by no duplicate ids in the answer."""
     g = golden("refcpu_c1.npz")
     X = regen(10000, 128, 0, True, g["X_sha"])
     G = g["G"].astype(np.int32)
-    Q = gaussian(1000, 128, 501, True)
+    Q = gaussian(2000, 128, 501, True)
     cat = g["catalogue"].astype(np.int64)
     idx, _ = O.select_nearest(Q, X[cat], 16, 0, nthreads=8)
     seeds = cat[idx].astype(np.int32)
@@ -442,11 +443,12 @@ def test_claims_and_bound_multi_branch_statistics():
     ids = ids.cpu().numpy(); dist = dist.cpu().numpy()
     Hc = E.cache_size(16, 64, 32)
     oi, od = O.search_batch(X, G, Q, seeds, k=10, L=12, B=64, metric=0, team=16, stop_eps=0.05,
-                            H=1, Hc=Hc, bound=True, exclusive=True, nthreads=8)
+                            H=1, Hc=Hc, bound=True, exclusive=True, nthreads=8,
+                            schedule="rounds")
     truth = exact_topk(X, Q, 10)
     r_gpu, r_cpu = recall(ids, truth, 10), recall(oi, truth, 10)
-    note("claims recall gpu", r_gpu, "oracle serial", r_cpu)
-    assert abs(r_gpu - r_cpu) < 0.01
+    note("claims recall gpu", r_gpu, "oracle rounds", r_cpu)
+    assert abs(r_gpu - r_cpu) <= 0.005
     for q in range(Q.shape[0]):
         got = ids[q][ids[q] >= 0]
         assert len(set(got.tolist())) == len(got)
