@@ -4,7 +4,7 @@ graph build, MI355X-native (gfx950 HIP kernels behind a C ABI).
 A query is split into `branches` trajectories that advance at the same time
 and share a per-query distance table, a bound on the answer, and node claims.
 
-    import swann_amd as swann
+    import swann                  # or: import swann_amd as swann
     index = swann.Index.build(X, metric="ip")
     ids, dist = index.search(Q, k=10)
 """

@@ -102,6 +102,15 @@ struct MfmaSweepArgs {
     float* bkey; int32_t* bid; int32_t* bcnt;
     int scaled;                  // rows carry a power-of-two scale (fp32 corpus)
     int splits;                  // column splits G: row r's buffer s is (r * G + s) * cap
+    // symmetric (banded) sweep: tiles (I, I + b) for b in [b0, b1), each
+    // scored once for both of its panels' rows; splits = 2 lists a row, list 0
+    // the row's own (row panel) candidates, list 1 those another workgroup
+    // found for it (column panel), with bcnt[2r + 1] a global slot counter
+    int sym;
+    int64_t b0, b1;
+    const float* gthr;           // [n] a row's threshold when the launch began
+    int* ovf;                    // foreign appends that found no room
+    int fcap;                    // room in list 1 (<= cap; smaller only as a test hook)
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -110,8 +119,9 @@ struct MfmaSweepArgs {
 // masked; cnt >= 1 here), so a row costs one memory round trip; the search counts with
 // ballots and scalar popcounts, no cross-lane shuffles; the kept entries are
 // written back from registers (funkey inverts fkey bit for bit).
-__device__ __forceinline__ void compact_row_w(float* key, int32_t* id, int cnt, int C,
-                                              float* thr_out, int* cnt_out) {
+struct Compacted { uint32_t T; int kept; };     // wave-uniform: the C-th key, entries kept
+
+__device__ __forceinline__ Compacted compact_row_core(float* key, int32_t* id, int cnt, int C) {
     const int lane = threadIdx.x & 63;
     constexpr int R = 16;                      // cap <= 1024
     cnt = __builtin_amdgcn_readfirstlane(cnt);
@@ -181,7 +191,13 @@ __device__ __forceinline__ void compact_row_w(float* key, int32_t* id, int cnt, 
         const int used = __popcll(meq);
         eq_left -= used < eq_left ? used : eq_left;
     }
-    if (lane == 0) { *thr_out = funkey(T); *cnt_out = w; }
+    return Compacted{T, w};
+}
+
+__device__ __forceinline__ void compact_row_w(float* key, int32_t* id, int cnt, int C,
+                                              float* thr_out, int* cnt_out) {
+    const Compacted r = compact_row_core(key, id, cnt, C);
+    if ((threadIdx.x & 63) == 0) { *thr_out = funkey(r.T); *cnt_out = r.kept; }
 }
 
 
@@ -275,6 +291,66 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
             const int64_t o = ((r0 + rl) * a.splits + split) * (int64_t)a.cap + p;
             a.bkey[o] = d;
             a.bid[o] = (int32_t)c;
+        }
+    }
+}
+
+// The foreign half of a tile's epilogue in the symmetric sweep: the same 32 x
+// 32 block scored for the column panel's rows.  Lane holds column c -- a row
+// of the column panel, whose threshold `thc` came from the last merge -- and
+// its 16 candidates rbase + (e/4)*8 + (e%4) of the row panel.  Row c's
+// distance to candidate r is the reference formula with the roles swapped
+// (na = |c|^2, nb = |r|^2), from the same score.  A screen in score space
+// (as screen_thr) rejects most blocks with one compare per score; survivors
+// take a slot of row c's second list from its global counter.  Candidates
+// past n are copies of row n - 1 (the panel loads clamp) and are skipped.
+template <int METRIC>
+__device__ __forceinline__ void epilogue_foreign(const f32x16& v, int rbase, int64_t r0,
+                                                 int64_t c, bool cok, float cn, float sc,
+                                                 float thc, const float* rs, const float* rnorm,
+                                                 const MfmaSweepArgs& a, int scaled) {
+    const float h = screen_thr<METRIC>(thc, cn);
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                 : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 r4 = METRIC == SWANN_METRIC_L2
+                              ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+            any = any || (METRIC == SWANN_METRIC_IP
+                              ? dot > h
+                              : dot > h + 0.5f * (r4[q] - 1e-5f * fabsf(r4[q])));
+        }
+    }
+    any = any && cok;
+    if (__ballot(any) == 0ull) return;
+    asm volatile("" ::: "memory");
+    if (!any) return;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                 : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 r4 = METRIC == SWANN_METRIC_L2
+                              ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+            const float d = dist_formula<METRIC>(dot, cn, r4[q]);
+            const int64_t r = r0 + rbase + g * 8 + q;
+            if (!(d < thc) || r >= a.n) continue;
+            const int p = atomicAdd(&a.bcnt[c * 2 + 1], 1);
+            if (p < a.fcap) {
+                const int64_t o = (c * 2 + 1) * (int64_t)a.cap + p;
+                a.bkey[o] = d;
+                a.bid[o] = (int32_t)r;
+            } else {
+                atomicAdd(a.ovf, 1);
+            }
         }
     }
 }
@@ -527,6 +603,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     __shared__ __align__(16) float rnorm[kBM2];
     __shared__ __align__(16) float rscale[kBM2];
     __shared__ int need[2];      // set by the appends of column tiles of that parity
+    // symmetric sweep: the current column tile's rows' thresholds (from the
+    // last merge, fixed for the launch), for the foreign half of its epilogue
+    __shared__ __align__(16) float thrc[kBN2];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -538,13 +617,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     // xcd_remap gives consecutive logical ids to one XCD, so the G readers of
     // a panel run together on one L2
     const int G = a.splits;
-    const int64_t lid = xcd_remap(blockIdx.x, ntile * G);
-    const int64_t r0 = (lid / G) * kBM2;
-    const int split = (int)(lid % G);
+    // symmetric sweep: one workgroup per row panel, which keeps list 0 of
+    // its rows and starts from the thresholds and lists the last merge left
+    const int64_t lid = xcd_remap(blockIdx.x, a.sym ? (int64_t)gridDim.x : ntile * G);
+    const int64_t r0 = (a.sym ? lid : lid / G) * kBM2;
+    const int split = a.sym ? 0 : (int)(lid % G);
 
     if (tid < kBM2) {
-        thr[tid] = r0 + tid < n ? INFINITY : -INFINITY;
-        cnt[tid] = 0;
+        thr[tid] = r0 + tid >= n ? -INFINITY : a.sym ? a.gthr[r0 + tid] : INFINITY;
+        cnt[tid] = (a.sym && r0 + tid < n) ? a.bcnt[(r0 + tid) * 2] : 0;
         rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
         if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
         if (METRIC == SWANN_METRIC_L2) sthr[tid] = screen_thr<METRIC>(thr[tid], rnorm[tid]);
@@ -567,7 +648,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     }
     const int nk = dim / kBK3;
     const int64_t nct = (n + kBN2 - 1) / kBN2;
-    const int64_t ct0 = nct * split / G, ct1 = nct * (split + 1) / G;
+    int64_t ct0 = nct * split / G, ct1 = nct * (split + 1) / G;
+    if (a.sym) {
+        ct0 = lid + a.b0;
+        ct1 = lid + a.b1 < nct ? lid + a.b1 : nct;
+    }
     const int64_t nsteps = (ct1 - ct0) * nk;
     const _Float16* X = a.hi;
 
@@ -667,6 +752,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             for (int i = 0; i < BI; ++i)
 #pragma unroll
                 for (int j = 0; j < BJ; ++j) acc[i][j] = (f32x16){};
+            // the new tile's column thresholds; every wave finished the last
+            // tile's epilogue before this stage's barrier, and the next barrier
+            // (or the one below, for a one-stage tile) publishes them
+            if (a.sym && cbt != r0) {
+                if (tid < kBN2) thrc[tid] = cbt + tid < n ? a.gthr[cbt + tid] : INFINITY;
+                if (nk == 1) __syncthreads();
+            }
         }
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
@@ -712,6 +804,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                                            thr, rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
                                            &need[tpar],
                                            METRIC == SWANN_METRIC_L2 ? sthr : nullptr);
+                    if (a.sym && !diag)
+                        epilogue_foreign<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j],
+                                                 thrc[wn * CW + j * 32 + (lane & 31)], rscale,
+                                                 rnorm, a, SCALED);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -720,7 +816,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (G > 1) {
+    if (G > 1 && !a.sym) {
         // each split leaves at most C per row, so the merge of the G lists
         // sorts at most G * C
         for (int rl = wave; rl < kBM2; rl += WAVES) {
@@ -734,7 +830,84 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     if (tid < kBM2 && r0 + tid < n) a.bcnt[(r0 + tid) * G + split] = cnt[tid];
 }
 
+// ---------------------------------------------------------------------------
+// Between two launches of the symmetric sweep: each row's two lists become its
+// C best so far (list 0), list 1 is emptied, and the row's threshold -- the
+// C-th best distance, +inf while it has fewer -- is published for the next
+// launch's screens in both directions.  One wave a row; the compactions are
+// exact (compact_row_core) and each one's stores are fenced before the next
+// step reads them back.
+__global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
+                                                 int32_t* __restrict__ bid,
+                                                 int32_t* __restrict__ bcnt,
+                                                 float* __restrict__ gthr, int* ovf, int64_t n,
+                                                 int cap, int fcap, int C) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= n) return;
+    const int lane = threadIdx.x & 63;
+    float* k0 = bkey + r * 2 * (int64_t)cap;
+    int32_t* i0 = bid + r * 2 * (int64_t)cap;
+    float* k1 = k0 + cap;
+    int32_t* i1 = i0 + cap;
+    int c0 = __builtin_amdgcn_readfirstlane(bcnt[r * 2]);
+    int c1 = __builtin_amdgcn_readfirstlane(bcnt[r * 2 + 1]);
+    if (c1 > fcap) {                     // appends were dropped: the caller redoes the sweep
+        if (lane == 0) atomicAdd(ovf, 1);
+        c1 = fcap;
+    }
+    if (c0 > C) c0 = compact_row_core(k0, i0, c0, C).kept;
+    if (c1 > cap - c0) c1 = compact_row_core(k1, i1, c1, C).kept;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    constexpr int R = 16;                // cap <= 1024
+    float kv[R];
+    int32_t iv[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const int i = t * 64 + lane;
+        if (i < c1) { kv[t] = k1[i]; iv[t] = i1[i]; }
+    }
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        const int i = t * 64 + lane;
+        if (i < c1) { k0[c0 + i] = kv[t]; i0[c0 + i] = iv[t]; }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    int c = c0 + c1;
+    float thr = INFINITY;
+    if (c >= C) {
+        const Compacted k = compact_row_core(k0, i0, c, C);
+        c = k.kept;
+        thr = funkey(k.T);
+    }
+    if (lane == 0) {
+        gthr[r] = thr;
+        bcnt[r * 2] = c;
+        bcnt[r * 2 + 1] = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
+                                                int32_t* __restrict__ bcnt, int* ovf,
+                                                int64_t n) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n) {
+        gthr[r] = INFINITY;
+        bcnt[r * 2] = 0;
+        bcnt[r * 2 + 1] = 0;
+    }
+    if (r == 0) *ovf = 0;
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
+
+// Whether the direct-load sweep runs symmetric: by default when there are at
+// least 1,024 row panels (n > 261,888), where every band launch still fills
+// the GPU; SWANN_SWEEP_SYM=0|1 forces it (read per call).
+inline bool sweep_sym(int64_t ntile) {
+    const char* e = getenv("SWANN_SWEEP_SYM");
+    if (e && *e) return *e != '0' && ntile >= 2;
+    return ntile >= 1024;
+}
 
 // Waves per direct-load workgroup: 8 (128 x 64 wave tiles) or 16 (64 x 64).
 // SWANN_SWEEP_WAVES=8|16 pins it.
@@ -768,17 +941,72 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                            xn, scale);
     } else {
         _Float16* h = (_Float16*)extra;
+        extra += al256(n * (int64_t)dim * 2);
         hipLaunchKernelGGL(split_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                            (const float*)X, n, dim, h, (_Float16*)nullptr, scale, xn);
         hi = h;
     }
-    MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled, 1};
+    MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled, 1,
+                    0, 0, 0, nullptr, nullptr, cap};
     const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2);
     const bool ip = metric == SWANN_METRIC_IP;
     *used = 1;
     // the direct loads address a stage's 256 rows with 32-bit byte offsets
     const bool off32 = (int64_t)dim * 2 * kBM2 < (int64_t(1) << 32);
     if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && off32 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
+        const int64_t ntile = (n + kBM2 - 1) / kBM2;
+        if (splits >= 2 && sweep_sym(ntile) && sweep_waves() == 16) {
+            // symmetric sweep: tile (I, J), J >= I, scored once for the rows of
+            // both panels; launched in bands of J - I (1, 1, 2, 4, ... 256 at
+            // a time) with a merge after each, so every launch starts from
+            // thresholds over everything scored so far.  Two lists a row.
+            float* gthr = (float*)extra; extra += al256(n * 4);
+            int* ovf = (int*)extra;
+            hipLaunchKernelGGL(sym_init, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gthr,
+                               bcnt, ovf, n);
+            MfmaSweepArgs s = a;
+            s.splits = 2;
+            s.sym = 1;
+            s.gthr = gthr;
+            s.ovf = ovf;
+            s.fcap = cap;
+            if (const char* e = getenv("SWANN_SWEEP_SYM_FCAP")) {   // test hook: force overflow
+                const int f = atoi(e);
+                if (f >= 1 && f < cap) s.fcap = f;
+            }
+            for (int64_t b0 = 0; b0 < ntile;) {
+                const int64_t B = b0 == 0 ? 1 : (b0 < 256 ? b0 : 256);
+                s.b0 = b0;
+                s.b1 = b0 + B < ntile ? b0 + B : ntile;
+                const unsigned grid = (unsigned)(ntile - b0);
+                if (scaled) {
+                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(grid), dim3(1024), 0, st, s);
+                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(grid), dim3(1024), 0, st, s);
+                } else {
+                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(grid), dim3(1024), 0, st, s);
+                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(grid), dim3(1024), 0, st, s);
+                }
+                hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, bkey,
+                                   bid, bcnt, gthr, ovf, n, cap, s.fcap, C);
+                const int rc = launch_status("sweep (mfma, symmetric)");
+                if (rc) return rc;
+                b0 = s.b1;
+            }
+            // a list that overflowed lost candidates: redo the sweep the
+            // one-sided way (one small read-back; the build is not on the
+            // search path)
+            int dropped = 0;
+            if (hipMemcpyAsync(&dropped, ovf, sizeof(int), hipMemcpyDeviceToHost, st) !=
+                    hipSuccess ||
+                hipStreamSynchronize(st) != hipSuccess) {
+                set_error("sweep (mfma, symmetric): reading the overflow count failed");
+                return SWANN_E_LAUNCH;
+            }
+            if (dropped == 0) {
+                *used = 2;
+                return SWANN_OK;
+            }
+        }
         a.splits = splits;
         *used = splits;
         const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2 * splits);
@@ -809,10 +1037,11 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     return launch_status("sweep (mfma)");
 }
 
-// Extra workspace: norms, scales and (fp32 corpus) the fp16 plane.
+// Extra workspace: norms, scales, (fp32 corpus) the fp16 plane, and the
+// symmetric sweep's thresholds and overflow count.
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
-    return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2);
+    return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) + al256(n * 4) + 256;
 }
 
 // Column splits of the direct-load sweep: enough workgroups to give every

@@ -1,7 +1,7 @@
 """The public interface: build an index over vectors, then search it
 (swann/index.py).
 
-    import swann_amd as swann
+    import swann                  # or: import swann_amd as swann
     index = swann.Index.build(X, metric="ip")      # X: (n, d) float32 or float16
     ids, dist = index.search(Q, k=10)
 

@@ -201,14 +201,20 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
 
 
-@pytest.mark.parametrize("switch", [("SWANN_SWEEP_WAVES", "8"), ("SWANN_SWEEP_REGSTAGE", "1")])
+@pytest.mark.parametrize("switch", [("SWANN_SWEEP_WAVES", "8"), ("SWANN_SWEEP_REGSTAGE", "1"),
+                                    ("SWANN_SWEEP_SYM", "1"), ("SWANN_SWEEP_SYM_FCAP", "4")])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtype):
-    """The direct-load sweep's 8-wave layout (128 x 64 wave tiles) and the
-    register-staged kernel, both chosen by environment at each call, keep
-    the oracle's lists like the default layout."""
+    """The direct-load sweep's 8-wave layout (128 x 64 wave tiles), the
+    register-staged kernel and the symmetric sweep (each tile scored once for
+    both of its panels' rows, in bands of launches), all chosen by
+    environment at each call, keep the oracle's lists like the default
+    layout; so does the symmetric sweep whose second lists are made to
+    overflow (4 entries of room), which must redo the sweep one-sided."""
     monkeypatch.setenv(*switch)
+    if switch[0] == "SWANN_SWEEP_SYM_FCAP":
+        monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
     n, d = 3001, 64
     X = gaussian(n, d, 431 + metric, metric == 0)
     if metric == 1:
@@ -228,13 +234,16 @@ def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtyp
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
+@pytest.mark.parametrize("sym", ["0", "1"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_with_duplicate_rows_matches_oracle(metric, dtype):
+def test_mfma_sweep_with_duplicate_rows_matches_oracle(monkeypatch, metric, dtype, sym):
     """A larger sweep (n = 12,000: 47 row panels, 47 column tiles, several
     compactions per row) with rows 0..999 duplicated at 6000..6999, so many
     rows hold exact ties, some of them at the C-th place: the lists must be
-    the oracle's, and each duplicated row must find its twin."""
+    the oracle's, and each duplicated row must find its twin -- one-sided
+    and symmetric (47 panels, 9 band launches)."""
+    monkeypatch.setenv("SWANN_SWEEP_SYM", sym)
     n, d, C = 12000, 64, 16
     X = gaussian(n, d, 421 + metric, metric == 0)
     if metric == 1:
