@@ -693,6 +693,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         if (++kt == nk) { kt = 0; cb += kBN2; }
     };
     f32x16 acc[BI][BJ];
+    float thr_next = INFINITY;       // symmetric sweep: this thread's column threshold in flight
     int tpar = 0;                    // parity of the current column tile (its need flag)
     issue(0, kt_f, cb_f);
     adv(kt_f, cb_f);
@@ -752,14 +753,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             for (int i = 0; i < BI; ++i)
 #pragma unroll
                 for (int j = 0; j < BJ; ++j) acc[i][j] = (f32x16){};
-            // the new tile's column thresholds; every wave finished the last
-            // tile's epilogue before this stage's barrier, and the next barrier
-            // (or the one below, for a one-stage tile) publishes them
-            if (a.sym && cbt != r0) {
-                if (tid < kBN2) thrc[tid] = cbt + tid < n ? a.gthr[cbt + tid] : INFINITY;
-                if (nk == 1) __syncthreads();
+            // the new tile's column thresholds: loaded now, stored into LDS
+            // after the next stage's barrier (the load lands under this
+            // stage's MFMAs and the kernel's vmcnt(0) wait) and read by the
+            // tile's epilogue stages later; every wave finished the last
+            // tile's epilogue before this stage's barrier.  A tile of one or
+            // two stages stores at once, behind a barrier of its own.
+            if (a.sym && cbt != r0 && tid < kBN2)
+                thr_next = cbt + tid < n ? a.gthr[cbt + tid] : INFINITY;
+            if (a.sym && cbt != r0 && nk <= 2) {
+                if (tid < kBN2) thrc[tid] = thr_next;
+                __syncthreads();
             }
         }
+        if (kt == 1 && nk > 2 && a.sym && cbt != r0 && tid < kBN2) thrc[tid] = thr_next;
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
         f16x8 fa[2][BI], fb[2][BJ];
