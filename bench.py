@@ -62,7 +62,8 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # profiles/advance_kernel_c3_hbm_traffic.md).  Valid only for the kernel source it
 # was measured on (kernel_source_key of swann_amd/csrc/search.hip: SHA-256 prefix of
 # the source without comments), the same workload and knobs and the same per-query
-# table size (Index._table_slots); otherwise `traffic` is reported as null.
+# claims layout (Index._claims: "bits<n>" or the table's slots); otherwise `traffic`
+# is reported as null.
 PMC_TRAFFIC = {
     ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, 524_288, "14d31daae3226b8d"): 4.992e12,
 }
@@ -197,6 +198,7 @@ class Searcher:
         self.cfg = cfg
         self.codes = None           # (codes, alpha, mu, margin) for the sign-code pre-filter
         self.ws = None
+        self.bits, self.slots = False, None     # claims layout, decided on the first step
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
 
     def step(self, eps, record=False):
@@ -205,6 +207,13 @@ class Searcher:
             self.ws = torch.empty(int(S._ws_size(self.Q.shape[0], ix._cat.shape[0])),
                                   dtype=torch.uint8, device=self.Q.device)
         ev = self.ev
+        if self.slots is None:
+            knobs = SimpleNamespace(branches=cfg["branches"], budget=cfg["budget"])
+            # the sign-code filter needs the (id, d) table; the plain search
+            # shares its claims as Index.search does
+            self.bits, self.slots = ((False, ix._table_size(self.Q.shape[0], knobs))
+                                     if self.codes is not None else
+                                     ix._claims(self.Q.shape[0], knobs))
         if record:
             ev[0].record()
         ent = S.select_nearest(self.Q, ix._cat, cfg["branches"], metric=ix._m, workspace=self.ws)
@@ -214,9 +223,8 @@ class Searcher:
         st = E.init_states(ix.X, self.Q, seeds, L=cfg["queue"], B=cfg["budget"], D=ix.G.shape[1],
                            metric=ix._m, team_size=cfg["team"], stop_eps=eps, kstop=self.k,
                            shared_cache=True, shared_bound=True, exclusive=True,
-                           elide_visited=True,
-                           cache_slots=ix._table_slots(self.Q.shape[0], SimpleNamespace(
-                               branches=cfg["branches"], budget=cfg["budget"])))
+                           elide_visited=True, cache_slots=None if self.bits else self.slots,
+                           claim_bits=self.bits)
         if record:
             ev[2].record()
         E.advance(ix.X, ix.G, self.Q, st, cfg["budget"], codes=self.codes)
@@ -608,10 +616,11 @@ def main():
     achieved = adv_bytes / adv_s
     ph_mean = {k2: round(float(np.mean([p[k2] for p in phases])), 3) for k2 in phases[0]}
     src_sha = kernel_source_key(ROOT / "swann_amd" / "csrc" / "search.hip")
-    slots = index._table_slots(nq, SimpleNamespace(branches=cfg["branches"],
-                                                   budget=cfg["budget"]))
+    bits, slots = index._claims(nq, SimpleNamespace(branches=cfg["branches"],
+                                                    budget=cfg["budget"]))
+    layout = f"bits{slots}" if bits else slots
     traffic = PMC_TRAFFIC.get((a.config, n, nq, cfg["branches"], cfg["queue"], cfg["budget"],
-                               eps, slots, src_sha))
+                               eps, layout, src_sha))
 
     cpu = None
     if not a.no_cpu and a.cpu_sample > 0:
@@ -692,7 +701,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
                      "kernel": "advance_kernel",
                      "bytes_per_launch": adv_bytes, "launch_ms": round(adv_s * 1e3, 3),
-                     "table_slots": slots},
+                     "claims": layout},
         "cpu_baseline": cpu,
         "with_codes": with_codes,
         "build_c5": build_c5,

@@ -72,7 +72,14 @@ int swann_device_count(void);
  *            kernels detect that adjacency and stride by 2; a claim and the
  *            distance stored into it then share a cache line, and a slot is
  *            probed as one 64-bit word, so the pairs must start 8-byte
- *            aligned -- SWANN_E_INVALID otherwise)
+ *            aligned -- SWANN_E_INVALID otherwise);
+ *            or claim bits: cache_id [Q, Hc / 32] int32 with cache_d = NULL,
+ *            one bit per corpus row (Hc a power of two >= n and >= 32).
+ *            For exclusive claims without sign codes only: a row whose bit
+ *            another branch set is skipped, as the table skips a row it
+ *            finds claimed; no distance is cached.  This layout has no
+ *            counterpart in the reference's table; it decides claims as
+ *            that table does when no probe chain runs out.
  *   bound    [Q] fp32 or NULL
  * A disabled feature is a NULL pointer (and Hc = 0), matching the
  * reference's empty-tensor convention (swann/_engine.py:269-274).

@@ -228,15 +228,20 @@ def cache_size(J, B, D, share=4.0, cap=1 << 20):
 def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                  policy=POLICY_BEST, stop_eps=-1.0, kstop=10, H=None, Hc=0,
                  bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0,
-                 codes=None, schedule="serial"):
+                 codes=None, schedule="serial", claim_bits=False):
     """All J branches of one query, stepped in turn (every step atomic).
     seeds: [J] or [J, V].  Returns a dict of [J, ...] arrays.
+
+    claim_bits: exclusive claims kept as one bit per corpus row instead of
+    the Hc-slot table (Hc is then ignored); the table at a size where no
+    probe fails decides every claim the same way.
 
     schedule "serial": a step reads the bound as the steps before it left it;
     "rounds": every step of round s reads the bound as it was when the round
     began (a concurrent launch's shape: a query's branches start together)."""
     X, dt = _corpus(X)
     cp, cw, ap, mp, mg, _keep = _codes(codes)
+    Hc = _claim_arg(X, Hc, exclusive, claim_bits, codes)
     G = np.ascontiguousarray(G, dtype=np.int32)
     q = np.ascontiguousarray(q, dtype=np.float32)
     seeds = np.asarray(seeds, dtype=np.int32)
@@ -248,7 +253,8 @@ def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
     ids = np.empty((J, L), np.int32); dist = np.empty((J, L), np.float32)
     expd = np.empty((J, L), np.uint8); lin = np.empty((J, L), np.uint8)
     vis = np.empty((J, H), np.int32); ctr = np.empty((J, NCTR), np.int32)
-    cid = np.empty(max(1, Hc), np.int32); cdd = np.empty(max(1, Hc), np.float32)
+    cid = np.empty(max(1, Hc, (-Hc + 31) // 32), np.int32)
+    cdd = np.empty(max(1, Hc), np.float32)
     bnd = np.empty(1, np.float32)
     lib().so_search_query(_p(X), dt, X.shape[1], _p(G), G.shape[1], _p(q), _p(seeds), J, V,
                           L, B, H, int(metric), int(team), int(policy), float(stop_eps),
@@ -257,15 +263,18 @@ def search_query(X, G, q, seeds, L=16, B=16, metric=METRIC_IP, team=32,
                           _p(ids), _p(dist), _p(expd), _p(lin), _p(vis), _p(ctr),
                           _p(cid), _p(cdd), _p(bnd), cp, cw, ap, mp, mg, SCHEDULES[schedule])
     return dict(ids=ids, dist=dist, expanded=expd, lineage=lin, visited=vis,
-                counters=ctr, cache_id=cid[:Hc], cache_d=cdd[:Hc], bound=bnd[0])
+                counters=ctr, cache_id=cid[:Hc] if Hc >= 0 else cid[:(-Hc + 31) // 32],
+                cache_d=cdd[:max(Hc, 0)], bound=bnd[0])
 
 
 def search_batch(X, G, Q, seeds, k=10, L=16, B=16, metric=METRIC_IP, team=32,
                  policy=POLICY_BEST, stop_eps=-1.0, H=None, Hc=0, bound=False,
-                 exclusive=False, nthreads=0, counters=False, schedule="serial"):
+                 exclusive=False, nthreads=0, counters=False, schedule="serial",
+                 claim_bits=False):
     """search_query + merge for every query (OpenMP over queries).
     seeds: [nq, J] or [nq, J, V]."""
     X, dt = _corpus(X)
+    Hc = _claim_arg(X, Hc, exclusive, claim_bits, None)
     G = np.ascontiguousarray(G, dtype=np.int32)
     Q = np.ascontiguousarray(Q, dtype=np.float32)
     seeds = np.asarray(seeds, dtype=np.int32)
@@ -282,6 +291,19 @@ def search_batch(X, G, Q, seeds, k=10, L=16, B=16, metric=METRIC_IP, team=32,
                           int(bool(exclusive)), int(k), _p(oi), _p(od), _p(oc),
                           int(nthreads), SCHEDULES[schedule])
     return (oi, od, oc) if counters else (oi, od)
+
+
+def _claim_arg(X, Hc, exclusive, claim_bits, codes):
+    """The C entry points' Hc: the table's slots, or minus the number of
+    claim bits (a power of two >= n and >= 32, as the GPU sizes them)."""
+    if not claim_bits:
+        return int(Hc)
+    if not exclusive or codes is not None:
+        raise ValueError("claim bits stand for exclusive claims without sign codes")
+    nb = 32
+    while nb < X.shape[0]:
+        nb <<= 1
+    return -nb
 
 
 # -- sign codes ----------------------------------------------------------

@@ -233,6 +233,9 @@ typedef struct {
     int max_exp, policy, V;
     float stop_eps; int kstop;
     int32_t* cid; float* cdd; int Hc; float* bound; int exclusive;
+    /* claim bits in place of the table (Hc < 0 at the entry points: -Hc
+     * bits, one per row); NULL: off */
+    uint32_t* cbits;
     /* where a step reads the bound (NULL: *bound itself).  The rounds
      * schedule points it at the value the bound had when the round began. */
     const float* bound_rd;
@@ -351,7 +354,14 @@ static int so_step(const so_cfg* c, int32_t* ids, float* dist, uint8_t* expd, ui
         if (!isnew) { cov += 1; continue; }
         int cs = -1, claimed = 0;
         float d = FLT_MAX;
-        if (c->Hc > 0) {
+        if (c->cbits) {
+            /* exclusive claims decide by the row's bit alone: the first
+             * branch to set it owns the row, everyone else skips it */
+            const uint32_t bit = 1u << (v & 31);
+            if (c->cbits[v >> 5] & bit) { ctr[4] += 1; cov += 1; continue; }
+            c->cbits[v >> 5] |= bit;
+            ctr[5] += 1;
+        } else if (c->Hc > 0) {
             cs = so_cache_slot(c->cid, c->Hc, v, &claimed);
             d = (cs >= 0 && !claimed) ? c->cdd[cs] : FLT_MAX;
         }
@@ -533,6 +543,7 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
                      const int32_t* codes, int cwords, const float* calpha, const float* cmu,
                      float cmargin, int sched) {
     for (int t = 0; t < Hc; ++t) { cache_id[t] = 0; cache_d[t] = FLT_MAX; }
+    for (int t = 0; t < (-Hc + 31) / 32; ++t) cache_id[t] = 0;     /* claim bits */
     float bound = FLT_MAX;
     for (int j = 0; j < J; ++j)
         so_init_branch(X, dt, dim, q, seeds + (int64_t)j * V, V, L, H, metric, team,
@@ -545,7 +556,8 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
     c.L = L; c.H = H; c.metric = metric; c.team = team;
     c.max_exp = B; c.policy = policy; c.V = V;
     c.stop_eps = stop_eps; c.kstop = kstop;
-    c.cid = Hc > 0 ? cache_id : NULL; c.cdd = Hc > 0 ? cache_d : NULL; c.Hc = Hc;
+    c.cid = Hc > 0 ? cache_id : NULL; c.cdd = Hc > 0 ? cache_d : NULL; c.Hc = Hc > 0 ? Hc : 0;
+    c.cbits = Hc < 0 ? (uint32_t*)cache_id : NULL;
     c.bound = use_bound ? &bound : NULL;
     c.exclusive = exclusive;
     c.stall_patience = stall_patience; c.crowd_frac = crowd_frac;
@@ -594,7 +606,8 @@ void so_search_batch(const void* X, int dt, int dim, const int32_t* G, int D,
         uint8_t* lin = (uint8_t*)malloc((size_t)J * L);
         int32_t* vis = (int32_t*)malloc(sizeof(int32_t) * (size_t)J * H);
         int32_t* ctr = (int32_t*)malloc(sizeof(int32_t) * (size_t)J * SO_NCTR);
-        int32_t* cid = (int32_t*)malloc(sizeof(int32_t) * (size_t)(Hc > 0 ? Hc : 1));
+        int32_t* cid = (int32_t*)malloc(sizeof(int32_t) *
+                                        (size_t)(Hc > 0 ? Hc : Hc < 0 ? (-Hc + 31) / 32 : 1));
         float* cdd = (float*)malloc(sizeof(float) * (size_t)(Hc > 0 ? Hc : 1));
         int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)J * kk);
         float* bd = (float*)malloc(sizeof(float) * (size_t)J * kk);

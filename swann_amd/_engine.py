@@ -77,6 +77,7 @@ class SearchState:
     cache_d: torch.Tensor = None
     bound: torch.Tensor = None
     exclusive: bool = False
+    table_slots: int = 0     # Hc: table slots, or claim bits, a query (0 = no table)
 
     @property
     def shape(self):
@@ -140,7 +141,8 @@ class SearchState:
                            stop_eps=self.stop_eps, stall_patience=self.stall_patience,
                            crowd_frac=self.crowd_frac, kstop=self.kstop,
                            cache_id=c(self.cache_id), cache_d=c(self.cache_d),
-                           bound=c(self.bound), exclusive=self.exclusive)
+                           bound=c(self.bound), exclusive=self.exclusive,
+                           table_slots=self.table_slots)
 
 
 def ctypes_ptr(t):
@@ -175,11 +177,17 @@ def _check_corpus(X, Qv):
 def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32,
                 policy=POLICY_BEST, stop_eps=-1.0, kstop=10, shared_cache=False,
                 shared_bound=False, exclusive=False, stall_patience=0, crowd_frac=0.0,
-                elide_visited=False, cache_slots=None) -> SearchState:
+                elide_visited=False, cache_slots=None, claim_bits=False) -> SearchState:
     """One state per (query, branch); swann/_engine.py:219-278.
 
     `seeds` is int32 [Q, J] (one entry per branch) or [Q, J, V] (V entries
-    sharing one branch).  -1 is an empty slot."""
+    sharing one branch).  -1 is an empty slot.
+
+    `claim_bits` replaces the shared table with one claim bit per corpus row
+    (exclusive claims only, and no sign codes in `advance`): under exclusive
+    claims a row found in the table is never a candidate again, so its cached
+    distance is never used, and the bit decides the same.  It takes n / 8
+    bytes a query instead of the table's 8 bytes a slot."""
     _check_corpus(X, Qv)
     seeds = seeds.to(device=X.device, dtype=torch.int32).contiguous()
     if seeds.dim() == 2:
@@ -202,7 +210,14 @@ def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32
         B=B, metric=metric, team_size=team_size, V=V, policy=policy,
         stop_eps=float(stop_eps), kstop=int(kstop), stall_patience=int(stall_patience),
         crowd_frac=float(crowd_frac))
-    if shared_cache and J > 1:
+    if claim_bits and not (exclusive and shared_cache and J > 1):
+        raise ValueError("claim_bits needs exclusive claims over a shared table (J > 1)")
+    if claim_bits:
+        Hc = next_pow2(max(X.shape[0], 32))
+        st.cache_id = torch.empty((Q, Hc // 32), dtype=torch.int32, device=dev)
+        st.cache_d = torch.empty((0, 0), dtype=torch.float32, device=dev)
+        st.table_slots = Hc
+    elif shared_cache and J > 1:
         # cache_slots (a power of two) replaces the closed-form size
         Hc = int(cache_slots) if cache_slots else cache_size(J, B, D)
         if Hc & (Hc - 1):
@@ -212,13 +227,14 @@ def init_states(X, Qv, seeds, L=16, B=16, D=None, metric=METRIC_IP, team_size=32
         tab = torch.empty((Q, Hc, 2), dtype=torch.int32, device=dev)
         st.cache_id = tab[..., 0]
         st.cache_d = tab.view(torch.float32)[..., 1]
+        st.table_slots = Hc
     else:
         st.cache_id = torch.empty((0, 0), dtype=torch.int32, device=dev)
         st.cache_d = torch.empty((0, 0), dtype=torch.float32, device=dev)
     st.exclusive = bool(exclusive and shared_cache and J > 1)
     st.bound = (torch.empty((Q,), dtype=torch.float32, device=dev)
                 if (shared_bound and J > 1) else torch.empty((0,), dtype=torch.float32, device=dev))
-    Hc = st.cache_id.shape[1] if st.cache_id.numel() else 0
+    Hc = st.table_slots
     with torch.cuda.device(dev):
         call("swann_init_states", ptr(X), _DTYPES[X.dtype], X.shape[0], X.shape[1],
              ptr(Qv), Q, ptr(seeds), J, V, ptr(st.ids), ptr(st.dist), ptr(st.expanded),
@@ -257,7 +273,9 @@ def advance(X, G, Qv, state: SearchState, delta_expansions: int, active=None,
         cw = cd.shape[1]
     Q, J, L = state.ids.shape
     H = state.visited.shape[-1]
-    Hc = state.cache_id.shape[1] if state.cache_id is not None and state.cache_id.numel() else 0
+    Hc = state.table_slots
+    if Hc and codes is not None and state.cache_d.numel() == 0:
+        raise ValueError("sign codes need the shared table: init_states(claim_bits=False)")
     nact = 0
     if active is not None:
         active = active.to(device=X.device, dtype=torch.int32).contiguous()
@@ -353,7 +371,7 @@ def advance_chunked(X, G, Qv, state: SearchState, total: int, chunk: int, codes=
 def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
            policy=POLICY_BEST, stop_eps=-1.0, shared_cache=False, shared_bound=False,
            exclusive=False, stall_patience=0, crowd_frac=0.0, elide_visited=False, chunk=0,
-           codes=None, check=None, cache_slots=None):
+           codes=None, check=None, cache_slots=None, claim_bits=False):
     """init -> advance(budget) -> per-branch best-k -> merged top-k
     (swann/_engine.py:428-447).  `check` overrides the global overflow guard:
     True checks synchronously, False skips it."""
@@ -361,7 +379,8 @@ def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
                      policy=policy, stop_eps=stop_eps, kstop=k, shared_cache=shared_cache,
                      shared_bound=shared_bound, exclusive=exclusive,
                      stall_patience=stall_patience, crowd_frac=crowd_frac,
-                     elide_visited=elide_visited, cache_slots=cache_slots)
+                     elide_visited=elide_visited, cache_slots=cache_slots,
+                     claim_bits=claim_bits)
     if chunk:
         advance_chunked(X, G, Qv, st, B, chunk, codes=codes)
     else:

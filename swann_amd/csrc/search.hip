@@ -307,6 +307,23 @@ __device__ __forceinline__ int cache_slot_pair(unsigned long long* tab, int Hc, 
     return -1;
 }
 
+// Claims without cached distances: one bit per corpus row (Hc >= n bits a
+// query).  Under exclusive claims a branch that finds a row in the shared
+// table never takes it as a candidate (local_search.cu:541-592): it skips it
+// when the distance is stored and, when the claimer has not stored it yet,
+// scores it again only to drop it.  The distance is therefore never read, and
+// a bit per row decides the same thing: the first to set it owns the row.  A
+// query's 128 KiB at a million rows stays in L2 and the MALL while its
+// branches run, where a 4 MiB table of (id, d) pairs does not; and there is
+// no probe chain to run out.  The sign-code filter keeps the table: a row it
+// skips stays claimed but unscored, and another branch may score it later.
+__device__ __forceinline__ bool claim_bit(int32_t* bits, int key) {
+    const uint32_t bit = 1u << (key & 31);
+    const uint32_t old = __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(bits) + (key >> 5),
+                                               bit, __ATOMIC_RELAXED, SWANN_TABLE_SCOPE);
+    return (old & bit) == 0;
+}
+
 __device__ __forceinline__ float load_agent_f(const float* p) {
     const int b = __hip_atomic_load(reinterpret_cast<const int*>(p), __ATOMIC_RELAXED,
                                     SWANN_TABLE_SCOPE);
@@ -381,7 +398,18 @@ __global__ __launch_bounds__(BLOCK) void init_kernel(InitArgs a) {
     }
     // The query's table and bound belong to all J branches; they clear it
     // between them (local_search.cu:302-313).
-    if (a.Hc > 0 && a.ts == 2) {
+    if (a.Hc > 0 && a.ts == 0) {
+        // claim bits, Hc / 32 words a query
+        const int64_t nw = a.Hc >> 5;
+        int32_t* bw = a.cache_id + q * nw;
+        if ((nw & 3) == 0 && (reinterpret_cast<uintptr_t>(bw) & 15) == 0) {
+            int4* b4 = reinterpret_cast<int4*>(bw);
+            for (int64_t t = j * BLOCK + tid; t < nw / 4; t += a.J * BLOCK)
+                b4[t] = make_int4(0, 0, 0, 0);
+        } else {
+            for (int64_t t = j * BLOCK + tid; t < nw; t += a.J * BLOCK) bw[t] = 0;
+        }
+    } else if (a.Hc > 0 && a.ts == 2) {
         // interleaved (id, d) pairs, one 8-byte store each
         int2* p2 = reinterpret_cast<int2*>(a.cache_id + q * (int64_t)a.Hc * 2);
         const int fm = __float_as_int(FLT_MAX);
@@ -525,8 +553,9 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     int32_t* ctr = a.counters + flat * kNctr;
     const int64_t qb = flat * (int64_t)L;
     const int ts = a.ts;
-    int32_t* cid = a.Hc > 0 ? a.cache_id + q * (int64_t)a.Hc * ts : nullptr;
-    float* cdd = a.Hc > 0 ? a.cache_d + q * (int64_t)a.Hc * ts : nullptr;
+    int32_t* cid = a.Hc == 0 ? nullptr
+                 : a.cache_id + q * (ts == 0 ? (int64_t)(a.Hc >> 5) : (int64_t)a.Hc * ts);
+    float* cdd = a.Hc > 0 && ts > 0 ? a.cache_d + q * (int64_t)a.Hc * ts : nullptr;
     const float* qrow = a.Qv + q * (int64_t)a.dim;
     const XT* X = reinterpret_cast<const XT*>(a.X);
 
@@ -647,7 +676,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (!isnew) { ++cov; continue; }
             int slot = -1, claimed = 0;
             float d = FLT_MAX;
-            if (a.Hc > 0 && ts == 2) {
+            if (a.Hc > 0 && ts == 0) {
+                if (!claim_bit(cid, v)) { ++r_hits; ++cov; continue; }  // owned elsewhere
+                ++r_claim;
+            } else if (a.Hc > 0 && ts == 2) {
                 slot = cache_slot_pair(reinterpret_cast<unsigned long long*>(cid), a.Hc, v,
                                        &claimed, &d);
             } else if (a.Hc > 0) {
@@ -963,8 +995,9 @@ size_t advance_lds(int dim, int D, int L) {
 // The table is interleaved (id, d) pairs when cache_d is the word right after
 // cache_id: two separate [Q, Hc] arrays cannot overlap that way.  Pairs are
 // probed as 64-bit words, so they must start 8-byte aligned (checked by the
-// entry points).
+// entry points).  With no cache_d it is claim bits: Hc bits a query, stride 0.
 int table_stride(const int32_t* cache_id, const float* cache_d, int Hc) {
+    if (Hc > 0 && cache_id && !cache_d) return 0;
     if (Hc > 0 && cache_id &&
         reinterpret_cast<const char*>(cache_d) == reinterpret_cast<const char*>(cache_id) + 4)
         return 2;
@@ -1156,10 +1189,13 @@ int swann_init_states(const void* X, int x_dtype, int64_t n, int dim, const floa
     if (rc) return rc;
     SWANN_REQUIRE(Q == 0 || (X && Qv && seeds && ids && dist && expd && lin && visited && counters),
                   "init_states: a required pointer is NULL");
-    SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "init_states: Hc > 0 needs cache_id and cache_d");
-    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) == 1 ||
+    SWANN_REQUIRE(Hc == 0 || cache_id, "init_states: Hc > 0 needs cache_id");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) != 2 ||
                       (reinterpret_cast<uintptr_t>(cache_id) & 7) == 0,
                   "init_states: an interleaved (id, d) table must be 8-byte aligned");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) != 0 || (Hc >= n && Hc >= 32),
+                  "init_states: claim bits (no cache_d) need Hc >= n and >= 32, got Hc = %d for "
+                  "n = %lld", Hc, (long long)n);
     if (Q == 0) return SWANN_OK;
     InitArgs a{X, Qv, seeds, ids, dist, expd, lin, visited, counters, dim, J, V, L, H, metric,
                Q, n, Hc ? cache_id : nullptr, Hc ? cache_d : nullptr, Hc, bound,
@@ -1187,11 +1223,15 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
     SWANN_REQUIRE(!codes || (alpha && cmu), "advance: codes need alpha and cmu");
     SWANN_REQUIRE(Q == 0 || (X && G && Qv && ids && dist && expd && lin && visited && counters),
                   "advance: a required pointer is NULL");
-    SWANN_REQUIRE(Hc == 0 || (cache_id && cache_d), "advance: Hc > 0 needs cache_id and cache_d");
-    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) == 1 ||
+    SWANN_REQUIRE(Hc == 0 || cache_id, "advance: Hc > 0 needs cache_id");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) != 2 ||
                       (reinterpret_cast<uintptr_t>(cache_id) & 7) == 0,
                   "advance: an interleaved (id, d) table must be 8-byte aligned");
     SWANN_REQUIRE(!exclusive || Hc > 0, "advance: exclusive claims need the shared table");
+    SWANN_REQUIRE(table_stride(cache_id, cache_d, Hc) != 0 || (Hc >= n && Hc >= 32 && exclusive &&
+                                                                 !codes),
+                  "advance: claim bits (no cache_d) need Hc >= n and >= 32, exclusive claims and "
+                  "no sign codes, got Hc = %d for n = %lld", Hc, (long long)n);
     const int64_t nb = active ? nactive : Q * J;
     if (nb == 0 || delta <= 0) return SWANN_OK;
     AdvArgs a{X, G, Qv, ids, dist, expd, lin, visited, counters, dim, D, J, L, H, metric,

@@ -105,37 +105,55 @@ class Index:
         be captured)."""
         entries = S.select_nearest(Q, self._cat, cfg.branches, metric=self._m)
         seeds = self.catalogue[entries].to(torch.int32)
+        bits, slots = self._claims(Q.shape[0], cfg)
         ids, dist, st = E.search(
             self.X, self.G, Q, seeds, k=k, L=cfg.queue, B=cfg.budget, metric=self._m,
             team_size=cfg.team, stop_eps=cfg.stop_eps, shared_cache=True, shared_bound=True,
             exclusive=True, elide_visited=True, check=False,
-            cache_slots=self._table_slots(Q.shape[0], cfg))
+            cache_slots=None if bits else slots, claim_bits=bits)
         return ids, dist, st, st.overflow()
 
-    def _table_slots(self, nq: int, cfg: SearchConfig) -> int:
-        """Slots of each query's shared table.  The reference sizes it for a
-        quarter of the rows the branches could score (swann/_engine.py:186-198);
-        a table that full runs long probe chains, so this takes up to four
-        times that (the closed form with share 1, capped at 2^20 slots), halved
-        until the batch's tables fit a quarter of the free device memory, and
-        never below the reference's size.  At C3 (64 branches, 10,000 queries)
-        the 4x table is 10% faster at the same recall.  Decided once per
-        (batch, branches, budget), so repeated and captured searches keep one
-        size."""
+    def _claims(self, nq: int, cfg: SearchConfig) -> tuple[bool, int]:
+        """How the branches of a query share their claims: (True, bits) for
+        one claim bit per corpus row, (False, slots) for the reference's
+        per-query table of (id, d) pairs (swann/_engine.py:186-198).  Under
+        exclusive claims a row found in the table is never a candidate again,
+        so the bits decide the same as a table whose probes never fail, in
+        n / 8 bytes a query, cleared and probed in L2 rather than HBM (at C3:
+        128 KiB a query against the table's 4 MiB, init 2 ms instead of 9,
+        the same advance time at 64 branches and 6% less at 32).  Bits are
+        taken when the batch's fit a quarter of the free device memory.
+
+        Otherwise the table: the reference sizes it for a quarter of the rows
+        the branches could score; a table that full runs long probe chains, so
+        this takes up to four times that (the closed form with share 1, capped
+        at 2^20 slots), halved until the batch's tables fit a quarter of the
+        free device memory, and never below the reference's size.  Decided
+        once per (batch, branches, budget), so repeated and captured searches
+        keep one layout."""
         key = (nq, cfg.branches, cfg.budget)
-        hc = self._slots.get(key) if hasattr(self, "_slots") else None
-        if hc is None:
-            D = self.G.shape[1]
-            base = E.cache_size(cfg.branches, cfg.budget, D)
-            hc = E.cache_size(cfg.branches, cfg.budget, D, share=1.0)
+        got = self._layouts.get(key) if hasattr(self, "_layouts") else None
+        if got is None:
             free, _ = torch.cuda.mem_get_info(self.X.device)
-            while hc > base and nq * hc * 8 > free // 4:
-                hc //= 2
-            hc = max(hc, base)
-            if not hasattr(self, "_slots"):
-                self._slots = {}
-            self._slots[key] = hc
-        return hc
+            nbits = E.next_pow2(max(self.X.shape[0], 32))
+            got = ((True, nbits) if nq * nbits // 8 <= free // 4 else
+                   (False, self._table_size(nq, cfg, free)))
+            if not hasattr(self, "_layouts"):
+                self._layouts = {}
+            self._layouts[key] = got
+        return got
+
+    def _table_size(self, nq: int, cfg, free: int | None = None) -> int:
+        """Slots of each query's (id, d) table (the layout the sign-code
+        filter needs, and the fallback of `_claims`)."""
+        if free is None:
+            free, _ = torch.cuda.mem_get_info(self.X.device)
+        D = self.G.shape[1]
+        base = E.cache_size(cfg.branches, cfg.budget, D)
+        hc = E.cache_size(cfg.branches, cfg.budget, D, share=1.0)
+        while hc > base and nq * hc * 8 > free // 4:
+            hc //= 2
+        return max(hc, base)
 
     def capture(self, batch: int, k: int = 10, config: SearchConfig | None = None,
                 **overrides) -> "CapturedSearch":

@@ -7,7 +7,7 @@ replay (Index.capture: no overflow guard) and eagerly.  Checked: replay and
 eager agree; returned distances equal an fp64 recomputation from the stored
 fp16 rows (1e-5) and the fp32 originals to 2e-3; no id twice in an answer;
 recall@10 over the whole pool (four batch-512 replays) within 0.005 of the
-oracle's rounds schedule on the same seeds and table size."""
+oracle's rounds schedule on the same seeds and claims layout."""
 import os
 import sys
 
@@ -106,14 +106,15 @@ def test_c4_captured_batches_match_eager_and_the_oracle(c4, J):
         note(f"c4 J={J} through batch {b}: replay {h_replay / (10 * nq_total):.4f} "
              f"eager {h_eager / (10 * nq_total):.4f} ({nq_total} queries)")
     assert abs(h_replay - h_eager) / (10 * nq_total) <= 0.005
-    # parity: the pool as four batch-512 searches, same seeds and table size
-    hc = index._table_slots(512, cfg)
+    # parity: the pool as four batch-512 searches, same seeds and claims layout
+    bits, hc = index._claims(512, cfg)
     seeds = index.catalogue[S.select_nearest(Qp, index._cat, J, metric=0)].to(torch.int32)
     cores = len(os.sched_getaffinity(0))
-    note(f"c4 J={J}: oracle rounds schedule on the pool, {cores} cores")
+    note(f"c4 J={J}: oracle rounds schedule on the pool, {cores} cores, bits {bits}")
     oi, _ = O.search_batch(c4["Xh"], c4["Gh"], Qp.cpu().numpy(), seeds.cpu().numpy(), k=10,
                            L=12, B=64, metric=0, team=32, stop_eps=0.05, H=1, Hc=hc, bound=True,
-                           exclusive=True, nthreads=cores, schedule="rounds")
+                           exclusive=True, nthreads=cores, schedule="rounds",
+                           claim_bits=bits)
     r_gpu = hits(pool_ids, truth) / (10 * POOL)
     r_oracle = hits(oi, truth) / (10 * POOL)
     note(f"c4 J={J} pool recall: gpu replay {r_gpu:.4f} oracle rounds {r_oracle:.4f}")

@@ -424,11 +424,13 @@ def test_large_batch_one_wave_layout_matches_oracle():
             assert_queue(st, qi, j, br, (qi, j))
 
 
-def test_claims_and_bound_multi_branch_statistics():
+@pytest.mark.parametrize("bits", [False, True])
+def test_claims_and_bound_multi_branch_statistics(bits):
     """Claims, bound and the elided visited table are racy by design: judge
     them by recall within 0.005 of the oracle's rounds schedule (every branch
     of a query starts together, as on the GPU), by distances that equal exact
-    recomputation, and by no duplicate ids in the answer."""
+    recomputation, and by no duplicate ids in the answer.  Claim bits are
+    judged against the oracle's table at a size no probe chain fills."""
     g = golden("refcpu_c1.npz")
     X = regen(10000, 128, 0, True, g["X_sha"])
     G = g["G"].astype(np.int32)
@@ -439,15 +441,15 @@ def test_claims_and_bound_multi_branch_statistics():
     Xg, Gg, Qg = to_gpu(X, G, Q)
     ids, dist, st = E.search(Xg, Gg, Qg, torch.from_numpy(seeds), k=10, L=12, B=64, metric=0,
                              team_size=16, stop_eps=0.05, shared_cache=True, shared_bound=True,
-                             exclusive=True, elide_visited=True)
+                             exclusive=True, elide_visited=True, claim_bits=bits)
     ids = ids.cpu().numpy(); dist = dist.cpu().numpy()
-    Hc = E.cache_size(16, 64, 32)
+    Hc = 16 * E.next_pow2(X.shape[0]) if bits else E.cache_size(16, 64, 32)
     oi, od = O.search_batch(X, G, Q, seeds, k=10, L=12, B=64, metric=0, team=16, stop_eps=0.05,
                             H=1, Hc=Hc, bound=True, exclusive=True, nthreads=8,
                             schedule="rounds")
     truth = exact_topk(X, Q, 10)
     r_gpu, r_cpu = recall(ids, truth, 10), recall(oi, truth, 10)
-    note("claims recall gpu", r_gpu, "oracle rounds", r_cpu)
+    note("claims recall gpu", r_gpu, "oracle rounds", r_cpu, "bits", bits)
     assert abs(r_gpu - r_cpu) <= 0.005
     for q in range(Q.shape[0]):
         got = ids[q][ids[q] >= 0]
@@ -625,6 +627,46 @@ def test_interleaved_and_separate_tables_agree():
         ea = sorted(zip(a.cache_id[q].tolist(), a.cache_d[q].view(torch.int32).tolist()))
         eb = sorted(zip(b.cache_id[q].tolist(), b.cache_d[q].view(torch.int32).tolist()))
         assert ea == eb, q
+
+
+@pytest.mark.parametrize("bits", [False, True])
+def test_claims_in_the_serial_schedule_are_exact(block, bits):
+    """Claims, bound and the elided visited table made deterministic: one
+    branch of each query per launch, one expansion each, is the oracle's
+    serial schedule (branch 0 step s, branch 1 step s, ...).  With a table
+    too sparse for a probe to fail, the (id, d) table and the claim bits
+    decide every claim alike, so both equal the oracle bit for bit: queues,
+    lineage and counters (claims stored, hits, scores)."""
+    X, G = toy(seed=141)
+    rng = np.random.default_rng(142)
+    nq, J, L, budget = 5, 4, 16, 20
+    Qv = gaussian(nq, X.shape[1], 143, True)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg = to_gpu(X, G, Qv)
+    Hc = 64 * E.next_pow2(X.shape[0])
+    st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=L, B=budget, D=G.shape[1],
+                       team_size=16, stop_eps=0.1, kstop=10, shared_cache=True,
+                       shared_bound=True, exclusive=True, elide_visited=True,
+                       cache_slots=None if bits else Hc, claim_bits=bits)
+    assert st.visited.shape[-1] == 1 and (st.cache_d.numel() == 0) == bits
+    for _ in range(budget):
+        for j in range(J):
+            act = torch.arange(nq, dtype=torch.int32, device=DEV) * J + j
+            E.advance(Xg, Gg, Qg, st, 1, active=act)
+    claims = 0
+    for qi in range(nq):
+        r = O.search_query(X, G, Qv[qi], seeds[qi], L=L, B=budget, team=16, stop_eps=0.1,
+                           kstop=10, H=1, Hc=Hc, bound=True, exclusive=True, schedule="serial")
+        gc = st.counters[qi].cpu().numpy()
+        for j in range(J):
+            assert np.array_equal(st.ids[qi, j].cpu().numpy(), r["ids"][j]), (qi, j)
+            assert st.dist[qi, j].cpu().numpy().tobytes() == r["dist"][j].tobytes(), (qi, j)
+            assert np.array_equal(st.expanded[qi, j].cpu().numpy(), r["expanded"][j]), (qi, j)
+            assert np.array_equal(st.lineage[qi, j].cpu().numpy(), r["lineage"][j]), (qi, j)
+            for c in (0, 1, 3, 4, 5, 6, 7, 8, 9):
+                assert gc[j, c] == r["counters"][j, c], (qi, j, c)
+        claims += int(gc[:, 4].sum())
+    assert claims > 0                       # branches did meet each other's claims
 
 
 def test_nan_distances_never_enter_a_queue():

@@ -133,14 +133,16 @@ def test_search_answers_are_exact_and_recall_meets_the_target(c3):
 
 
 def test_c3_headline_knobs_match_the_oracle_rounds_schedule(c3):
-    """The production search -- claims, bound, shared table, no visited table
+    """The production search -- claims, bound, no visited table
     (swann/index.py:105-109) -- at the bench's operating point (64 branches,
     queue 44, budget 64, stop_eps 0.3) on 1,000 queries, against the oracle's
     rounds schedule (each round's steps read the bound the round began with,
-    claims land at once) on the same seeds and the reference's table size
-    (swann/_engine.py:186-198): recall@10 within 0.005 with the reference's
-    table and with Index's larger one, distances equal to an fp64
-    recomputation, no id twice in an answer."""
+    claims land at once) on the same seeds.  Claims kept three ways: the
+    reference's table size (swann/_engine.py:186-198) and a 4x larger table,
+    each against the oracle at the reference's size, and claim bits (what
+    Index.search takes) against the oracle's claim bits.  Recall@10 within
+    0.005, distances equal to an fp64 recomputation, no id twice in an
+    answer."""
     import os
     from swann_amd import _engine as E
     from swann_amd import _select as S
@@ -149,35 +151,40 @@ def test_c3_headline_knobs_match_the_oracle_rounds_schedule(c3):
     J, L, Bud, eps = 64, 44, 64, 0.3
     seeds = index.catalogue[S.select_nearest(Q, index._cat, J, metric=0)].to(torch.int32)
     base = E.cache_size(J, Bud, DEG)
-    big = index._table_slots(Q.shape[0], swann.SearchConfig(branches=J, budget=Bud))
+    big = E.cache_size(J, Bud, DEG, share=1.0)
     truth = torch.topk(Q @ X16.float().T, 10, dim=1).indices.cpu().numpy()
 
     def rec(ids):
         return float(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(ids.tolist(),
                                                                         truth.tolist())]))
     cores = len(os.sched_getaffinity(0))
-    note(f"c3 headline: oracle rounds schedule on {cores} cores")
-    oi, _ = O.search_batch(X16.cpu().numpy(), G.cpu().numpy(), Q.cpu().numpy(),
-                           seeds.cpu().numpy(), k=10, L=L, B=Bud, metric=0, team=16,
-                           stop_eps=eps, H=1, Hc=base, bound=True, exclusive=True,
-                           nthreads=cores, schedule="rounds")
-    r_oracle = rec(oi)
-    for hc in (base, big):
+    Xh, Gh, Qh, Sh = X16.cpu().numpy(), G.cpu().numpy(), Q.cpu().numpy(), seeds.cpu().numpy()
+    r_oracle = {}
+    for bits in (False, True):
+        note(f"c3 headline: oracle rounds schedule on {cores} cores, claim bits {bits}")
+        oi, _ = O.search_batch(Xh, Gh, Qh, Sh, k=10, L=L, B=Bud, metric=0, team=16,
+                               stop_eps=eps, H=1, Hc=base, bound=True, exclusive=True,
+                               nthreads=cores, schedule="rounds", claim_bits=bits)
+        r_oracle[bits] = rec(oi)
+    for bits, hc in ((False, base), (False, big), (True, None)):
         ids, dist, _ = E.search(X16, G, Q, seeds, k=10, L=L, B=Bud, metric=0, team_size=16,
                                 stop_eps=eps, shared_cache=True, shared_bound=True,
-                                exclusive=True, elide_visited=True, check=False, cache_slots=hc)
+                                exclusive=True, elide_visited=True, check=False, cache_slots=hc,
+                                claim_bits=bits)
         ids_h = ids.cpu().numpy()
         r_gpu = rec(ids_h)
-        note("c3 headline recall: gpu", r_gpu, "table", hc, "oracle rounds", r_oracle)
-        assert abs(r_gpu - r_oracle) <= 0.005
+        note("c3 headline recall: gpu", r_gpu, "table", hc, "bits", bits,
+             "oracle rounds", r_oracle[bits])
+        assert abs(r_gpu - r_oracle[bits]) <= 0.005
         assert (ids_h >= 0).all() and all(len(set(r)) == 10 for r in ids_h.tolist())
         exact = 1.0 - (X16[ids.long().reshape(-1)].double().reshape(-1, 10, DIM)
                        @ Q.double()[:, :, None])[..., 0]
         assert torch.allclose(dist.double(), exact, rtol=0, atol=1e-5)
+    assert index._claims(Q.shape[0], swann.SearchConfig(branches=J, budget=Bud))[0]
     ids, _ = index.search(Q, k=10, branches=J, queue=L, budget=Bud, stop_eps=eps, team=16)
     r_index = rec(ids)
     note("c3 headline recall: Index.search", r_index)
-    assert abs(r_index - r_oracle) <= 0.005
+    assert abs(r_index - r_oracle[True]) <= 0.005
 
 
 # ---------------------------------------------------------------------------

@@ -489,3 +489,28 @@ def test_many_branches_keep_recall_in_every_layout(monkeypatch):
     note("128 branches recall by layout", rec)
     assert rec["64"] > 0.9
     assert min(rec["256"], rec["1024"]) >= rec["64"] - 0.07
+
+
+def test_claims_fall_back_to_the_table_when_bits_do_not_fit(monkeypatch):
+    """Index.search shares claims as one bit per row while the batch's bits
+    fit a quarter of the free device memory, else as the reference's (id, d)
+    table; both layouts decide claims alike, so recall agrees within 0.01 on
+    the same seeds, and a layout is kept per (batch, branches, budget)."""
+    X, Q = corpus(nq=400, seed=5)
+    index = swann.Index.build(X, degree=48, candidates=64)
+    truth = exact_topk(X, Q, 10)
+    cfg = swann.SearchConfig(branches=32, budget=48)
+    assert index._claims(Q.shape[0], cfg) == (True, 8192)
+    r_bits = recall(index.search(Q, k=10, branches=32, budget=48)[0], truth, 10)
+    small = swann.Index(index.X, index.G, metric="ip", catalogue=index.catalogue)
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda *a, **k: (4 * 400 * 8192 // 8 - 4,
+                                                                      1 << 40))
+    bits, slots = small._claims(Q.shape[0], cfg)
+    assert not bits and slots == swann._engine.cache_size(32, 48, 48)
+    ids, _, st, _ = small.search_async(Q, k=10, branches=32, budget=48)
+    assert st.cache_d.numel() > 0 and st.table_slots == slots
+    r_table = recall(ids.cpu().numpy(), truth, 10)
+    note("claims layouts: bits", r_bits, "table", r_table)
+    assert abs(r_bits - r_table) <= 0.01
+    monkeypatch.undo()
+    assert small._claims(Q.shape[0], cfg) == (False, slots)      # kept once decided

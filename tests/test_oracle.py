@@ -267,6 +267,36 @@ def test_claims_keep_branches_disjoint():
 
 
 @pytest.mark.parametrize("schedule", ["serial", "rounds"])
+def test_claim_bits_decide_like_a_table_that_never_fails(schedule):
+    """Exclusive claims as one bit per row equal the (id, d) table wherever
+    the table's probes never fail: every queue, lineage and counter.  A
+    small table, whose probe chains do run out, must differ (a failed probe
+    scores the row and keeps it as a candidate, a bit never fails), and so
+    must the bits without exclusive claims' skip of an owned row."""
+    X = gaussian(2000, 64, 85, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 32)
+    Q = gaussian(6, 64, 86, True)
+    rng = np.random.default_rng(87)
+    kw = dict(L=12, B=24, H=1, bound=True, exclusive=True, stop_eps=0.05, schedule=schedule)
+    differs_small = 0
+    for qi in range(6):
+        seeds = rng.integers(0, 2000, 16).astype(np.int32)
+        bits = O.search_query(X, G, Q[qi], seeds, claim_bits=True, **kw)
+        table = O.search_query(X, G, Q[qi], seeds, Hc=1 << 17, **kw)
+        for f in ("ids", "dist", "expanded", "lineage", "counters"):
+            assert np.array_equal(bits[f], table[f]), (qi, f)
+        assert bits["counters"][:, 4].sum() > 0                 # branches met
+        owned = np.unpackbits(bits["cache_id"].view(np.uint8), bitorder="little")
+        assert owned.sum() == bits["counters"][:, 5].sum()     # one bit per claim
+        small = O.search_query(X, G, Q[qi], seeds, Hc=32, **kw)
+        differs_small += not np.array_equal(small["counters"], bits["counters"])
+    assert differs_small > 0
+    with pytest.raises(ValueError):
+        O.search_query(X, G, Q[0], seeds, claim_bits=True, L=12, B=24, H=1, exclusive=False)
+
+
+@pytest.mark.parametrize("schedule", ["serial", "rounds"])
 @pytest.mark.parametrize("kstop", [1, 5, 10, 40])
 @pytest.mark.parametrize("exclusive", [False, True])
 def test_bound_is_the_least_kth_distance_any_branch_reached(kstop, exclusive, schedule):
