@@ -223,6 +223,47 @@ __device__ __forceinline__ float screen_thr(float thr, float na) {
 // threshold, so they never pass.  Self scores were set to -inf in the
 // accumulator (self_out), so their distance is +inf and never passes; the
 // merge adds self back at 3.4e38 where a row has fewer than C others.
+// The survivors of one block for their rows' own buffers: each distance
+// recomputed exactly from fresh LDS reads and appended to its row's buffer.
+// Called by the lanes whose screen passed, once the wave's ballot has shown
+// that some did.
+template <int METRIC>
+__device__ __forceinline__ void append_own(const f32x16& v, int rbase, int64_t r0, int64_t c,
+                                           float cn, float sc, const float* rs, const float* thr,
+                                           const float* rnorm, int* cnt, const MfmaSweepArgs& a,
+                                           int split, int nterm_scale, const f32x16* vx,
+                                           int* needf) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 t4 = *reinterpret_cast<const float4*>(thr + rbase + g * 8);
+        const float4 r4 = METRIC == SWANN_METRIC_L2
+                              ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 s4 = nterm_scale ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                      : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = g * 4 + q;
+            float dot;
+            if (nterm_scale == 1)
+                dot = s4[q] * sc * (v[e] + (*vx)[e] * (1.0f / 2048.0f));
+            else if (nterm_scale == 2)
+                dot = s4[q] * sc * v[e];
+            else
+                dot = v[e];
+            const float d = dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? r4[q] : 0.f, cn);
+            if (!(d < t4[q])) continue;
+            const int rl = rbase + g * 8 + q;
+            const int p = atomicAdd(&cnt[rl], 1);
+            // the append that leaves less than a tile of room flags a compaction
+            if (needf && p == a.cap - kBN2) *needf = 1;
+            const int64_t o = ((r0 + rl) * a.splits + split) * (int64_t)a.cap + p;
+            a.bkey[o] = d;
+            a.bid[o] = (int32_t)c;
+        }
+    }
+}
+
 template <int METRIC>
 __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64_t r0, int64_t c,
                                                bool cok, float cn, float sc, const float* rs,
@@ -276,23 +317,8 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
     if (__ballot(any) == 0ull) return;
     asm volatile("" ::: "memory");           // rare path: reload rather than keep live
     if (!any) return;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        float4 t4, r4, s4;
-        group(g, t4, r4, s4);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float d = dist(g * 4 + q, r4, s4);
-            if (!(d < t4[q])) continue;
-            const int rl = rbase + g * 8 + q;
-            const int p = atomicAdd(&cnt[rl], 1);
-            // the append that leaves less than a tile of room flags a compaction
-            if (needf && p == a.cap - kBN2) *needf = 1;
-            const int64_t o = ((r0 + rl) * a.splits + split) * (int64_t)a.cap + p;
-            a.bkey[o] = d;
-            a.bid[o] = (int32_t)c;
-        }
-    }
+    append_own<METRIC>(v, rbase, r0, c, cn, sc, rs, thr, rnorm, cnt, a, split, nterm_scale, vx,
+                       needf);
 }
 
 // The foreign half of a tile's epilogue in the symmetric sweep: the same 32 x
@@ -300,36 +326,15 @@ __device__ __forceinline__ void epilogue_block(const f32x16& v, int rbase, int64
 // of the column panel, whose threshold `thc` came from the last merge -- and
 // its 16 candidates rbase + (e/4)*8 + (e%4) of the row panel.  Row c's
 // distance to candidate r is the reference formula with the roles swapped
-// (na = |c|^2, nb = |r|^2), from the same score.  A screen in score space
-// (as screen_thr) rejects most blocks with one compare per score; survivors
-// take a slot of row c's second list from its global counter.  Candidates
-// past n are copies of row n - 1 (the panel loads clamp) and are skipped.
+// (na = |c|^2, nb = |r|^2), from the same score.  Survivors of the screen
+// (screen_pair) take a slot of row c's second list from its global counter.
+// Candidates past n are copies of row n - 1 (the panel loads clamp) and are
+// skipped.
 template <int METRIC>
-__device__ __forceinline__ void epilogue_foreign(const f32x16& v, int rbase, int64_t r0,
-                                                 int64_t c, bool cok, float cn, float sc,
-                                                 float thc, const float* rs, const float* rnorm,
-                                                 const MfmaSweepArgs& a, int scaled) {
-    const float h = screen_thr<METRIC>(thc, cn);
-    bool any = false;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
-                                 : make_float4(1.f, 1.f, 1.f, 1.f);
-        const float4 r4 = METRIC == SWANN_METRIC_L2
-                              ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
-            any = any || (METRIC == SWANN_METRIC_IP
-                              ? dot > h
-                              : dot > h + 0.5f * (r4[q] - 1e-5f * fabsf(r4[q])));
-        }
-    }
-    any = any && cok;
-    if (__ballot(any) == 0ull) return;
-    asm volatile("" ::: "memory");
-    if (!any) return;
+__device__ __forceinline__ void append_foreign(const f32x16& v, int rbase, int64_t r0,
+                                               int64_t c, float cn, float sc, float thc,
+                                               const float* rs, const float* rnorm,
+                                               const MfmaSweepArgs& a, int scaled) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
@@ -353,6 +358,96 @@ __device__ __forceinline__ void epilogue_foreign(const f32x16& v, int rbase, int
             }
         }
     }
+}
+
+// Foreign survivors queued in LDS instead of taking their global slots at
+// once: a slot is a returning atomic on row c's counter, and a wave that
+// waits for it (vmcnt) stalls for a memory round trip per survivor.  The
+// queue (column and row within the tile, distance) is drained at the next
+// column tile's first stage, where each thread takes one entry's slot with
+// an atomic whose return is waited for by that stage's own barrier, and the
+// entries are stored at the second stage.  A full queue takes the direct
+// path.
+constexpr int kFQueue = 1024;
+
+template <int METRIC>
+__device__ __forceinline__ void queue_foreign(const f32x16& v, int rbase, int64_t r0, int64_t c,
+                                              int cl, float cn, float sc, float thc,
+                                              const float* rs, const float* rnorm,
+                                              const MfmaSweepArgs& a, int scaled, int* qn,
+                                              int2* qe) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                 : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 r4 = METRIC == SWANN_METRIC_L2
+                              ? *reinterpret_cast<const float4*>(rnorm + rbase + g * 8)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+            const float d = dist_formula<METRIC>(dot, cn, r4[q]);
+            const int rl = rbase + g * 8 + q;
+            if (!(d < thc) || r0 + rl >= a.n) continue;
+            const int k = atomicAdd(qn, 1);
+            if (k < kFQueue) {
+                qe[k] = make_int2((cl << 16) | rl, __float_as_int(d));
+            } else {
+                const int p = atomicAdd(&a.bcnt[c * 2 + 1], 1);
+                if (p < a.fcap) {
+                    const int64_t o = (c * 2 + 1) * (int64_t)a.cap + p;
+                    a.bkey[o] = d;
+                    a.bid[o] = (int32_t)(r0 + rl);
+                } else {
+                    atomicAdd(a.ovf, 1);
+                }
+            }
+        }
+    }
+}
+
+// Both screens of a block of the DMA sweep in one pass, as wave masks: each
+// score is scaled once, then tested for its row's own buffer and, when `fon`
+// (the symmetric sweep off the diagonal), for its column's foreign list.
+// The tests are in score space, one compare each after at most one add: the
+// row's own threshold sthr (screen_thr) plus, for l2, the column's half-norm
+// term ch; the column's threshold h (screen_thr of thc) plus, for l2, the
+// row's half-norm term fr = (|r|^2 - 1e-5 ||r|^2|) / 2.  Each compare goes
+// straight into a 64-bit lane mask (a ballot), so the "any" costs no VALU.
+// Both keep at least what the exact tests of the append paths keep.
+template <int METRIC, int SCALED>
+__device__ __forceinline__ void screen_pair(const f32x16& v, int rbase, float cn, float sc,
+                                            float thc, bool fon, const float* rs,
+                                            const float* sthr, const float* fr, uint64_t& own,
+                                            uint64_t& frn) {
+    const float ch = METRIC == SWANN_METRIC_L2 ? 0.5f * (cn - 1e-5f * fabsf(cn)) : 0.f;
+    const float h = screen_thr<METRIC>(thc, cn);
+    uint64_t o = 0, f = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 s4 = SCALED ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
+                                 : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 t4 = *reinterpret_cast<const float4*>(sthr + rbase + g * 8);
+        if (fon) {
+            const float4 f4 = METRIC == SWANN_METRIC_L2
+                                  ? *reinterpret_cast<const float4*>(fr + rbase + g * 8)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float dot = SCALED ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+                o |= __ballot(METRIC == SWANN_METRIC_L2 ? dot > ch + t4[q] : dot > t4[q]);
+                f |= __ballot(METRIC == SWANN_METRIC_L2 ? dot > h + f4[q] : dot > h);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float dot = SCALED ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+                o |= __ballot(METRIC == SWANN_METRIC_L2 ? dot > ch + t4[q] : dot > t4[q]);
+            }
+        }
+    }
+    own = o;
+    frn = f;
 }
 
 // On the diagonal tile, the score of each row against itself becomes -inf
@@ -595,10 +690,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     __shared__ __align__(16) unsigned char sA[2][kStage];
     __shared__ __align__(16) unsigned char sB[2][kStage];
     __shared__ __align__(16) float thr[kBM2];
-    // thr in score space (screen_thr), for l2 only: there it saves the
-    // distance formula's four operations per score; ip's formula is one
-    // subtraction and the screen measured no faster
+    // thr in score space (screen_thr), kept beside thr: the screens compare
+    // scores with it, and only survivors evaluate the distance formula
     __shared__ __align__(16) float sthr[kBM2];
+    __shared__ __align__(16) float frow[kBM2];   // l2: the foreign screen's row term
     __shared__ int cnt[kBM2];
     __shared__ __align__(16) float rnorm[kBM2];
     __shared__ __align__(16) float rscale[kBM2];
@@ -606,75 +701,77 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     // symmetric sweep: the current column tile's rows' thresholds (from the
     // last merge, fixed for the launch), for the foreign half of its epilogue
     __shared__ __align__(16) float thrc[kBN2];
+    // symmetric sweep: foreign survivors waiting for their slots (queue_foreign)
+    __shared__ int fqn;
+    __shared__ int2 fq[kFQueue];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;          // rows wm*RW.., cols wn*CW..
-    const int64_t n = a.n;
+    // Row and tile indices are 32-bit (the entry point bounds n by
+    // INT32_MAX / 2); only addresses are formed in 64 bits.  Held in 64-bit
+    // scalar pairs they overflowed the SGPRs into VGPR lanes.
+    const int n = (int)a.n;
     const int dim = a.dim;
-    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    const int ntile = (n + kBM2 - 1) / kBM2;
     // G workgroups share a row panel, each taking 1/G of the column tiles;
     // xcd_remap gives consecutive logical ids to one XCD, so the G readers of
     // a panel run together on one L2
     const int G = a.splits;
     // symmetric sweep: one workgroup per row panel, which keeps list 0 of
     // its rows and starts from the thresholds and lists the last merge left
-    const int64_t lid = xcd_remap(blockIdx.x, a.sym ? (int64_t)gridDim.x : ntile * G);
-    const int64_t r0 = (a.sym ? lid : lid / G) * kBM2;
-    const int split = a.sym ? 0 : (int)(lid % G);
+    const int lid = (int)xcd_remap(blockIdx.x, a.sym ? (int64_t)gridDim.x : (int64_t)ntile * G);
+    const int r0 = (a.sym ? lid : lid / G) * kBM2;
+    const int split = a.sym ? 0 : lid % G;
 
     if (tid < kBM2) {
         thr[tid] = r0 + tid >= n ? -INFINITY : a.sym ? a.gthr[r0 + tid] : INFINITY;
-        cnt[tid] = (a.sym && r0 + tid < n) ? a.bcnt[(r0 + tid) * 2] : 0;
+        cnt[tid] = (a.sym && r0 + tid < n) ? a.bcnt[(int64_t)(r0 + tid) * 2] : 0;
         rnorm[tid] = (r0 + tid < n) ? a.xn[r0 + tid] : 0.f;
         if (SCALED) rscale[tid] = (r0 + tid < n) ? a.scale[r0 + tid] : 1.f;
-        if (METRIC == SWANN_METRIC_L2) sthr[tid] = screen_thr<METRIC>(thr[tid], rnorm[tid]);
+        sthr[tid] = screen_thr<METRIC>(thr[tid], rnorm[tid]);
+        if (METRIC == SWANN_METRIC_L2) frow[tid] = 0.5f * (rnorm[tid] - 1e-5f * fabsf(rnorm[tid]));
     }
     if (tid < 2) need[tid] = 0;
+    if (tid == 0) fqn = 0;
 
     // direct-load assignment: instruction j of this wave fills rows
     // 8 (NQ wave + j) .. + 7 of the stage; this lane fetches one 16-byte
-    // chunk, at byte offset voff from the stage's first row (rows past n
-    // read row n - 1: clamped for the panel here, for a column tile at issue)
-    const int64_t rowb = (int64_t)dim * 2;
-    uint32_t voffA[NQ], voffB[NQ];
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-        const int lrow = (wave * NQ + j) * 8 + (lane >> 3);
-        const int lchunk = ((lane & 7) ^ swz(lrow)) * 8;
-        const int64_t ra = r0 + lrow < n ? lrow : n - 1 - r0;
-        voffA[j] = (uint32_t)(ra * rowb + lchunk * 2);
-        voffB[j] = (uint32_t)(lrow * rowb + lchunk * 2);
-    }
+    // chunk, at byte offset lrow * rowb + chunk from the stage's first row
+    // (rows past n read row n - 1: the panel and the last column tile clamp)
+    const uint32_t rowb = (uint32_t)dim * 2;
     const int nk = dim / kBK3;
-    const int64_t nct = (n + kBN2 - 1) / kBN2;
-    int64_t ct0 = nct * split / G, ct1 = nct * (split + 1) / G;
+    const int nct = (n + kBN2 - 1) / kBN2;
+    int ct0 = (int)((int64_t)nct * split / G), ct1 = (int)((int64_t)nct * (split + 1) / G);
     if (a.sym) {
-        ct0 = lid + a.b0;
-        ct1 = lid + a.b1 < nct ? lid + a.b1 : nct;
+        ct0 = lid + (int)a.b0;
+        ct1 = lid + a.b1 < nct ? lid + (int)a.b1 : nct;
     }
-    const int64_t nsteps = (ct1 - ct0) * nk;
+    const int nsteps = (ct1 - ct0) * nk;
     const _Float16* X = a.hi;
 
-    auto issue = [&](int64_t t, int kt, int64_t cb) {
+    auto issue = [&](int t, int kt, int cb) {
         if (t >= nsteps) return;
-        const int buf = (int)(t & 1);
+        const int buf = t & 1;
         const int k0 = kt * kBK3;
-        const _Float16* ba = X + r0 * dim + k0;
-        const _Float16* bb = X + cb * dim + k0;
-        const bool part = cb + kBN2 > n;           // the last, partial column tile
+        const _Float16* ba = X + (int64_t)r0 * dim + k0;
+        const _Float16* bb = X + (int64_t)cb * dim + k0;
+        // The lane offsets are recomputed at every issue (a few VALU) rather
+        // than held across the loop: held, they are the first registers the
+        // allocator spills, and each reload's wait (vmcnt counts scratch
+        // loads and direct loads alike) then waited for the direct load
+        // issued just before it, a memory latency per instruction.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int j = 0; j < NQ; ++j) {
             const int q = wave * NQ + j;
-            dma16(ba, voffA[j], &sA[buf][q * 1024]);
-            uint32_t vb = voffB[j];
-            if (part) {
-                const int lrow = (wave * NQ + j) * 8 + (lane >> 3);
-                const int lchunk = ((lane & 7) ^ swz(lrow)) * 8;
-                const int64_t rb = cb + lrow < n ? lrow : n - 1 - cb;
-                vb = (uint32_t)(rb * rowb + lchunk * 2);
-            }
-            dma16(bb, vb, &sB[buf][q * 1024]);
+            const int lrow = q * 8 + (ln >> 3);
+            const uint32_t lb = (uint32_t)(((ln & 7) ^ swz(lrow)) * 16);
+            const uint32_t ra = r0 + lrow < n ? (uint32_t)lrow : (uint32_t)(n - 1 - r0);
+            const uint32_t rb = cb + lrow < n ? (uint32_t)lrow : (uint32_t)(n - 1 - cb);
+            dma16(ba, ra * rowb + lb, &sA[buf][q * 1024]);
+            dma16(bb, rb * rowb + lb, &sB[buf][q * 1024]);
         }
     };
 
@@ -688,21 +785,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     for (int j = 0; j < BJ; ++j) bro[j] = (wn * CW + j * 32 + (lane & 31)) * kRowBytes;
 
     int kt_c = 0, kt_f = 0;
-    int64_t cb_c = ct0 * kBN2, cb_f = ct0 * kBN2;
-    auto adv = [&](int& kt, int64_t& cb) {
+    int cb_c = ct0 * kBN2, cb_f = ct0 * kBN2;
+    auto adv = [&](int& kt, int& cb) {
         if (++kt == nk) { kt = 0; cb += kBN2; }
     };
     f32x16 acc[BI][BJ];
     float thr_next = INFINITY;       // symmetric sweep: this thread's column threshold in flight
+    // the foreign queue: staged when a tile has at least three stages, so
+    // that its drain (first stage) and stores (second) come before the next
+    // epilogue (last stage) refills it
+    const bool fstage = a.sym && nk >= 3;
+    int fslot = 0, fqd = 0;          // this thread's drained entry: its slot; entries drained
+    int cb_prev = 0;                 // column base of the tile whose entries are queued
     int tpar = 0;                    // parity of the current column tile (its need flag)
     issue(0, kt_f, cb_f);
     adv(kt_f, cb_f);
 
-    for (int64_t t = 0; t < nsteps; ++t) {
+    for (int t = 0; t < nsteps; ++t) {
         const int kt = kt_c;
-        const int64_t cbt = cb_c;
+        const int cbt = cb_c;
         adv(kt_c, cb_c);
-        const int buf = (int)(t & 1);
+        const int buf = t & 1;
         // column norms/scales of a finishing tile, issued before the next
         // stage's loads so the epilogue's wait does not include them
         float cn[BJ], cs[BJ];
@@ -711,13 +814,41 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         if (kt == nk - 1) {
 #pragma unroll
             for (int j = 0; j < BJ; ++j) {
-                const int64_t c = cbt + wn * CW + j * 32 + (lane & 31);
+                const int c = cbt + wn * CW + j * 32 + (lane & 31);
                 if (METRIC == SWANN_METRIC_L2) cn[j] = c < n ? a.xn[c] : 0.f;
                 if (SCALED) cs[j] = c < n ? a.scale[c] : 1.f;
             }
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's stage-t loads
         __syncthreads();                                // every wave's stage-t loads have landed
+        // the column thresholds loaded at the tile's first stage go to LDS
+        // here, before the next stage's loads are issued: the store waits for
+        // its load with vmcnt(0), which would otherwise wait for those too
+        if (kt == 1 && nk > 2 && a.sym && cbt != r0 && tid < kBN2) thrc[tid] = thr_next;
+        if (fstage && kt == 0) {
+            // take the slots of the last tile's queued foreign survivors; the
+            // returns are waited for by the next stage's barrier
+            fqd = fqn < kFQueue ? fqn : kFQueue;
+            if (tid < fqd) {
+                const int2 e = fq[tid];
+                fslot = atomicAdd(&a.bcnt[(int64_t)(cb_prev + (e.x >> 16)) * 2 + 1], 1);
+            }
+        }
+        if (fstage && kt == 1) {
+            if (tid < fqd) {
+                const int2 e = fq[tid];
+                const int64_t c = cb_prev + (e.x >> 16);
+                if (fslot < a.fcap) {
+                    const int64_t o = (c * 2 + 1) * (int64_t)a.cap + fslot;
+                    a.bkey[o] = __int_as_float(e.y);
+                    a.bid[o] = (int32_t)(r0 + (e.x & 0xffff));
+                } else {
+                    atomicAdd(a.ovf, 1);
+                }
+            }
+            if (tid == 0) fqn = 0;      // the next refill is after the next barrier
+            fqd = 0;
+        }
         issue(t + 1, kt_f, cb_f);
         adv(kt_f, cb_f);
         if (kt == 0) {
@@ -736,8 +867,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                         compact_row_w(a.bkey + (r * G + split) * a.cap,
                                       a.bid + (r * G + split) * a.cap, cnt[rl], a.C, &thr[rl],
                                       &cnt[rl]);
-                        if (METRIC == SWANN_METRIC_L2 && lane == 0)
-                            sthr[rl] = screen_thr<METRIC>(thr[rl], rnorm[rl]);
+                        if (lane == 0) sthr[rl] = screen_thr<METRIC>(thr[rl], rnorm[rl]);
                     }
                 }
                 // let the compaction's stores finish here: left pending, the
@@ -754,8 +884,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
 #pragma unroll
                 for (int j = 0; j < BJ; ++j) acc[i][j] = (f32x16){};
             // the new tile's column thresholds: loaded now, stored into LDS
-            // after the next stage's barrier (the load lands under this
-            // stage's MFMAs and the kernel's vmcnt(0) wait) and read by the
+            // just after the next stage's barrier (the load lands under this
+            // stage's MFMAs and that barrier's vmcnt(0) wait) and read by the
             // tile's epilogue stages later; every wave finished the last
             // tile's epilogue before this stage's barrier.  A tile of one or
             // two stages stores at once, behind a barrier of its own.
@@ -766,7 +896,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                 __syncthreads();
             }
         }
-        if (kt == 1 && nk > 2 && a.sym && cbt != r0 && tid < kBN2) thrc[tid] = thr_next;
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
         f16x8 fa[2][BI], fb[2][BJ];
@@ -796,33 +925,66 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         __builtin_amdgcn_iglp_opt(1);
         if (kt == nk - 1) {
             // ---- epilogue of this column tile: distance, threshold, append ----
-            const int64_t cb = cbt;
+            const int cb = cbt;
             const bool diag = (cb == r0);
 #pragma unroll
             for (int j = 0; j < BJ; ++j) {
-                const int64_t c = cb + wn * CW + j * 32 + (lane & 31);
+                const int c = cb + wn * CW + j * 32 + (lane & 31);
                 const bool cok = c < n;
 #pragma unroll
                 for (int i = 0; i < BI; ++i) {
                     int rbase = wm * RW + i * 32 + (lane >> 5) * 4;
                     asm volatile("" : "+v"(rbase));
                     if (diag) self_out(acc[i][j], rbase, wn * CW + j * 32 + (lane & 31));
-                    epilogue_block<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j], rscale,
-                                           thr, rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
-                                           &need[tpar],
-                                           METRIC == SWANN_METRIC_L2 ? sthr : nullptr);
-                    if (a.sym && !diag)
-                        epilogue_foreign<METRIC>(acc[i][j], rbase, r0, c, cok, cn[j], cs[j],
-                                                 thrc[wn * CW + j * 32 + (lane & 31)], rscale,
-                                                 rnorm, a, SCALED);
+                    const bool fon = a.sym && !diag;
+                    const float thc = fon ? thrc[wn * CW + j * 32 + (lane & 31)] : 0.f;
+                    uint64_t own, frn;
+                    screen_pair<METRIC, SCALED>(acc[i][j], rbase, cn[j], cs[j], thc, fon, rscale,
+                                                sthr, frow, own, frn);
+                    // the append paths test every score exactly, so once any
+                    // lane passed a screen the whole wave runs them
+                    const uint64_t valid = __ballot(cok);
+                    if (own & valid) {
+                        asm volatile("" ::: "memory");   // rare path: reload, do not keep live
+                        if (cok)
+                            append_own<METRIC>(acc[i][j], rbase, r0, c, cn[j], cs[j], rscale, thr,
+                                               rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
+                                               &need[tpar]);
+                    }
+                    if (frn & valid) {
+                        asm volatile("" ::: "memory");
+                        if (cok && fstage)
+                            queue_foreign<METRIC>(acc[i][j], rbase, r0, c, c - cb, cn[j], cs[j],
+                                                  thc, rscale, rnorm, a, SCALED, &fqn, fq);
+                        else if (cok)
+                            append_foreign<METRIC>(acc[i][j], rbase, r0, c, cn[j], cs[j], thc,
+                                                   rscale, rnorm, a, SCALED);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
             tpar ^= 1;
+            cb_prev = cb;
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    if (fstage) {
+        // the last tile's queue: slots, then stores
+        const int nq = fqn < kFQueue ? fqn : kFQueue;
+        for (int k = tid; k < nq; k += WAVES * 64) {
+            const int2 e = fq[k];
+            const int64_t c = cb_prev + (e.x >> 16);
+            const int p = atomicAdd(&a.bcnt[c * 2 + 1], 1);
+            if (p < a.fcap) {
+                const int64_t o = (c * 2 + 1) * (int64_t)a.cap + p;
+                a.bkey[o] = __int_as_float(e.y);
+                a.bid[o] = (int32_t)(r0 + (e.x & 0xffff));
+            } else {
+                atomicAdd(a.ovf, 1);
+            }
+        }
+    }
     if (G > 1 && !a.sym) {
         // each split leaves at most C per row, so the merge of the G lists
         // sorts at most G * C
@@ -834,7 +996,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         }
         __syncthreads();
     }
-    if (tid < kBM2 && r0 + tid < n) a.bcnt[(r0 + tid) * G + split] = cnt[tid];
+    if (tid < kBM2 && r0 + tid < n) a.bcnt[(int64_t)(r0 + tid) * G + split] = cnt[tid];
 }
 
 // ---------------------------------------------------------------------------
