@@ -232,7 +232,7 @@ __device__ __forceinline__ void append_own(const f32x16& v, int rbase, int64_t r
                                            float cn, float sc, const float* rs, const float* thr,
                                            const float* rnorm, int* cnt, const MfmaSweepArgs& a,
                                            int split, int nterm_scale, const f32x16* vx,
-                                           int* needf) {
+                                           int* needf, bool cok = true) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const float4 t4 = *reinterpret_cast<const float4*>(thr + rbase + g * 8);
@@ -251,6 +251,7 @@ __device__ __forceinline__ void append_own(const f32x16& v, int rbase, int64_t r
                 dot = s4[q] * sc * v[e];
             else
                 dot = v[e];
+            if (!cok) continue;
             const float d = dist_formula<METRIC>(dot, METRIC == SWANN_METRIC_L2 ? r4[q] : 0.f, cn);
             if (!(d < t4[q])) continue;
             const int rl = rbase + g * 8 + q;
@@ -334,7 +335,7 @@ template <int METRIC>
 __device__ __forceinline__ void append_foreign(const f32x16& v, int rbase, int64_t r0,
                                                int64_t c, float cn, float sc, float thc,
                                                const float* rs, const float* rnorm,
-                                               const MfmaSweepArgs& a, int scaled) {
+                                               const MfmaSweepArgs& a, int scaled, bool cok) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
@@ -345,6 +346,7 @@ __device__ __forceinline__ void append_foreign(const f32x16& v, int rbase, int64
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+            if (!cok) continue;
             const float d = dist_formula<METRIC>(dot, cn, r4[q]);
             const int64_t r = r0 + rbase + g * 8 + q;
             if (!(d < thc) || r >= a.n) continue;
@@ -375,7 +377,7 @@ __device__ __forceinline__ void queue_foreign(const f32x16& v, int rbase, int64_
                                               int cl, float cn, float sc, float thc,
                                               const float* rs, const float* rnorm,
                                               const MfmaSweepArgs& a, int scaled, int* qn,
-                                              int2* qe) {
+                                              int2* qe, bool cok) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const float4 s4 = scaled ? *reinterpret_cast<const float4*>(rs + rbase + g * 8)
@@ -386,6 +388,7 @@ __device__ __forceinline__ void queue_foreign(const f32x16& v, int rbase, int64_
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float dot = scaled ? s4[q] * sc * v[g * 4 + q] : v[g * 4 + q];
+            if (!cok) continue;
             const float d = dist_formula<METRIC>(dot, cn, r4[q]);
             const int rl = rbase + g * 8 + q;
             if (!(d < thc) || r0 + rl >= a.n) continue;
@@ -668,11 +671,23 @@ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // (they alternate at run time), and would make every fragment read wait for
 // the loads in flight.  The kernel waits for them itself: vmcnt(0) and a
 // barrier before a stage is read.  m0 carries the LDS address: an input
-// operand, so the compiler writes m0 and knows it holds this value; the
-// s_nop is the one wait state the load needs after that write.
+// operand, so the compiler writes m0 and knows it holds this value.
+// The compiler does not see into the assembly, so it does not pad the
+// hazards of its operands: a VMEM instruction that reads an SGPR a VALU
+// instruction wrote (v_readlane restoring a spilled base) needs 5 wait
+// states, and one that reads m0 after an SALU write 1.  The s_nop 4 gives
+// both: with one wait state only, a base restored by v_readlane the
+// instruction before was read stale, and the load went to a wild address.
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, unsigned char* lds) {
     const unsigned m = (unsigned)(uintptr_t)(lds_vptr)lds;
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(base), "{m0}"(m) : "memory");
+}
+
+// The same for 4 bytes a lane: lane i's word lands at lds + 4 i.
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, unsigned char* lds) {
+    const unsigned m = (unsigned)(uintptr_t)(lds_vptr)lds;
+    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
                  :: "v"(voff), "s"(base), "{m0}"(m) : "memory");
 }
 
@@ -790,7 +805,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         if (++kt == nk) { kt = 0; cb += kBN2; }
     };
     f32x16 acc[BI][BJ];
-    float thr_next = INFINITY;       // symmetric sweep: this thread's column threshold in flight
     // the foreign queue: staged when a tile has at least three stages, so
     // that its drain (first stage) and stores (second) come before the next
     // epilogue (last stage) refills it
@@ -821,10 +835,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's stage-t loads
         __syncthreads();                                // every wave's stage-t loads have landed
-        // the column thresholds loaded at the tile's first stage go to LDS
-        // here, before the next stage's loads are issued: the store waits for
-        // its load with vmcnt(0), which would otherwise wait for those too
-        if (kt == 1 && nk > 2 && a.sym && cbt != r0 && tid < kBN2) thrc[tid] = thr_next;
+        // Everything a stage does before its MFMAs that may wait on memory
+        // (the queue's slot atomics, the compaction, the column thresholds)
+        // comes before the next stage's direct loads are issued, so that no
+        // wait of its own -- the compiler's vmcnt for a spill or a load --
+        // also waits for those.
         if (fstage && kt == 0) {
             // take the slots of the last tile's queued foreign survivors; the
             // returns are waited for by the next stage's barrier
@@ -849,8 +864,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             if (tid == 0) fqn = 0;      // the next refill is after the next barrier
             fqd = 0;
         }
-        issue(t + 1, kt_f, cb_f);
-        adv(kt_f, cb_f);
         if (kt == 0) {
           if (t > 0) {
             // compaction flagged by the previous column tile's appends; the
@@ -883,19 +896,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             for (int i = 0; i < BI; ++i)
 #pragma unroll
                 for (int j = 0; j < BJ; ++j) acc[i][j] = (f32x16){};
-            // the new tile's column thresholds: loaded now, stored into LDS
-            // just after the next stage's barrier (the load lands under this
-            // stage's MFMAs and that barrier's vmcnt(0) wait) and read by the
-            // tile's epilogue stages later; every wave finished the last
-            // tile's epilogue before this stage's barrier.  A tile of one or
-            // two stages stores at once, behind a barrier of its own.
-            if (a.sym && cbt != r0 && tid < kBN2)
-                thr_next = cbt + tid < n ? a.gthr[cbt + tid] : INFINITY;
-            if (a.sym && cbt != r0 && nk <= 2) {
-                if (tid < kBN2) thrc[tid] = thr_next;
-                __syncthreads();
+            // the new tile's column thresholds, straight into LDS by a
+            // direct load (no register held, no wait here): the next stage's
+            // barrier waits for it, and the tile's epilogue, at its last
+            // stage, reads it; every wave finished the last tile's epilogue
+            // before this stage's barrier.  Columns past n read row n - 1's
+            // (their scores are never appended).  A one-stage tile waits at
+            // once.
+            if (a.sym && cbt != r0) {
+                if (tid < kBN2) {
+                    const int ci = cbt + tid < n ? cbt + tid : n - 1;
+                    dma4(a.gthr, (uint32_t)ci * 4u,
+                         reinterpret_cast<unsigned char*>(thrc) + wave * 256);
+                }
+                if (nk == 1) {
+                    __builtin_amdgcn_s_waitcnt(0x0F70);
+                    __syncthreads();
+                }
             }
         }
+        issue(t + 1, kt_f, cb_f);
+        adv(kt_f, cb_f);
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
         f16x8 fa[2][BI], fb[2][BJ];
@@ -946,19 +967,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                     const uint64_t valid = __ballot(cok);
                     if (own & valid) {
                         asm volatile("" ::: "memory");   // rare path: reload, do not keep live
-                        if (cok)
-                            append_own<METRIC>(acc[i][j], rbase, r0, c, cn[j], cs[j], rscale, thr,
-                                               rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
-                                               &need[tpar]);
+                        append_own<METRIC>(acc[i][j], rbase, r0, c, cn[j], cs[j], rscale, thr,
+                                           rnorm, cnt, a, split, SCALED ? 2 : 0, nullptr,
+                                           &need[tpar], cok);
                     }
                     if (frn & valid) {
                         asm volatile("" ::: "memory");
-                        if (cok && fstage)
+                        if (fstage)
                             queue_foreign<METRIC>(acc[i][j], rbase, r0, c, c - cb, cn[j], cs[j],
-                                                  thc, rscale, rnorm, a, SCALED, &fqn, fq);
-                        else if (cok)
+                                                  thc, rscale, rnorm, a, SCALED, &fqn, fq, cok);
+                        else
                             append_foreign<METRIC>(acc[i][j], rbase, r0, c, cn[j], cs[j], thc,
-                                                   rscale, rnorm, a, SCALED);
+                                                   rscale, rnorm, a, SCALED, cok);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }

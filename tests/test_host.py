@@ -163,3 +163,54 @@ def test_swann_is_the_drop_in_name():
     from swann.index import Index
     assert E2 is E and Index is swann_amd.Index
     assert E2.cache_size(32, 64, 64) == 131072
+
+
+def test_direct_loads_are_padded_for_their_sgpr_operands(tmp_path):
+    """The sweep's direct global->LDS loads are inline assembly, whose
+    operands the compiler's hazard padding does not see.  A base address
+    restored into SGPRs by v_readlane (a VALU write) must be 5 wait states
+    old when a VMEM instruction reads it; with one, the load read a stale
+    base and faulted.  Compile the sweep for gfx950 and check every direct
+    load for a VALU write of its base within the last 5 wait states."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    src = ROOT / "swann_amd" / "csrc" / "sweep_mfma.hip"
+    out = tmp_path / "sweep.s"
+    subprocess.run([hipcc, "-O3", "-std=c++17", "--offload-arch=gfx950", "--cuda-device-only",
+                    "-S", "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", f"-I{ROOT / 'include'}",
+                    f"-I{ROOT / 'swann_amd' / 'csrc'}", str(src), "-o", str(out)],
+                   check=True, capture_output=True)
+
+    def sregs(tok):
+        m = re.match(r"s\[(\d+):(\d+)\]", tok)
+        if m:
+            return set(range(int(m.group(1)), int(m.group(2)) + 1))
+        m = re.match(r"s(\d+)$", tok)
+        return {int(m.group(1))} if m else set()
+
+    lines = [ln.strip() for ln in out.read_text().splitlines()]
+    loads, hazards = 0, []
+    for i, ln in enumerate(lines):
+        if not ln.startswith("global_load_lds"):
+            continue
+        loads += 1
+        base = sregs(ln.split(",")[-1].strip())
+        waits, j = 0, i - 1
+        while j >= 0 and waits < 5:
+            t = lines[j]
+            j -= 1
+            if not t or t.startswith((";", ".")) or t.endswith(":"):
+                continue
+            op = t.split()[0]
+            if op == "s_nop":
+                waits += int(t.split()[1], 0) + 1
+                continue
+            if op.startswith("v_") and len(t.split()) > 1 and sregs(t.split()[1].rstrip(",")) & base:
+                hazards.append((i, t, ln))
+            waits += 1
+    assert loads > 0
+    assert not hazards, hazards[:3]
