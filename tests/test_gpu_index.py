@@ -62,8 +62,11 @@ def test_round_trip(tmp_path):
     again = swann.Index.load(tmp_path / "ix", X)
     assert torch.equal(again.G, index.G) and torch.equal(again.catalogue, index.catalogue)
     after, _ = again.search(Q, k=10)
-    # claims and the bound are racy: the answers agree, up to rare reorders
+    # claims and the bound are racy: the answers agree, up to rare reorders,
+    # and find the same share of the true neighbours
     assert (before == after).mean() > 0.99
+    truth = exact_topk(X, Q, 10)
+    assert abs(recall(before, truth, 10) - recall(after, truth, 10)) <= 0.005
 
 
 def test_batch_beyond_65535_is_served():
@@ -338,16 +341,17 @@ def test_captured_search_replays_exactly():
 
 
 def test_index_capture_matches_eager_search():
-    """`Index.capture`: the production configuration (shared table, bound,
-    claims -- racy by design) replayed on several batches agrees with the
-    eager search, and its distances are exact."""
-    X, Q = corpus(n=6000, d=96, nq=64, seed=5)
+    """`Index.capture`: the production configuration (claims, bound -- racy
+    by design) replayed on 64 batches agrees with the eager search on the same
+    batches (recall within 0.005 over 1,024 queries), and its distances are
+    exact."""
+    X, Q = corpus(n=6000, d=96, nq=1024, seed=5)
     index = swann.Index.build(X, degree=32, candidates=48)
     cs = index.capture(16, k=10, branches=16, queue=16)
     Xd = X.astype(np.float64)
     truth = exact_topk(X, Q, 10)
     agree, rg, re = [], [], []
-    for rep in range(4):
+    for rep in range(Q.shape[0] // 16):
         sl = slice(rep * 16, (rep + 1) * 16)
         ei, _ = index.search(Q[sl], k=10, branches=16, queue=16)
         gi, gd = cs.run(Q[sl])
@@ -356,13 +360,15 @@ def test_index_capture_matches_eager_search():
         agree.append(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(gi, ei)]))
         rg.append(recall(gi, truth[sl], 10)); re.append(recall(ei, truth[sl], 10))
         assert int(cs.overflow) == 0
-        for qi in range(16):
-            for i, dv in zip(gi[qi], gd[qi]):
-                if i >= 0:
-                    assert abs(dv - (1.0 - Q[rep * 16 + qi].astype(np.float64) @ Xd[i])) < 1e-5
-    note("capture set agreement / recall graph / recall eager", agree, np.mean(rg), np.mean(re))
+        if rep < 4:
+            for qi in range(16):
+                for i, dv in zip(gi[qi], gd[qi]):
+                    if i >= 0:
+                        assert abs(dv - (1.0 - Q[rep * 16 + qi].astype(np.float64) @ Xd[i])) < 1e-5
+    note("capture set agreement / recall graph / recall eager", np.mean(agree), np.mean(rg),
+         np.mean(re))
     assert np.mean(agree) > 0.95
-    assert abs(np.mean(rg) - np.mean(re)) < 0.03
+    assert abs(np.mean(rg) - np.mean(re)) <= 0.005       # 1,024 queries in 64 replays
     with pytest.raises(ValueError):
         cs.run(Q[:3])
 
