@@ -274,7 +274,10 @@ def advance(X, G, Qv, state: SearchState, delta_expansions: int, active=None,
     Q, J, L = state.ids.shape
     H = state.visited.shape[-1]
     Hc = state.table_slots
-    if Hc and codes is not None and state.cache_d.numel() == 0:
+    if not Hc and state.cache_id is not None and state.cache_id.numel() \
+            and state.cache_d is not None and state.cache_d.numel():
+        Hc = state.cache_id.shape[1]        # a state assembled by hand: the table's width
+    if Hc and codes is not None and (state.cache_d is None or state.cache_d.numel() == 0):
         raise ValueError("sign codes need the shared table: init_states(claim_bits=False)")
     nact = 0
     if active is not None:
