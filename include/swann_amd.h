@@ -245,6 +245,14 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
                         const int32_t* deg_per_node, int32_t* out, void* workspace,
                         void* stream);
 
+/* The MFMA rate the chip sustains (measurement; no counterpart in the
+ * reference): `blocks` workgroups of four waves each run `iters` rounds of four
+ * independent v_mfma_f32_32x32x16_f16 on register operands.  The caller times
+ * the launch; swann_mfma_probe_flop gives its FLOP.  `sink` is one float the
+ * kernel may write. */
+int64_t swann_mfma_probe_flop(int iters, int blocks);
+int swann_mfma_probe(int iters, int blocks, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,8 @@ LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libswann_amd.so"
 ARCH = os.environ.get("SWANN_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["api.cpp", "search.hip", "select.hip", "build.hip", "sweep_mfma.hip", "codes.hip", "offline.hip"]
+SOURCES = ["api.cpp", "search.hip", "select.hip", "build.hip", "sweep_mfma.hip", "codes.hip", "offline.hip",
+           "probe.hip"]
 
 HIPCC_FLAGS = [
     "-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",

@@ -37,6 +37,8 @@ PROTOTYPES = {
     "swann_select_workspace_size": (I64, [I64, I64]),
     "swann_select_nearest": (I, [P, I64, I, P, I64, I, I, P, P, P, P]),
     "swann_select_nearest_noalloc": (I, [P, I64, I, P, I64, I, I, P, P, P]),
+    "swann_mfma_probe_flop": (I64, [I, I]),
+    "swann_mfma_probe": (I, [I, I, P, P]),
     "swann_sweep_workspace_size": (I64, [I64, I, I, I]),
     "swann_build_sweep": (I, [P, I, I64, I, I, I, P, P, P, P]),
     "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P]),

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from conftest import gaussian, golden, regen
+from conftest import ROOT, gaussian, golden, regen
 from test_oracle_helpers import exact_topk, recall
 
 pytestmark = pytest.mark.gpu
@@ -520,3 +520,16 @@ def test_claims_fall_back_to_the_table_when_bits_do_not_fit(monkeypatch):
     assert abs(r_bits - r_table) <= 0.01
     monkeypatch.undo()
     assert small._claims(Q.shape[0], cfg) == (False, slots)      # kept once decided
+
+
+def test_mfma_probe_reports_a_rate_below_the_published_peak():
+    """The measurement probe's FLOP count is its launch's MFMA work
+    (blocks x 4 waves x iters x 4 MFMAs x 2*32*32*16), and the rate it gives
+    is positive and below the published dense fp16 peak."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from swann_amd import _lib
+    assert _lib.lib().swann_mfma_probe_flop(10, 3) == 3 * 4 * 10 * 4 * 2 * 32 * 32 * 16
+    rate = bench.mfma_probe(torch.device("cuda:0"), seconds=0.05)
+    note("mfma probe TFLOP/s", rate / 1e12)
+    assert 0.2e15 < rate < bench.MFMA_F16_PEAK
