@@ -19,6 +19,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "panel_order.h"
 
 namespace swann {
 namespace {
@@ -734,8 +735,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     // a panel run together on one L2
     const int G = a.splits;
     // symmetric sweep: one workgroup per row panel, which keeps list 0 of
-    // its rows and starts from the thresholds and lists the last merge left
-    const int lid = (int)xcd_remap(blockIdx.x, a.sym ? (int64_t)gridDim.x : (int64_t)ntile * G);
+    // its rows and starts from the thresholds and lists the last merge left;
+    // sym_panel spreads the band's short panels over the XCDs
+    const int lid = a.sym ? sym_panel((int)blockIdx.x, (int)gridDim.x, (int)(a.b1 - a.b0))
+                          : (int)xcd_remap(blockIdx.x, (int64_t)ntile * G);
     const int r0 = (a.sym ? lid : lid / G) * kBM2;
     const int split = a.sym ? 0 : lid % G;
 
@@ -1089,6 +1092,13 @@ __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
 
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
+// Widest band of the symmetric sweep.  Wider bands mean fewer launches and
+// merges but staler column thresholds (more foreign appends); with the
+// balanced panel order (sym_panel) the candidate stage at n = 1M took 1.506 s
+// (1M x 1024 fp32, l2) and 1.959 s (1M x 1536 fp16, ip) with bands of 256,
+// 1.452 s and 1.901 s with 512, and within 1% of that with 640 to 1,024.
+constexpr int64_t kBandMax = 512;
+
 // Whether the direct-load sweep runs symmetric: by default when there are at
 // least 1,024 row panels (n > 261,888), where every band launch still fills
 // the GPU; SWANN_SWEEP_SYM=0|1 forces it (read per call).
@@ -1146,9 +1156,10 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         const int64_t ntile = (n + kBM2 - 1) / kBM2;
         if (splits >= 2 && sweep_sym(ntile) && sweep_waves() == 16) {
             // symmetric sweep: tile (I, J), J >= I, scored once for the rows of
-            // both panels; launched in bands of J - I (1, 1, 2, 4, ... 256 at
-            // a time) with a merge after each, so every launch starts from
-            // thresholds over everything scored so far.  Two lists a row.
+            // both panels; launched in bands of J - I (1, 1, 2, 4, ... 256, then
+            // kBandMax at a time) with a merge after each, so every launch
+            // starts from thresholds over everything scored so far.  Two lists
+            // a row.
             float* gthr = (float*)extra; extra += al256(n * 4);
             int* ovf = (int*)extra;
             hipLaunchKernelGGL(sym_init, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gthr,
@@ -1164,7 +1175,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 if (f >= 1 && f < cap) s.fcap = f;
             }
             for (int64_t b0 = 0; b0 < ntile;) {
-                const int64_t B = b0 == 0 ? 1 : (b0 < 256 ? b0 : 256);
+                const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
                 s.b0 = b0;
                 s.b1 = b0 + B < ntile ? b0 + B : ntile;
                 const unsigned grid = (unsigned)(ntile - b0);
