@@ -1026,9 +1026,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
 // Between two launches of the symmetric sweep: each row's two lists become its
 // C best so far (list 0), list 1 is emptied, and the row's threshold -- the
 // C-th best distance, +inf while it has fewer -- is published for the next
-// launch's screens in both directions.  One wave a row; the compactions are
-// exact (compact_row_core) and each one's stores are fenced before the next
-// step reads them back.
+// launch's screens in both directions.  One wave a row, one pass: every entry
+// of list 0 and then list 1 is loaded into registers, the C smallest of that
+// concatenation are found by the same exact search compact_row_core runs
+// (ties kept in concatenation order), and the kept entries are written to the
+// front of list 0 in that order.  This keeps exactly what compacting list 0,
+// appending list 1 and compacting again would keep, in the same order: an
+// entry among the C smallest of the whole is among the C smallest of its own
+// list, and whatever a first compaction drops has C entries ahead of it.
 __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
                                                  int32_t* __restrict__ bid,
                                                  int32_t* __restrict__ bcnt,
@@ -1039,41 +1044,95 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
     const int lane = threadIdx.x & 63;
     float* k0 = bkey + r * 2 * (int64_t)cap;
     int32_t* i0 = bid + r * 2 * (int64_t)cap;
-    float* k1 = k0 + cap;
-    int32_t* i1 = i0 + cap;
-    int c0 = __builtin_amdgcn_readfirstlane(bcnt[r * 2]);
+    const float* k1 = k0 + cap;
+    const int32_t* i1 = i0 + cap;
+    const int c0 = __builtin_amdgcn_readfirstlane(bcnt[r * 2]);
     int c1 = __builtin_amdgcn_readfirstlane(bcnt[r * 2 + 1]);
     if (c1 > fcap) {                     // appends were dropped: the caller redoes the sweep
         if (lane == 0) atomicAdd(ovf, 1);
         c1 = fcap;
     }
-    if (c0 > C) c0 = compact_row_core(k0, i0, c0, C).kept;
-    if (c1 > cap - c0) c1 = compact_row_core(k1, i1, c1, C).kept;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    constexpr int R = 16;                // cap <= 1024
-    float kv[R];
-    int32_t iv[R];
+    const int cnt = c0 + c1;
+    constexpr int R = 32;                // c0 <= cap, c1 <= fcap <= cap, cap <= 1024
+    // lanes of word t that hold an entry: l < cnt - 64 t
+    auto valid = [&](int t) -> uint64_t {
+        const int rem = cnt - t * 64;
+        return rem >= 64 ? ~0ull : rem <= 0 ? 0ull : ((1ull << rem) - 1);
+    };
+    uint32_t u[R];
+    int32_t v[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) {        // words past cnt are neither loaded nor used
+        u[t] = 0xffffffffu;
+        v[t] = 0;
+        if (t * 64 < cnt) {
+            const int i = min(t * 64 + lane, cnt - 1);
+            const bool first = i < c0;
+            const float* kp = first ? k0 + i : k1 + (i - c0);
+            const int32_t* ip = first ? i0 + i : i1 + (i - c0);
+            const float kf = *kp;
+            v[t] = *ip;
+            u[t] = fkey(kf);
+        }
+    }
+    uint32_t mn = 0xffffffffu, mx = 0;
 #pragma unroll
     for (int t = 0; t < R; ++t) {
-        const int i = t * 64 + lane;
-        if (i < c1) { kv[t] = k1[i]; iv[t] = i1[i]; }
+        if (t * 64 >= cnt) break;
+        const bool in = (valid(t) >> lane) & 1ull;
+        mn = in && u[t] < mn ? u[t] : mn;
+        mx = in && u[t] > mx ? u[t] : mx;
     }
 #pragma unroll
-    for (int t = 0; t < R; ++t) {
-        const int i = t * 64 + lane;
-        if (i < c1) { k0[c0 + i] = kv[t]; i0[c0 + i] = iv[t]; }
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t x = __shfl_xor(mn, off, 64), y = __shfl_xor(mx, off, 64);
+        mn = x < mn ? x : mn;
+        mx = y > mx ? y : mx;
     }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    int c = c0 + c1;
-    float thr = INFINITY;
-    if (c >= C) {
-        const Compacted k = compact_row_core(k0, i0, c, C);
-        c = k.kept;
-        thr = funkey(k.T);
+    uint32_t lo = __builtin_amdgcn_readfirstlane(mn), hi = __builtin_amdgcn_readfirstlane(mx);
+    if (cnt < C) lo = hi = 0xffffffffu;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+            if (t * 64 >= cnt) break;
+            c += __popcll(__ballot(u[t] <= mid) & valid(t));
+        }
+        if (c >= C) hi = mid; else lo = mid + 1;
+    }
+    const uint32_t T = lo;
+    int nlt = 0;
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        if (t * 64 >= cnt) break;
+        nlt += __popcll(__ballot(u[t] < T) & valid(t));
+    }
+    int eq_left = C - nlt;
+    int w = 0;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+        if (t * 64 >= cnt) break;
+        const bool in = (valid(t) >> lane) & 1ull;
+        const bool is_lt = in && u[t] < T;
+        const bool is_eq = in && u[t] == T;
+        const uint64_t meq = __ballot(is_eq);
+        const int eq_rank = __popcll(meq & below);
+        const bool keep = is_lt || (is_eq && eq_rank < eq_left);
+        const uint64_t mk = __ballot(keep);
+        if (keep) {
+            const int dst = w + __popcll(mk & below);
+            k0[dst] = funkey(u[t]);
+            i0[dst] = v[t];
+        }
+        w += __popcll(mk);
+        const int used = __popcll(meq);
+        eq_left -= used < eq_left ? used : eq_left;
     }
     if (lane == 0) {
-        gthr[r] = thr;
-        bcnt[r * 2] = c;
+        gthr[r] = cnt >= C ? funkey(T) : INFINITY;
+        bcnt[r * 2] = w;
         bcnt[r * 2 + 1] = 0;
     }
 }
