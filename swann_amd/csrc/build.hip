@@ -689,20 +689,75 @@ __global__ __launch_bounds__(256) void rev_assemble(const XT* __restrict__ X, in
 }
 
 // ---------------------------------------------------------------------------
+// Row order for the exact re-rank.  Re-ranking row u reads the fp32 rows of its
+// Cs screened candidates (Cs x 4 KB at d = 1024), so rows whose candidates
+// overlap should run together: then most of those reads come from L2 and the
+// memory-side cache instead of HBM.  Each row takes the smallest id reachable
+// through its kOrderK nearest screened candidates (min-label propagation, with
+// a pointer jump per round), and a counting sort by label groups the rows; on
+// a clustered corpus a group is a cluster.  Only the order of the workgroups
+// changes: each row's re-rank is the same computation in any order.
+constexpr int kOrderK = 8, kOrderRounds = 8;
+
+__global__ void order_init(const int32_t* __restrict__ scand, int Cs, int64_t n,
+                           int32_t* __restrict__ lab) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= n) return;
+    int32_t m = (int32_t)u;
+    for (int j = 0; j < kOrderK && j < Cs; ++j) {
+        const int32_t c = scand[u * Cs + j];
+        if (c >= 0 && c < n && c < m) m = c;
+    }
+    lab[u] = m;
+}
+
+// One round, from lin to lout (labels are row ids, so lin[m] is in range).
+__global__ void order_round(const int32_t* __restrict__ scand, int Cs, int64_t n,
+                            const int32_t* __restrict__ lin, int32_t* __restrict__ lout) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= n) return;
+    int32_t m = lin[u];
+    const int32_t jump = lin[m];
+    m = jump < m ? jump : m;
+    for (int j = 0; j < kOrderK && j < Cs; ++j) {
+        const int32_t c = scand[u * Cs + j];
+        if (c >= 0 && c < n) {
+            const int32_t l = lin[c];
+            m = l < m ? l : m;
+        }
+    }
+    lout[u] = m;
+}
+
+__global__ void order_count(const int32_t* __restrict__ lab, int64_t n, int32_t* __restrict__ cnt) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u < n) atomicAdd(&cnt[lab[u]], 1);
+}
+
+// start[l] is the first slot of label l (an exclusive scan of the counts); each
+// row takes the next one, so order is a permutation of [0, n).
+__global__ void order_place(const int32_t* __restrict__ lab, int64_t n, int32_t* __restrict__ start,
+                            int32_t* __restrict__ order) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u < n) order[atomicAdd(&start[lab[u]], 1)] = (int32_t)u;
+}
+
 // Exact re-rank of screened candidates (fp32 corpus): per row, the reference
 // formula on fp32 dot products with each of its Cs screened candidates, sorted
-// by (d, id), the first C kept.  One workgroup per row, 16 lanes per candidate.
+// by (d, id), the first C kept.  One workgroup per row, 16 lanes per candidate;
+// workgroup b re-ranks row order[b] (row b without an order).
 template <int METRIC>
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ X, int64_t n, int dim,
                                                      const float* __restrict__ xn,
                                                      const int32_t* __restrict__ scand, int Cs,
-                                                     int C, int32_t* __restrict__ cand,
+                                                     int C, const int32_t* __restrict__ order,
+                                                     int32_t* __restrict__ cand,
                                                      float* __restrict__ cdist) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* xu = reinterpret_cast<float*>(smem);
     __shared__ float sd[512];
     __shared__ int si[512];
-    const int64_t u = blockIdx.x;
+    const int64_t u = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
     const int tid = threadIdx.x, team = tid >> 4, tl = tid & 15;
     for (int t = tid; t < dim; t += 256) xu[t] = X[u * dim + t];
     int np = 2;
@@ -857,16 +912,34 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
                        bcnt, n, cap, Gu, Cs, mf ? 1 : 0, scand, scd);
     rc = launch_status("sweep final");
     if (rc) return rc;
+    // the re-rank's row order, in the sweep's lists (free once sweep_final has
+    // read them: n * G * cap >= 4 n words)
+    int32_t* lab = (int32_t*)bkey;
+    int32_t* lab2 = lab + n;
+    int32_t* cntl = lab + 2 * n;
+    int32_t* order = lab + 3 * n;
+    const unsigned nb = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(order_init, dim3(nb), dim3(256), 0, st, scand, Cs, n, lab);
+    for (int round = 0; round < kOrderRounds; ++round) {
+        hipLaunchKernelGGL(order_round, dim3(nb), dim3(256), 0, st, scand, Cs, n, lab, lab2);
+        int32_t* t = lab; lab = lab2; lab2 = t;
+    }
+    hipLaunchKernelGGL(fill_i32, dim3(nb), dim3(256), 0, st, cntl, n, 0);
+    hipLaunchKernelGGL(order_count, dim3(nb), dim3(256), 0, st, lab, n, cntl);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cntl, n, lab2);
+    hipLaunchKernelGGL(order_place, dim3(nb), dim3(256), 0, st, lab, n, lab2, order);
+    rc = launch_status("sweep re-rank order");
+    if (rc) return rc;
     // exact fp32 re-rank of the screened lists; the norms are the sweep's
     const float* xnorm = (const float*)extra;
     if (metric == SWANN_METRIC_IP)
         hipLaunchKernelGGL(rerank_kernel<SWANN_METRIC_IP>, dim3((unsigned)n), dim3(256),
-                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C, cand,
-                           cdist);
+                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C,
+                           order, cand, cdist);
     else
         hipLaunchKernelGGL(rerank_kernel<SWANN_METRIC_L2>, dim3((unsigned)n), dim3(256),
-                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C, cand,
-                           cdist);
+                           (size_t)dim * 4, st, (const float*)X, n, dim, xnorm, scand, Cs, C,
+                           order, cand, cdist);
     return launch_status("sweep re-rank");
 }
 
