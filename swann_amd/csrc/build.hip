@@ -745,7 +745,7 @@ __global__ void order_place(const int32_t* __restrict__ lab, int64_t n, int32_t*
 // Exact re-rank of screened candidates (fp32 corpus): per row, the reference
 // formula on fp32 dot products with each of its Cs screened candidates, sorted
 // by (d, id), the first C kept.  One workgroup per row, 16 lanes per candidate;
-// workgroup b re-ranks row order[b] (row b without an order).
+// with an order, the workgroups take its entries in XCD-contiguous runs.
 template <int METRIC>
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ X, int64_t n, int dim,
                                                      const float* __restrict__ xn,
@@ -757,7 +757,10 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ X
     float* xu = reinterpret_cast<float*>(smem);
     __shared__ float sd[512];
     __shared__ int si[512];
-    const int64_t u = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    // consecutive entries of the order run on one XCD (one L2), a group's
+    // rows together
+    const int64_t u = order ? (int64_t)order[xcd_remap(blockIdx.x, gridDim.x)]
+                            : (int64_t)blockIdx.x;
     const int tid = threadIdx.x, team = tid >> 4, tl = tid & 15;
     for (int t = tid; t < dim; t += 256) xu[t] = X[u * dim + t];
     int np = 2;
