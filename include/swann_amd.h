@@ -228,11 +228,18 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
  * w satisfies alpha * d(w, i) <= d(u, i); rows of `deg` ids, -1 padded.
  * C <= 128, deg <= 128.  deg_per_node [n] (or NULL) caps node u at
  * min(deg_per_node[u], deg) kept; protect [n, C] bytes (or NULL): a nonzero
- * entry exempts that candidate from the detour test (build.py:78-81). */
+ * entry exempts that candidate from the detour test (build.py:78-81).
+ * `workspace`: swann_prune_workspace_size bytes, or NULL.  With it the nodes
+ * run grouped by shared candidates (the same result in any order), and an
+ * fp32 corpus whose dim is a multiple of 8 takes the pair Gram from split
+ * fp16 planes (a row scale each: hi and lo halves, three fp16 MFMAs per 16 of
+ * K); without it, nodes in order and the Gram from fp32 MFMAs (the same rows
+ * up to near-ties). */
+int64_t swann_prune_workspace_size(int64_t n, int dim, int x_dtype);
 int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
                       const int32_t* cand, const float* cdist, int C, int deg, float alpha,
                       const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
-                      void* stream);
+                      void* workspace, void* stream);
 
 /* Reverse (build.py:94-150): offer every edge u->v back to v (ascending
  * source, at most max_in per target), dedup [G_u | in_u] minus self, score

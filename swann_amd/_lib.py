@@ -41,7 +41,8 @@ PROTOTYPES = {
     "swann_mfma_probe": (I, [I, I, P, P]),
     "swann_sweep_workspace_size": (I64, [I64, I, I, I]),
     "swann_build_sweep": (I, [P, I, I64, I, I, I, P, P, P, P]),
-    "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P]),
+    "swann_prune_workspace_size": (I64, [I64, I, I]),
+    "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P, P]),
     "swann_reverse_workspace_size": (I64, [I64, I, I]),
     "swann_build_reverse": (I, [P, I, I64, I, I, P, I, F, I, P, P, P, P]),
     "swann_codes_workspace_size": (I64, [I64, I]),

@@ -90,9 +90,11 @@ def robust_prune(Xg, cand, cdist, deg, alpha=1.2, chunk=4096, deg_per_node=None,
         if prot.shape != (n, C):
             raise ValueError("protect must be [n, C] like the candidates")
     out = torch.empty((n, width), dtype=torch.int32, device=Xg.device)
+    wsb = int(lib().swann_prune_workspace_size(n, Xg.shape[1], _DT[Xg.dtype]))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=Xg.device) if wsb else None
     with torch.cuda.device(Xg.device):
         call("swann_build_prune", ptr(Xg), _DT[Xg.dtype], n, Xg.shape[1], _m(metric), ptr(cand),
-             ptr(cdist), int(C), width, float(alpha), ptr(dpn), ptr(prot), ptr(out),
+             ptr(cdist), int(C), width, float(alpha), ptr(dpn), ptr(prot), ptr(out), ptr(ws),
              stream_of(Xg.device))
     return out
 

@@ -292,13 +292,26 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 // floats, four 32x32x2 MFMAs (k = 4*(l/32) + s of the step's 8, a
 // permutation of the K order, which a sum over k does not see).  Products
 // are exact (fp16) or fp32 (fp32), sums fp32.  dim % 8 (fp16: % 16) == 0.
+//
+// PLANES (fp32 rows): each staged float y = x / s_r (s_r a power of two with
+// |y| < 2^15 for the whole row) is split into hi = fp16(y) and lo =
+// fp16((y - hi) * 2^11), hi in logical chunks 0-3 of the row's 128 bytes, lo
+// in 4-7; the Gram entry is s_a s_b (hi.hi + (hi.lo + lo.hi) / 2^11), three
+// 32x32x16 f16 MFMAs per 16 of K (exact products, fp32 sums) for what the
+// fp32 path does in eight 32x32x2 f32 MFMAs.  y keeps 22 of its 24
+// significant bits (the lo.lo term and lo's own rounding are below 2^-22 of
+// the element), so the Gram differs from the fp32 one by a few of its last
+// bits, like a different summation order.
 constexpr int kStgRow = 128;                       // bytes of a row per K chunk
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int pswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-template <typename XT>
+template <typename XT, bool PLANES = false>
 __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, const int* cid,
-                                 int C, float* gram, float* vn, unsigned char* stg) {
+                                 int C, float* gram, float* vn, unsigned char* stg,
+                                 const float* srow = nullptr) {
+    static_assert(!PLANES || sizeof(XT) == 4, "the split planes are for fp32 rows");
     constexpr int EPC = 16 / sizeof(XT);           // elements per 16-byte chunk
     constexpr int KC = kStgRow / sizeof(XT);       // elements of a row per K chunk
     const int tid = threadIdx.x, lane = tid & 63;
@@ -318,11 +331,15 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
         on[x] = ti[x] >= 0 && ti[x] * 32 < C && tj[x] * 32 < C;
     }
     const bool busy = on[0] || on[1] || on[2];
-    f32x16v acc[3];
+    f32x16v acc[3], accx[PLANES ? 3 : 1];
 #pragma unroll
     for (int x = 0; x < 3; ++x)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[x][e] = 0.f;
+#pragma unroll
+    for (int x = 0; x < (PLANES ? 3 : 1); ++x)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) accx[x][e] = 0.f;
     const int half = lane >> 5;
     // staging: 128 rows x 8 chunks, 4 per thread; the next K chunk's loads
     // go out before this chunk's MFMAs, so their latency hides behind them
@@ -350,12 +367,56 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
         for (int q = 0; q < 4; ++q) {
             const int e = q * 256 + tid;
             const int r = e >> 3, c = e & 7;
-            if (r < rows)
-                *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = nxt[q];
+            if (r < rows) {
+                if constexpr (PLANES) {
+                    // floats 4c..4c+3 of the chunk: their hi halves to byte
+                    // 8c of the hi plane (logical chunk c/2), lo to the lo plane
+                    const float inv = 1.f / srow[r];
+                    const f32x4v v = __builtin_bit_cast(f32x4v, nxt[q]);
+                    h16x4 hi, lo;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float y = v[i] * inv;
+                        const _Float16 h = (_Float16)y;
+                        hi[i] = h;
+                        lo[i] = (_Float16)((y - (float)h) * 2048.f);
+                    }
+                    unsigned char* row = stg + r * kStgRow + ((c & 1) << 3);
+                    *reinterpret_cast<uint2*>(row + (((c >> 1) ^ pswz(r)) << 4)) =
+                        __builtin_bit_cast(uint2, hi);
+                    *reinterpret_cast<uint2*>(row + (((4 + (c >> 1)) ^ pswz(r)) << 4)) =
+                        __builtin_bit_cast(uint2, lo);
+                } else {
+                    *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = nxt[q];
+                }
+            }
         }
         __syncthreads();
         if (k0 + KC < dim) fetch(k0 + KC);
-        if (busy) {
+        if (PLANES && busy) {
+            // 32 of K a chunk: two 16-wide steps of hi.hi, hi.lo and lo.hi
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int chh = 2 * t + half, chl = 4 + 2 * t + half;
+#pragma unroll
+                for (int x = 0; x < 3; ++x) {
+                    if (!on[x]) continue;
+                    const int ar = ti[x] * 32 + (lane & 31);
+                    const int br = tj[x] * 32 + (lane & 31);
+                    const h16x8 ah = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(
+                        stg + ar * kStgRow + ((chh ^ pswz(ar)) << 4)));
+                    const h16x8 al = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(
+                        stg + ar * kStgRow + ((chl ^ pswz(ar)) << 4)));
+                    const h16x8 bh = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(
+                        stg + br * kStgRow + ((chh ^ pswz(br)) << 4)));
+                    const h16x8 bl = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(
+                        stg + br * kStgRow + ((chl ^ pswz(br)) << 4)));
+                    acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[x], 0, 0, 0);
+                    accx[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, accx[x], 0, 0, 0);
+                    accx[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, accx[x], 0, 0, 0);
+                }
+            }
+        } else if (busy) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int ch = 2 * t + half;
@@ -394,28 +455,59 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
         for (int e = 0; e < 16; ++e) {
             const int r = ti[x] * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
             if (r < C && cc < C) {
-                if (r < cc) gram[tri(r, cc)] = acc[x][e];
-                else if (r == cc) vn[r] = acc[x][e];
+                float g = acc[x][e];
+                if constexpr (PLANES)
+                    g = (srow[r] * srow[cc]) * (acc[x][e] + accx[x][e] * (1.f / 2048.f));
+                if (r < cc) gram[tri(r, cc)] = g;
+                else if (r == cc) vn[r] = g;
             }
         }
     }
 }
 
-template <typename XT, bool MFMA>
-__global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, int64_t n,
+// Per fp32 row, the power of two s with max |x| / s < 2^15 (1 for a zero or
+// non-finite row): the scale of its split planes.  One wave a row.
+__global__ __launch_bounds__(256) void row_scale(const float* __restrict__ X, int64_t n, int dim,
+                                                 float* __restrict__ scale) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= n) return;
+    const int lane = threadIdx.x & 63;
+    float m = 0.f;
+    for (int k = lane; k < dim; k += 64) m = fmaxf(m, fabsf(X[r * dim + k]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) {
+        float sc = 1.f;
+        if (m > 0.f && m <= FLT_MAX) {
+            int e;
+            frexpf(m, &e);                       // m < 2^e
+            sc = ldexpf(1.f, e - 15 < -126 ? -126 : e - 15);
+        }
+        scale[r] = sc;
+    }
+}
+
+// At least two workgroups a CU: the split-plane Gram's fragments and its six
+// accumulator tiles otherwise take 300 registers a wave, one workgroup a CU.
+template <typename XT, bool MFMA, bool PLANES = false>
+__global__ __launch_bounds__(256, 2) void prune_kernel(const XT* __restrict__ X, int64_t n,
                                                     int dim, int metric,
                                                     const int32_t* __restrict__ cand,
                                                     const float* __restrict__ cdist, int C,
                                                     int deg, float alpha,
                                                     const int32_t* __restrict__ dpn,
                                                     const uint8_t* __restrict__ protect,
-                                                    int32_t* __restrict__ out) {
+                                                    int32_t* __restrict__ out,
+                                                    const float* __restrict__ rscale = nullptr,
+                                                    const int32_t* __restrict__ order = nullptr) {
     __shared__ float gram[kPruneMaxC * (kPruneMaxC - 1) / 2];
     __shared__ float vn[kPruneMaxC];
     __shared__ float Vs[MFMA ? 1 : kPKC][kPruneMaxC + 4];
     __shared__ int cid[kPruneMaxC];
     __shared__ float cdu[kPruneMaxC];
-    const int64_t u = blockIdx.x;
+    // with an order, consecutive entries (nodes sharing candidates) on one XCD
+    const int64_t u = order ? (int64_t)order[xcd_remap(blockIdx.x, gridDim.x)]
+                            : (int64_t)blockIdx.x;
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     for (int i = tid; i < C; i += 256) {
         const int c = cand[u * C + i];
@@ -426,13 +518,20 @@ __global__ __launch_bounds__(256) void prune_kernel(const XT* __restrict__ X, in
     if constexpr (MFMA) {
         // candidates past the last valid one are never read: the Gram stops there
         __shared__ __align__(16) unsigned char stg[kPruneMaxC * kStgRow];
+        __shared__ float srow[PLANES ? kPruneMaxC : 1];
         __shared__ int s_nv;
         if (tid == 0) s_nv = 0;
+        if constexpr (PLANES) {
+            for (int i = tid; i < kPruneMaxC; i += 256) {
+                const int c = i < C ? cid[i] : -1;
+                srow[i] = (c >= 0 && c < n) ? rscale[c] : 1.f;
+            }
+        }
         __syncthreads();
         for (int i = tid; i < C; i += 256)
             if (cid[i] >= 0 && cid[i] < n) atomicMax(&s_nv, i + 1);
         __syncthreads();
-        gram_mfma_staged<XT>(X, n, dim, cid, s_nv, gram, vn, stg);
+        gram_mfma_staged<XT, PLANES>(X, n, dim, cid, s_nv, gram, vn, stg, srow);
     } else {
     // thread (ty, tx) accumulates Gram rows ty*8.., columns tx*8.. (C <= 128)
     float acc[8][8] = {};
@@ -729,17 +828,103 @@ __global__ void order_round(const int32_t* __restrict__ scand, int Cs, int64_t n
     lout[u] = m;
 }
 
-__global__ void order_count(const int32_t* __restrict__ lab, int64_t n, int32_t* __restrict__ cnt) {
+// A wave's rows take their labels' slots one distinct label at a time: one
+// atomic per label and wave, so a corpus whose rows share a label (an
+// unclustered one ends with one label) does not serialize on one counter.
+// Returns this lane's slot: the counter's value before its wave's add, plus
+// its rank among the wave's lanes of that label.
+__device__ __forceinline__ int wave_label_add(int32_t* ctr, int label, bool on) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    uint64_t left = __ballot(on);
+    int mine = 0;
+    while (left) {
+        const int first = __builtin_ctzll(left);
+        const int l0 = __shfl(label, first, 64);
+        const uint64_t same = __ballot(on && label == l0) & left;
+        int base = 0;
+        if (lane == first) base = atomicAdd(&ctr[l0], __popcll(same));
+        base = __shfl(base, first, 64);
+        if ((same >> lane) & 1ull) mine = base + __popcll(same & below);
+        left &= ~same;
+    }
+    return mine;
+}
+
+__global__ __launch_bounds__(256) void order_count(const int32_t* __restrict__ lab, int64_t n,
+                                                   int32_t* __restrict__ cnt) {
     const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (u < n) atomicAdd(&cnt[lab[u]], 1);
+    const bool on = u < n;
+    wave_label_add(cnt, on ? lab[u] : 0, on);
 }
 
 // start[l] is the first slot of label l (an exclusive scan of the counts); each
 // row takes the next one, so order is a permutation of [0, n).
-__global__ void order_place(const int32_t* __restrict__ lab, int64_t n, int32_t* __restrict__ start,
-                            int32_t* __restrict__ order) {
+__global__ __launch_bounds__(256) void order_place(const int32_t* __restrict__ lab, int64_t n,
+                                                   int32_t* __restrict__ start,
+                                                   int32_t* __restrict__ order) {
     const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (u < n) order[atomicAdd(&start[lab[u]], 1)] = (int32_t)u;
+    const bool on = u < n;
+    const int slot = wave_label_add(start, on ? lab[u] : 0, on);
+    if (on) order[slot] = (int32_t)u;
+}
+
+// Exclusive scan of n counts across the GPU: each 1,024-block scans its own
+// (scan_blocks, totals to tmp[b]), one workgroup scans the nb totals
+// (scan_kernel, into tmp + nb), each block adds its offset (scan_add).
+// tmp holds 2 nb words.
+__global__ __launch_bounds__(1024) void scan_blocks(const int32_t* __restrict__ in, int64_t n,
+                                                    int32_t* __restrict__ out,
+                                                    int32_t* __restrict__ total) {
+    __shared__ int buf[1024];
+    const int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const int v = i < n ? in[i] : 0;
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int t = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+        __syncthreads();
+        buf[threadIdx.x] += t;
+        __syncthreads();
+    }
+    if (i < n) out[i] = buf[threadIdx.x] - v;
+    if (threadIdx.x == 1023) total[blockIdx.x] = buf[1023];
+}
+
+__global__ __launch_bounds__(1024) void scan_add(int32_t* __restrict__ out, int64_t n,
+                                                 const int32_t* __restrict__ offset) {
+    const int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    if (i < n) out[i] += offset[blockIdx.x];
+}
+
+void scan_exclusive(const int32_t* in, int64_t n, int32_t* out, int32_t* tmp, hipStream_t st) {
+    const int64_t nb = (n + 1023) / 1024;
+    hipLaunchKernelGGL(scan_blocks, dim3((unsigned)nb), dim3(1024), 0, st, in, n, out, tmp);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, tmp, nb, tmp + nb);
+    hipLaunchKernelGGL(scan_add, dim3((unsigned)nb), dim3(1024), 0, st, out, n, tmp + nb);
+}
+
+// The order over `scratch` (4 n words: two label arrays, counts, the order),
+// from the first kOrderK of each row's C candidates; returns the order.
+int32_t* neighbourhood_order(const int32_t* cand, int C, int64_t n, int32_t* scratch,
+                             hipStream_t st) {
+    int32_t* lab = scratch;
+    int32_t* lab2 = scratch + n;
+    int32_t* cntl = scratch + 2 * n;
+    int32_t* order = scratch + 3 * n;
+    const unsigned nb = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(order_init, dim3(nb), dim3(256), 0, st, cand, C, n, lab);
+    for (int round = 0; round < kOrderRounds; ++round) {
+        hipLaunchKernelGGL(order_round, dim3(nb), dim3(256), 0, st, cand, C, n, lab, lab2);
+        int32_t* t = lab; lab = lab2; lab2 = t;
+    }
+    hipLaunchKernelGGL(fill_i32, dim3(nb), dim3(256), 0, st, cntl, n, 0);
+    hipLaunchKernelGGL(order_count, dim3(nb), dim3(256), 0, st, lab, n, cntl);
+    // the scan's 2 * ceil(n / 1024) words of block totals sit in `order`,
+    // which order_place fills only afterwards
+    scan_exclusive(cntl, n, lab2, order, st);
+    hipLaunchKernelGGL(order_place, dim3(nb), dim3(256), 0, st, lab, n, lab2, order);
+    return order;
 }
 
 // Exact re-rank of screened candidates (fp32 corpus): per row, the reference
@@ -917,20 +1102,7 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     if (rc) return rc;
     // the re-rank's row order, in the sweep's lists (free once sweep_final has
     // read them: n * G * cap >= 4 n words)
-    int32_t* lab = (int32_t*)bkey;
-    int32_t* lab2 = lab + n;
-    int32_t* cntl = lab + 2 * n;
-    int32_t* order = lab + 3 * n;
-    const unsigned nb = (unsigned)((n + 255) / 256);
-    hipLaunchKernelGGL(order_init, dim3(nb), dim3(256), 0, st, scand, Cs, n, lab);
-    for (int round = 0; round < kOrderRounds; ++round) {
-        hipLaunchKernelGGL(order_round, dim3(nb), dim3(256), 0, st, scand, Cs, n, lab, lab2);
-        int32_t* t = lab; lab = lab2; lab2 = t;
-    }
-    hipLaunchKernelGGL(fill_i32, dim3(nb), dim3(256), 0, st, cntl, n, 0);
-    hipLaunchKernelGGL(order_count, dim3(nb), dim3(256), 0, st, lab, n, cntl);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cntl, n, lab2);
-    hipLaunchKernelGGL(order_place, dim3(nb), dim3(256), 0, st, lab, n, lab2, order);
+    const int32_t* order = neighbourhood_order(scand, Cs, n, (int32_t*)bkey, st);
     rc = launch_status("sweep re-rank order");
     if (rc) return rc;
     // exact fp32 re-rank of the screened lists; the norms are the sweep's
@@ -946,10 +1118,15 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     return launch_status("sweep re-rank");
 }
 
+int64_t swann_prune_workspace_size(int64_t n, int dim, int x_dtype) {
+    // the node order (4 n words), then the fp32 rows' plane scales
+    return align256(n * 16) + (x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 ? align256(n * 4) : 0);
+}
+
 int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
                       const int32_t* cand, const float* cdist, int C, int deg, float alpha,
                       const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
-                      void* stream) {
+                      void* workspace, void* stream) {
     clear_error();
     SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
                   "metric must be 0 (ip) or 1 (l2)");
@@ -966,29 +1143,49 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
     const bool simt = getenv_flag("SWANN_PRUNE_SIMT");
     const bool mfma16 = x_dtype == SWANN_DTYPE_F16 && dim % 16 == 0 && (uintptr_t)X % 16 == 0;
     const bool mfma32 = x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 && (uintptr_t)X % 16 == 0;
+    // fp32 rows with a workspace for their scales: the Gram on split fp16
+    // planes (SWANN_PRUNE_F32=1 keeps the fp32 MFMA Gram)
+    const bool planes = mfma32 && workspace && !getenv_flag("SWANN_PRUNE_F32");
+    // with a workspace, nodes run grouped by shared candidates (each node's
+    // prune is the same computation in any order): their candidate rows then
+    // come from L2 and the memory-side cache on a clustered corpus
+    const int32_t* order = nullptr;
+    if (workspace) {
+        order = neighbourhood_order(cand, C, n, (int32_t*)workspace, st);
+        const int rc = launch_status("prune order");
+        if (rc) return rc;
+    }
+    float* rscale = workspace ? (float*)((char*)workspace + align256(n * 16)) : nullptr;
     if (!simt && mfma16)
         hipLaunchKernelGGL((prune_kernel<_Float16, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                           deg_per_node, protect, out);
-    else if (!simt && mfma32)
+                           deg_per_node, protect, out, nullptr, order);
+    else if (!simt && planes) {
+        hipLaunchKernelGGL(row_scale, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
+                           (const float*)X, n, dim, rscale);
+        hipLaunchKernelGGL((prune_kernel<float, true, true>), dim3((unsigned)n), dim3(256), 0,
+                           st, (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
+                           deg_per_node, protect, out, rscale, order);
+    } else if (!simt && mfma32)
         hipLaunchKernelGGL((prune_kernel<float, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                           deg_per_node, protect, out);
+                           deg_per_node, protect, out, nullptr, order);
     else
         SWANN_BY_DTYPE(x_dtype,
             hipLaunchKernelGGL((prune_kernel<float, false>), dim3((unsigned)n), dim3(256), 0, st,
                                (const float*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                               deg_per_node, protect, out),
+                               deg_per_node, protect, out, nullptr, order),
             hipLaunchKernelGGL((prune_kernel<_Float16, false>), dim3((unsigned)n), dim3(256), 0,
                                st, (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
-                               deg_per_node, protect, out));
+                               deg_per_node, protect, out, nullptr, order));
     return launch_status("prune");
 }
 
 int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in) {
     const int keepn = (deg + max_in) < kPruneMaxC ? (deg + max_in) : kPruneMaxC;
+    // then the re-prune's workspace (swann_prune_workspace_size for fp32)
     return align256(n * 4) * 3 + align256(n * (int64_t)deg * 4) +
-           align256(n * (int64_t)keepn * 4) * 2;
+           align256(n * (int64_t)keepn * 4) * 2 + align256(n * 16) + align256(n * 4);
 }
 
 int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metric,
@@ -1012,7 +1209,8 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
     int32_t* start = (int32_t*)ws; ws += align256(n * 4);
     int32_t* src = (int32_t*)ws; ws += align256(n * (int64_t)deg * 4);
     int32_t* cand2 = (int32_t*)ws; ws += align256(n * (int64_t)keepn * 4);
-    float* cd2 = (float*)ws;
+    float* cd2 = (float*)ws; ws += align256(n * (int64_t)keepn * 4);
+    void* prune_ws = ws;
     // counters are cleared by a kernel, not a memset, so the pass can be captured
     const unsigned nbk = (unsigned)((n + 255) / 256);
     hipLaunchKernelGGL(fill_i32, dim3(nbk), dim3(256), 0, st, cnt, n, 0);
@@ -1034,7 +1232,7 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
     rc = launch_status("reverse assemble");
     if (rc) return rc;
     return swann_build_prune(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha,
-                             deg_per_node, nullptr, out, stream);
+                             deg_per_node, nullptr, out, prune_ws, stream);
 }
 
 }  // extern "C"

@@ -432,16 +432,20 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
 
 
 @pytest.mark.parametrize("C", [48, 100])
-@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("dtype", ["f16", "f32", "f32-fp32gram"])
 @pytest.mark.parametrize("metric", [0, 1])
 def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
     """The prune's Gram on MFMA -- fp16 rows: exact products, fp32 sums
-    (32x32x16 f16); fp32 rows: fp32 products and sums (32x32x2 f32) -- keeps
+    (32x32x16 f16); fp32 rows: split fp16 planes (hi.hi + (hi.lo + lo.hi) /
+    2^11 on 32x32x16 f16), or with SWANN_PRUNE_F32=1 fp32 products and sums
+    (32x32x2 f32); nodes grouped by shared candidates -- keeps
     the same rows as the fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle
     (double dots) up to near-ties.  d = 80 leaves a ragged last K group for
     fp16; C = 48 fills two of the four 32-row blocks (three of the ten Gram
     tiles), C = 100 all four with a ragged last (every tile, every wave);
     per-node caps and protect ride along."""
+    if dtype == "f32-fp32gram":
+        monkeypatch.setenv("SWANN_PRUNE_F32", "1")
     X = gaussian(3000, 80, 71 + metric, metric == 0)
     if metric == 1:
         X = X * 2.0 + 0.5
