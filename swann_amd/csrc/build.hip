@@ -684,12 +684,15 @@ __global__ __launch_bounds__(256) void rev_assemble(const XT* __restrict__ X, in
                                                     const int32_t* __restrict__ start,
                                                     const int32_t* __restrict__ src, int keepn,
                                                     int32_t* __restrict__ cand2,
-                                                    float* __restrict__ cd2) {
+                                                    float* __restrict__ cd2,
+                                                    const int32_t* __restrict__ order) {
     __shared__ int ib[kRevBuf];
     __shared__ int row[512];
     __shared__ float rd[512];
     __shared__ float xu[4096];
-    const int64_t u = blockIdx.x;
+    // with an order, consecutive entries (nodes sharing neighbours) on one XCD
+    const int64_t u = order ? (int64_t)order[xcd_remap(blockIdx.x, gridDim.x)]
+                            : (int64_t)blockIdx.x;
     const int tid = threadIdx.x;
     const int cu = cnt[u];
     const int64_t s0 = start[u];
@@ -1123,21 +1126,16 @@ int64_t swann_prune_workspace_size(int64_t n, int dim, int x_dtype) {
     return align256(n * 16) + (x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 ? align256(n * 4) : 0);
 }
 
-int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
-                      const int32_t* cand, const float* cdist, int C, int deg, float alpha,
-                      const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
-                      void* workspace, void* stream) {
-    clear_error();
-    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
-                  "metric must be 0 (ip) or 1 (l2)");
-    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
-                  "X: float32 or float16");
-    SWANN_REQUIRE(C >= 1 && C <= kPruneMaxC, "prune: candidates per node must be in 1..%d",
-                  kPruneMaxC);
-    SWANN_REQUIRE(deg >= 1 && deg <= kPruneMaxC, "prune: degree must be in 1..%d", kPruneMaxC);
-    SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
-    SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
-    hipStream_t st = (hipStream_t)stream;
+}  // extern "C"
+
+namespace swann {
+namespace {
+// The prune's launches: `order` (or NULL) the node order, `rscale` (or NULL)
+// n words for an fp32 corpus's plane scales.
+int prune_run(const void* X, int x_dtype, int64_t n, int dim, int metric, const int32_t* cand,
+              const float* cdist, int C, int deg, float alpha, const int32_t* deg_per_node,
+              const uint8_t* protect, int32_t* out, const int32_t* order, float* rscale,
+              hipStream_t st) {
     // the Gram on MFMA: fp16 rows with 16-byte aligned 16-wide K steps, fp32
     // rows with 16-byte aligned 8-wide K steps
     const bool simt = getenv_flag("SWANN_PRUNE_SIMT");
@@ -1145,17 +1143,7 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
     const bool mfma32 = x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 && (uintptr_t)X % 16 == 0;
     // fp32 rows with a workspace for their scales: the Gram on split fp16
     // planes (SWANN_PRUNE_F32=1 keeps the fp32 MFMA Gram)
-    const bool planes = mfma32 && workspace && !getenv_flag("SWANN_PRUNE_F32");
-    // with a workspace, nodes run grouped by shared candidates (each node's
-    // prune is the same computation in any order): their candidate rows then
-    // come from L2 and the memory-side cache on a clustered corpus
-    const int32_t* order = nullptr;
-    if (workspace) {
-        order = neighbourhood_order(cand, C, n, (int32_t*)workspace, st);
-        const int rc = launch_status("prune order");
-        if (rc) return rc;
-    }
-    float* rscale = workspace ? (float*)((char*)workspace + align256(n * 16)) : nullptr;
+    const bool planes = mfma32 && rscale && !getenv_flag("SWANN_PRUNE_F32");
     if (!simt && mfma16)
         hipLaunchKernelGGL((prune_kernel<_Float16, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,
@@ -1180,6 +1168,39 @@ int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric
                                deg_per_node, protect, out, nullptr, order));
     return launch_status("prune");
 }
+}  // namespace
+}  // namespace swann
+
+extern "C" {
+
+int swann_build_prune(const void* X, int x_dtype, int64_t n, int dim, int metric,
+                      const int32_t* cand, const float* cdist, int C, int deg, float alpha,
+                      const int32_t* deg_per_node, const uint8_t* protect, int32_t* out,
+                      void* workspace, void* stream) {
+    clear_error();
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(x_dtype == SWANN_DTYPE_F32 || x_dtype == SWANN_DTYPE_F16,
+                  "X: float32 or float16");
+    SWANN_REQUIRE(C >= 1 && C <= kPruneMaxC, "prune: candidates per node must be in 1..%d",
+                  kPruneMaxC);
+    SWANN_REQUIRE(deg >= 1 && deg <= kPruneMaxC, "prune: degree must be in 1..%d", kPruneMaxC);
+    SWANN_REQUIRE(n >= 1 && n <= INT32_MAX, "prune: n out of range");
+    SWANN_REQUIRE(X && cand && cdist && out, "prune: a required pointer is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    // with a workspace, nodes run grouped by shared candidates (each node's
+    // prune is the same computation in any order): their candidate rows then
+    // come from L2 and the memory-side cache on a clustered corpus
+    const int32_t* order = nullptr;
+    if (workspace) {
+        order = neighbourhood_order(cand, C, n, (int32_t*)workspace, st);
+        const int rc = launch_status("prune order");
+        if (rc) return rc;
+    }
+    float* rscale = workspace ? (float*)((char*)workspace + align256(n * 16)) : nullptr;
+    return prune_run(X, x_dtype, n, dim, metric, cand, cdist, C, deg, alpha, deg_per_node,
+                     protect, out, order, rscale, st);
+}
 
 int64_t swann_reverse_workspace_size(int64_t n, int deg, int max_in) {
     const int keepn = (deg + max_in) < kPruneMaxC ? (deg + max_in) : kPruneMaxC;
@@ -1199,6 +1220,8 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
                   "X: float32 or float16");
     SWANN_REQUIRE(deg >= 1 && max_in >= 0 && deg + max_in <= 512,
                   "reverse: need deg >= 1, max_in >= 0, deg + max_in <= 512");
+    SWANN_REQUIRE(deg <= kPruneMaxC, "reverse: degree must be in 1..%d (the re-prune's)",
+                  kPruneMaxC);
     SWANN_REQUIRE(n >= 1 && n * (int64_t)deg < INT32_MAX, "reverse: n * deg must fit in int32");
     SWANN_REQUIRE(X && G && out && workspace, "reverse: a required pointer is NULL");
     hipStream_t st = (hipStream_t)stream;
@@ -1222,17 +1245,21 @@ int swann_build_reverse(const void* X, int x_dtype, int64_t n, int dim, int metr
     hipLaunchKernelGGL(rev_scatter, dim3(eb), dim3(256), 0, st, G, n, deg, start, fill, src);
     int rc = launch_status("reverse scatter");
     if (rc) return rc;
+    // one node order, from the graph's rows, for both the assembly and the
+    // re-prune: both gather the rows of a node's neighbours
+    const int32_t* order = neighbourhood_order(G, deg, n, (int32_t*)prune_ws, st);
+    float* rscale = (float*)((char*)prune_ws + align256(n * 16));
     SWANN_BY_DTYPE(x_dtype,
         hipLaunchKernelGGL(rev_assemble<float>, dim3((unsigned)n), dim3(256), 0, st,
                            (const float*)X, n, dim, metric, G, deg, max_in, cnt, start, src,
-                           keepn, cand2, cd2),
+                           keepn, cand2, cd2, order),
         hipLaunchKernelGGL(rev_assemble<_Float16>, dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, G, deg, max_in, cnt, start, src,
-                           keepn, cand2, cd2));
+                           keepn, cand2, cd2, order));
     rc = launch_status("reverse assemble");
     if (rc) return rc;
-    return swann_build_prune(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha,
-                             deg_per_node, nullptr, out, prune_ws, stream);
+    return prune_run(X, x_dtype, n, dim, metric, cand2, cd2, keepn, deg, alpha, deg_per_node,
+                     nullptr, out, order, rscale, st);
 }
 
 }  // extern "C"
