@@ -83,6 +83,52 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ X, i
     if (lane == 0) { scale[r] = s; norm[r] = s2; }
 }
 
+// The spread of an fp32 corpus's row maxima: rng[0] the largest and rng[1] the
+// smallest max |x| of a row, as float bits (non-negative floats order as
+// ints; a NaN row reads as the largest).  rng starts at {0, INT_MAX}.
+__global__ __launch_bounds__(256) void row_range(const float* __restrict__ X, int64_t n, int dim,
+                                                 int* __restrict__ rng) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n) return;
+    const float* x = X + r * dim;
+    float m = 0.f;
+    for (int t = lane; t < dim; t += 64) m = fmaxf(m, fabsf(x[t]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) {
+        atomicMax(&rng[0], __float_as_int(m));
+        atomicMin(&rng[1], __float_as_int(m));
+    }
+}
+
+__global__ void range_init(int* rng) {
+    if (threadIdx.x == 0) { rng[0] = 0; rng[1] = 0x7fffffff; }
+}
+
+// An fp32 corpus whose row maxima all lie in [2^-4, 2^14] goes to fp16 as it
+// is: fp16 keeps 11 significant bits of every element in its normal range at
+// any scale, as the row-scaled plane does, and the sweep then runs its
+// unscaled kernel (no per-score scale products).  Norms as split_rows
+// computes them (the same order), so the re-rank's are unchanged.
+__global__ __launch_bounds__(256) void rows_to_f16(const float* __restrict__ X, int64_t n, int dim,
+                                                   _Float16* __restrict__ hi,
+                                                   float* __restrict__ norm) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n) return;
+    const float* x = X + r * dim;
+    float s2 = 0.f;
+    for (int t = lane; t < dim; t += 64) {
+        const float v = x[t];
+        s2 = __builtin_fmaf(v, v, s2);
+        hi[r * dim + t] = (_Float16)v;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off, 64);
+    if (lane == 0) norm[r] = s2;
+}
+
 __global__ __launch_bounds__(256) void norms_f16(const _Float16* __restrict__ X, int64_t n,
                                                  int dim, float* __restrict__ norm,
                                                  float* __restrict__ scale) {
@@ -1192,16 +1238,33 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     float* xn = (float*)extra; extra += al256(n * 4);
     float* scale = (float*)extra; extra += al256(n * 4);
     const _Float16* hi;
-    const int scaled = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
+    int scaled = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
+    const unsigned nrb = (unsigned)((n + 3) / 4);
     if (!scaled) {
         hi = (const _Float16*)X;
-        hipLaunchKernelGGL(norms_f16, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, hi, n, dim,
-                           xn, scale);
+        hipLaunchKernelGGL(norms_f16, dim3(nrb), dim3(256), 0, st, hi, n, dim, xn, scale);
     } else {
         _Float16* h = (_Float16*)extra;
         extra += al256(n * (int64_t)dim * 2);
-        hipLaunchKernelGGL(split_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
-                           (const float*)X, n, dim, h, (_Float16*)nullptr, scale, xn);
+        // the row maxima's range (in `scale`, unused until split_rows writes it)
+        int* rng = (int*)scale;
+        hipLaunchKernelGGL(range_init, dim3(1), dim3(64), 0, st, rng);
+        hipLaunchKernelGGL(row_range, dim3(nrb), dim3(256), 0, st, (const float*)X, n, dim, rng);
+        int hr[2] = {0, 0};
+        if (hipMemcpyAsync(hr, rng, sizeof(hr), hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            set_error("sweep (mfma): reading the rows' range failed");
+            return SWANN_E_LAUNCH;
+        }
+        const float gmax = __builtin_bit_cast(float, hr[0]), gmin = __builtin_bit_cast(float, hr[1]);
+        if (gmax <= 16384.f && gmin >= 0.0625f && !getenv_flag("SWANN_SWEEP_ROWSCALE")) {
+            hipLaunchKernelGGL(rows_to_f16, dim3(nrb), dim3(256), 0, st, (const float*)X, n, dim,
+                               h, xn);
+            scaled = 0;
+        } else {
+            hipLaunchKernelGGL(split_rows, dim3(nrb), dim3(256), 0, st, (const float*)X, n, dim,
+                               h, (_Float16*)nullptr, scale, xn);
+        }
         hi = h;
     }
     MfmaSweepArgs a{hi, nullptr, scale, xn, n, dim, metric, C, cap, bkey, bid, bcnt, scaled, 1,
