@@ -205,7 +205,8 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
 
 
 @pytest.mark.parametrize("switch", [("SWANN_SWEEP_WAVES", "8"), ("SWANN_SWEEP_REGSTAGE", "1"),
-                                    ("SWANN_SWEEP_SYM", "1"), ("SWANN_SWEEP_SYM_FCAP", "4")])
+                                    ("SWANN_SWEEP_SYM", "1"), ("SWANN_SWEEP_SYM_FCAP", "4"),
+                                    ("SWANN_SWEEP_ROWSCALE", "1")])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtype):
@@ -214,7 +215,9 @@ def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtyp
     both of its panels' rows, in bands of launches), all chosen by
     environment at each call, keep the oracle's lists like the default
     layout; so does the symmetric sweep whose second lists are made to
-    overflow (4 entries of room), which must redo the sweep one-sided."""
+    overflow (4 entries of room), which must redo the sweep one-sided, and an
+    fp32 corpus screened on a row-scaled fp16 plane (the default takes these
+    corpora's values into fp16 unscaled)."""
     monkeypatch.setenv(*switch)
     if switch[0] == "SWANN_SWEEP_SYM_FCAP":
         monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
