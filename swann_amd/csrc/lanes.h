@@ -70,6 +70,20 @@ __device__ __forceinline__ uint64_t row_down64(uint64_t v) {
     return ((uint64_t)h2 << 32) | l2;
 }
 
+// Minimum of v over all 64 lanes (every lane active), returned wave-uniform;
+// a lane whose row_shr source falls off its row keeps its own value.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    auto mn = [](uint32_t a, uint32_t b) { return a < b ? a : b; };
+    v = mn(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xF, 0xF, false));
+    v = mn(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x112, 0xF, 0xF, false));
+    v = mn(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xF, 0xF, false));
+    v = mn(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x118, 0xF, 0xF, false));
+    uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+    m = mn(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 31));
+    m = mn(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 47));
+    return mn(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 63));
+}
+
 // Minimum of v over all 64 lanes (every lane active), returned wave-uniform:
 // row_shr steps leave each row's minimum in its lane 15, and the four row
 // results are read out as scalars.

@@ -19,6 +19,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "lanes.h"
 #include "panel_order.h"
 
 namespace swann {
@@ -84,21 +85,49 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ X, i
 }
 
 // The spread of an fp32 corpus's row maxima: rng[0] the largest and rng[1] the
-// smallest max |x| of a row, as float bits (non-negative floats order as
-// ints; a NaN row reads as the largest).  rng starts at {0, INT_MAX}.
+// smallest max |x| of a row, as float bits.  Compared as integers: |x|'s bits
+// order as |x| does, and a NaN's bits lie above infinity's, so a row holding
+// a NaN reads as NaN, the largest, and fails the caller's range test.  rng
+// starts at {0, INT_MAX}.  Each wave takes rows in a grid stride, reading a
+// row as 16-byte vectors when vec4 (four in flight a lane, dim % 4 == 0 and
+// X 16-byte aligned) and keeping its own extremes: one pair of atomics a
+// wave, not a row.
+constexpr int kRangeBlocks = 4096;
+
 __global__ __launch_bounds__(256) void row_range(const float* __restrict__ X, int64_t n, int dim,
-                                                 int* __restrict__ rng) {
-    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                 int vec4, int* __restrict__ rng) {
     const int lane = threadIdx.x & 63;
-    if (r >= n) return;
-    const float* x = X + r * dim;
-    float m = 0.f;
-    for (int t = lane; t < dim; t += 64) m = fmaxf(m, fabsf(x[t]));
+    const int64_t w0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t stride = (int64_t)gridDim.x * 4;
+    uint32_t hi = 0, lo = 0x7fffffffu;
+    for (int64_t r = w0; r < n; r += stride) {
+        const float* x = X + r * dim;
+        uint32_t m = 0;
+        auto take = [&](float v) {
+            const uint32_t b = __float_as_uint(v) & 0x7fffffffu;
+            m = b > m ? b : m;
+        };
+        if (vec4) {
+            const float4* x4 = reinterpret_cast<const float4*>(x);
+            const int d4 = dim >> 2;
+            for (int t = lane; t < d4; t += 256) {
+                float4 v[4];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if (lane == 0) {
-        atomicMax(&rng[0], __float_as_int(m));
-        atomicMin(&rng[1], __float_as_int(m));
+                for (int j = 0; j < 4; ++j)
+                    v[j] = t + 64 * j < d4 ? x4[t + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { take(v[j].x); take(v[j].y); take(v[j].z); take(v[j].w); }
+            }
+        } else {
+            for (int t = lane; t < dim; t += 64) take(x[t]);
+        }
+        m = ~wave_min_u32(~m);
+        hi = m > hi ? m : hi;
+        lo = m < lo ? m : lo;
+    }
+    if (lane == 0 && w0 < n) {
+        atomicMax(&rng[0], (int)hi);
+        atomicMin(&rng[1], (int)lo);
     }
 }
 
@@ -1249,7 +1278,10 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         // the row maxima's range (in `scale`, unused until split_rows writes it)
         int* rng = (int*)scale;
         hipLaunchKernelGGL(range_init, dim3(1), dim3(64), 0, st, rng);
-        hipLaunchKernelGGL(row_range, dim3(nrb), dim3(256), 0, st, (const float*)X, n, dim, rng);
+        const int vec4 = dim % 4 == 0 && (uintptr_t)X % 16 == 0;
+        const unsigned nrr = (unsigned)(nrb < (unsigned)kRangeBlocks ? nrb : kRangeBlocks);
+        hipLaunchKernelGGL(row_range, dim3(nrr), dim3(256), 0, st, (const float*)X, n, dim, vec4,
+                           rng);
         int hr[2] = {0, 0};
         if (hipMemcpyAsync(hr, rng, sizeof(hr), hipMemcpyDeviceToHost, st) != hipSuccess ||
             hipStreamSynchronize(st) != hipSuccess) {

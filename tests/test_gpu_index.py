@@ -240,6 +240,43 @@ def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtyp
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
+@pytest.mark.parametrize("metric,spread", [(0, "wide"), (1, "wide"), (1, "tiny"), (1, "some")])
+def test_mfma_sweep_picks_the_row_scaled_plane_from_the_range(metric, spread):
+    """An fp32 corpus goes to fp16 unscaled only when every row's max |x| lies
+    in [2^-4, 2^14]; the sweep measures that range on the GPU (row_range,
+    several rows a wave).  A corpus scaled past fp16's range (x 3e5), far
+    below it (x 1e-6, subnormal in fp16) or with every 7th row past it must
+    go to the row-scaled plane: unscaled, those values overflow to inf or
+    keep a few bits, and the lists would not be the oracle's.  dim 64 reads
+    rows as 16-byte vectors, dim 66 element by element.  (A tiny corpus under
+    ip has every distance within an ulp of 1, ties that fp32 rounding order
+    decides, so it runs under l2.)"""
+    factor = {"wide": 3e5, "tiny": 1e-6, "some": 3e5}[spread]
+    for d in (64, 66):
+        n = 3001
+        X = gaussian(n, d, 441 + metric + d, metric == 0)
+        if metric == 1:
+            X = X * 3.0 + 1.5
+        if spread == "some":
+            X[::7] *= factor
+        else:
+            X *= factor
+        X = np.ascontiguousarray(X.astype(np.float32))
+        Xg = torch.from_numpy(X).cuda()
+        m = "ip" if metric == 0 else "l2"
+        note("mfma sweep plane choice", spread, m, d)
+        cand, cdist = B.knn_candidates(Xg, 40, metric=m)
+        oc, od = O.knn_candidates(X, 40, metric, nthreads=8)
+        same = (cand.cpu().numpy() == oc).mean()
+        note("mfma sweep plane choice agreement", spread, m, d, same)
+        assert same > 0.995
+        assert np.isfinite(cdist.cpu().numpy()).all()
+        # rounding of (|a|^2 + |b|^2) - 2 a.b in fp32 scales with the norms
+        nrm = (X.astype(np.float64) ** 2).sum(1)
+        scale = nrm[:, None] + nrm[oc] if metric == 1 else np.abs(od).max()
+        assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=4e-6 * scale)
+
+
 @pytest.mark.parametrize("sym", ["0", "1"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
