@@ -1109,11 +1109,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
 // appending list 1 and compacting again would keep, in the same order: an
 // entry among the C smallest of the whole is among the C smallest of its own
 // list, and whatever a first compaction drops has C entries ahead of it.
+// With seeds (below), a row under C entries keeps its seed as threshold.
 __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
                                                  int32_t* __restrict__ bid,
                                                  int32_t* __restrict__ bcnt,
                                                  float* __restrict__ gthr, int* ovf, int64_t n,
-                                                 int cap, int fcap, int C) {
+                                                 int cap, int fcap, int C,
+                                                 const float* __restrict__ seed) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= n) return;
     const int lane = threadIdx.x & 63;
@@ -1206,7 +1208,7 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
         eq_left -= used < eq_left ? used : eq_left;
     }
     if (lane == 0) {
-        gthr[r] = cnt >= C ? funkey(T) : INFINITY;
+        gthr[r] = cnt >= C ? funkey(T) : seed ? seed[r] : INFINITY;
         bcnt[r * 2] = w;
         bcnt[r * 2 + 1] = 0;
     }
@@ -1214,17 +1216,163 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 
 __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
                                                 int32_t* __restrict__ bcnt, int* ovf,
-                                                int64_t n) {
+                                                int64_t n, const float* __restrict__ seed) {
     const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (r < n) {
-        gthr[r] = INFINITY;
+        gthr[r] = seed ? seed[r] : INFINITY;
         bcnt[r * 2] = 0;
         bcnt[r * 2 + 1] = 0;
     }
     if (r == 0) *ovf = 0;
 }
 
+// ---------------------------------------------------------------------------
+// Seeds for the symmetric sweep's thresholds.  A row's threshold only falls
+// as the bands reach its neighbours; until then it appends much of what it
+// sees.  A short pre-pass gives every row a bound first: rows are put in a
+// locality order (grouped by the nearest of P evenly spaced pivot rows,
+// measured on a 64-coordinate sketch), the tiles within kSeedBand panels of
+// the diagonal of that ordered copy are swept, and each row's resulting
+// threshold -- the C-th best of real distances, so an upper bound of its
+// true C-th -- seeds the main sweep, which runs on the rows in their own
+// order.  A seed holds back (in both directions) only candidates that could
+// not be among the row's C best, so the lists come out as without it.  The
+// margin added to a seed (2^-16 of |t| + |x|^2) lies far above any
+// difference in how the accumulators round the same pair in another tile
+// position.  (Sweeping in the ordered copy itself would concentrate each
+// row's survivors in few tiles, but a row whose seed stayed loose then
+// meets its neighbours in one burst that can overflow its second list.)
+constexpr int kSketch = 64;          // sketch coordinates a row
+constexpr int kMaxPivots = 1024;
+constexpr int kPivChunk = 256;       // pivots staged in LDS at a time (64 KB)
+constexpr int64_t kSeedBand = 4;     // the pre-pass scores tiles (I, I + b), b < kSeedBand
+
+// Coordinates l * dim / 64 of each row, as float (zeros past dim).
+template <typename XT>
+__global__ __launch_bounds__(256) void row_sketch(const XT* __restrict__ X, int64_t n, int dim,
+                                                  float* __restrict__ sk) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= n) return;
+    const int l = threadIdx.x & 63;
+    const int k = dim >= kSketch ? (int)(((int64_t)l * dim) / kSketch) : l;
+    sk[r * kSketch + l] = k < dim ? (float)X[r * (int64_t)dim + k] : 0.f;
+}
+
+// Each row's nearest pivot on the sketch (pivot p is row p * n / P; ties to
+// the lower p), and the rows per pivot.  One thread a row; the pivots'
+// sketches are staged in LDS, kPivChunk at a time, read by every lane at
+// once (broadcast).
+__global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ sk, int64_t n,
+                                                     int P, int* __restrict__ lab,
+                                                     int* __restrict__ pcnt) {
+    __shared__ __align__(16) float sp[kPivChunk * kSketch];
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool ok = r < n;
+    float x[kSketch];
+#pragma unroll
+    for (int k = 0; k < kSketch; k += 4) {
+        const float4 v = ok ? *reinterpret_cast<const float4*>(sk + r * kSketch + k)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[k] = v.x; x[k + 1] = v.y; x[k + 2] = v.z; x[k + 3] = v.w;
+    }
+    float best = INFINITY;
+    int bi = 0;
+    for (int p0 = 0; p0 < P; p0 += kPivChunk) {
+        const int pc = P - p0 < kPivChunk ? P - p0 : kPivChunk;
+        __syncthreads();
+        for (int i = threadIdx.x; i < pc * kSketch; i += 256) {
+            const int64_t pr = (int64_t)(p0 + i / kSketch) * n / P;
+            sp[i] = sk[pr * kSketch + i % kSketch];
+        }
+        __syncthreads();
+        for (int p = 0; p < pc; ++p) {
+            const float4* s4 = reinterpret_cast<const float4*>(sp + p * kSketch);
+            float d = 0.f;
+#pragma unroll
+            for (int k = 0; k < kSketch / 4; ++k) {
+                const float4 v = s4[k];
+                float t;
+                t = x[4 * k] - v.x; d = __builtin_fmaf(t, t, d);
+                t = x[4 * k + 1] - v.y; d = __builtin_fmaf(t, t, d);
+                t = x[4 * k + 2] - v.z; d = __builtin_fmaf(t, t, d);
+                t = x[4 * k + 3] - v.w; d = __builtin_fmaf(t, t, d);
+            }
+            if (d < best) { best = d; bi = p0 + p; }
+        }
+    }
+    if (ok) {
+        lab[r] = bi;
+        atomicAdd(&pcnt[bi], 1);
+    }
+}
+
+__global__ void fill_zero(int* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+// Exclusive scan of the P <= 1024 counts in place: each pivot's first slot.
+__global__ __launch_bounds__(1024) void pivot_scan(int* pcnt, int P) {
+    __shared__ int s[kMaxPivots];
+    const int t = threadIdx.x;
+    const int v = t < P ? pcnt[t] : 0;
+    s[t] = v;
+    __syncthreads();
+    for (int off = 1; off < kMaxPivots; off <<= 1) {
+        const int u = t >= off ? s[t - off] : 0;
+        __syncthreads();
+        s[t] += u;
+        __syncthreads();
+    }
+    if (t < P) pcnt[t] = s[t] - v;
+}
+
+// perm[i]: the row at position i of the locality order (rows of one pivot
+// together, in no particular order among themselves).
+__global__ void pivot_place(const int* __restrict__ lab, int64_t n, int* pcur,
+                            int* __restrict__ perm) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n) perm[atomicAdd(&pcur[lab[r]], 1)] = (int)r;
+}
+
+// The ordered copy: row perm[i] of the plane, its norm and scale at i.
+__global__ __launch_bounds__(256) void gather_rows(const _Float16* __restrict__ h, int64_t n,
+                                                   int dim, const int* __restrict__ perm,
+                                                   const float* __restrict__ xn,
+                                                   const float* __restrict__ sc,
+                                                   _Float16* __restrict__ hp,
+                                                   float* __restrict__ xnp,
+                                                   float* __restrict__ scp) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (i >= n) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = perm[i];
+    const uint4* src = reinterpret_cast<const uint4*>(h + r * dim);
+    uint4* dst = reinterpret_cast<uint4*>(hp + i * dim);
+    for (int t = lane; t < dim / 8; t += 64) dst[t] = src[t];
+    if (lane == 0) {
+        xnp[i] = xn[r];
+        if (sc) scp[i] = sc[r];
+    }
+}
+
+// seed[perm[i]]: ordered row i's pre-pass threshold plus the margin, or +inf
+// where the pre-pass left it under C entries.
+__global__ void seed_map(const float* __restrict__ gthr, const int* __restrict__ perm,
+                         const float* __restrict__ xn, int64_t n, float* __restrict__ seed) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float t = gthr[i];
+    const int r = perm[i];
+    seed[r] = t < INFINITY ? t + (fabsf(t) + fabsf(xn[r])) * (1.f / 65536.f) + 1e-30f : INFINITY;
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
+
+inline int64_t seed_bytes(int64_t n, int dim) {
+    return al256(n * kSketch * 4) + al256(n * 4) * 6 + al256(kMaxPivots * 4) +
+           al256(n * (int64_t)dim * 2);
+}
 
 // Widest band of the symmetric sweep.  Wider bands mean fewer launches and
 // merges but staler column thresholds (more foreign appends); with the
@@ -1315,9 +1463,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             // starts from thresholds over everything scored so far.  Two lists
             // a row.
             float* gthr = (float*)extra; extra += al256(n * 4);
-            int* ovf = (int*)extra;
-            hipLaunchKernelGGL(sym_init, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gthr,
-                               bcnt, ovf, n);
+            int* ovf = (int*)extra; extra += 256;
             MfmaSweepArgs s = a;
             s.splits = 2;
             s.sym = 1;
@@ -1328,23 +1474,73 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 const int f = atoi(e);
                 if (f >= 1 && f < cap) s.fcap = f;
             }
-            for (int64_t b0 = 0; b0 < ntile;) {
-                const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
-                s.b0 = b0;
-                s.b1 = b0 + B < ntile ? b0 + B : ntile;
-                const unsigned grid = (unsigned)(ntile - b0);
-                if (scaled) {
-                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(grid), dim3(1024), 0, st, s);
-                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(grid), dim3(1024), 0, st, s);
-                } else {
-                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(grid), dim3(1024), 0, st, s);
-                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(grid), dim3(1024), 0, st, s);
+            // the launches of bands [b0, bend), each followed by a merge
+            auto bands = [&](MfmaSweepArgs& sa, int64_t bend, const float* seed) -> int {
+                for (int64_t b0 = 0; b0 < bend;) {
+                    const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
+                    sa.b0 = b0;
+                    sa.b1 = b0 + B < bend ? b0 + B : bend;
+                    const unsigned grid = (unsigned)(ntile - b0);
+                    if (scaled) {
+                        if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(grid), dim3(1024), 0, st, sa);
+                        else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(grid), dim3(1024), 0, st, sa);
+                    } else {
+                        if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(grid), dim3(1024), 0, st, sa);
+                        else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(grid), dim3(1024), 0, st, sa);
+                    }
+                    hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
+                                       bkey, bid, bcnt, gthr, ovf, n, cap, sa.fcap, C, seed);
+                    const int rc = launch_status("sweep (mfma, symmetric)");
+                    if (rc) return rc;
+                    b0 = sa.b1;
                 }
-                hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, bkey,
-                                   bid, bcnt, gthr, ovf, n, cap, s.fcap, C);
-                const int rc = launch_status("sweep (mfma, symmetric)");
+                return SWANN_OK;
+            };
+            const unsigned nb256 = (unsigned)((n + 255) / 256);
+            float* seed = nullptr;
+            if (ntile > 2 * kSeedBand && !getenv_flag("SWANN_SWEEP_NOSEED")) {
+                // the pre-pass (seed_bytes of workspace)
+                float* sk = (float*)extra; extra += al256(n * kSketch * 4);
+                int* lab = (int*)extra; extra += al256(n * 4);
+                int* perm = (int*)extra; extra += al256(n * 4);
+                seed = (float*)extra; extra += al256(n * 4);
+                float* xnp = (float*)extra; extra += al256(n * 4);
+                float* scp = (float*)extra; extra += al256(n * 4) * 2;
+                int* pcnt = (int*)extra; extra += al256(kMaxPivots * 4);
+                _Float16* hp = (_Float16*)extra; extra += al256(n * (int64_t)dim * 2);
+                const int64_t pw = n / 1024;
+                const int P = (int)(pw < 1 ? 1 : pw > kMaxPivots ? kMaxPivots : pw);
+                if (x_dtype == SWANN_DTYPE_F16)
+                    hipLaunchKernelGGL(row_sketch<_Float16>, dim3(nrb), dim3(256), 0, st,
+                                       (const _Float16*)X, n, dim, sk);
+                else
+                    hipLaunchKernelGGL(row_sketch<float>, dim3(nrb), dim3(256), 0, st,
+                                       (const float*)X, n, dim, sk);
+                hipLaunchKernelGGL(fill_zero, dim3(kMaxPivots / 256), dim3(256), 0, st, pcnt,
+                                   kMaxPivots);
+                hipLaunchKernelGGL(nearest_pivot, dim3(nb256), dim3(256), 0, st, sk, n, P, lab,
+                                   pcnt);
+                hipLaunchKernelGGL(pivot_scan, dim3(1), dim3(1024), 0, st, pcnt, P);
+                hipLaunchKernelGGL(pivot_place, dim3(nb256), dim3(256), 0, st, lab, n, pcnt, perm);
+                hipLaunchKernelGGL(gather_rows, dim3(nrb), dim3(256), 0, st, hi, n, dim, perm, xn,
+                                   scaled ? scale : nullptr, hp, xnp, scp);
+                hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
+                                   (const float*)nullptr);
+                MfmaSweepArgs pre = s;
+                pre.hi = hp;
+                pre.xn = xnp;
+                pre.scale = scp;
+                int rc = launch_status("sweep (mfma, seed order)");
                 if (rc) return rc;
-                b0 = s.b1;
+                rc = bands(pre, kSeedBand, nullptr);
+                if (rc) return rc;
+                hipLaunchKernelGGL(seed_map, dim3(nb256), dim3(256), 0, st, gthr, perm, xn, n, seed);
+            }
+            hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
+                               (const float*)seed);
+            {
+                const int rc = bands(s, ntile, seed);
+                if (rc) return rc;
             }
             // a list that overflowed lost candidates: redo the sweep the
             // one-sided way (one small read-back; the build is not on the
@@ -1391,11 +1587,12 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     return launch_status("sweep (mfma)");
 }
 
-// Extra workspace: norms, scales, (fp32 corpus) the fp16 plane, and the
-// symmetric sweep's thresholds and overflow count.
+// Extra workspace: norms, scales, (fp32 corpus) the fp16 plane, the
+// symmetric sweep's thresholds and overflow count, and its seed pre-pass.
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
-    return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) + al256(n * 4) + 256;
+    return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) + al256(n * 4) + 256 +
+           seed_bytes(n, dim);
 }
 
 // Column splits of the direct-load sweep: enough workgroups to give every
