@@ -26,7 +26,7 @@ int sweep_mfma_cap(int C);
 int sweep_mfma_splits(int64_t n, int dim);
 int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
                    int splits, float* bkey, int32_t* bid, int32_t* bcnt, char* extra,
-                   hipStream_t st, int* used);
+                   hipStream_t st, int* used, const int32_t** perm_out);
 
 namespace {
 
@@ -220,15 +220,20 @@ __global__ __launch_bounds__(256) void sweep_kernel(SweepArgs a) {
 
 // Sort each row's survivors and emit the first C.  A row has G lists
 // (column splits of the sweep) of up to `cap` entries at (r * G + s) * cap;
-// they are gathered in split order and sorted together.
+// they are gathered in split order and sorted together.  With perm (the
+// sweep ran on the rows in that order), list r is row perm[r]'s and an id j
+// means row perm[j]: ids are mapped before the (d, id) sort, so ties order
+// by the rows' own ids, and the row is written at perm[r].
 __global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bkey,
                                                    const int32_t* __restrict__ bid,
                                                    const int32_t* __restrict__ bcnt, int64_t n,
                                                    int cap, int G, int C, int pad_self,
+                                                   const int32_t* __restrict__ perm,
                                                    int32_t* __restrict__ cand,
                                                    float* __restrict__ cdist) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int64_t r = blockIdx.x;
+    const int64_t ro = perm ? (int64_t)perm[r] : r;       // the row written
     int segc[8], cnt = 0;
     for (int sg = 0; sg < 8; ++sg) {
         segc[sg] = sg < G ? bcnt[r * G + sg] : 0;
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bke
         const bool real = i < cnt;
         const int64_t at = (r * G + sg) * (int64_t)cap + off;
         sd[i] = real ? bkey[at] : INFINITY;
-        si[i] = real ? bid[at] : INT32_MAX;
+        si[i] = real ? (perm ? perm[bid[at]] : bid[at]) : INT32_MAX;
     }
     __syncthreads();
     for (int size = 2; size <= np; size <<= 1)
@@ -267,8 +272,8 @@ __global__ __launch_bounds__(256) void sweep_final(const float* __restrict__ bke
     for (int t = threadIdx.x; t < C; t += 256) {
         const bool ok = t < cnt;
         const bool self = pad_self && t == cnt;
-        cand[r * C + t] = ok ? si[t] : self ? (int32_t)r : -1;
-        cdist[r * C + t] = ok ? sd[t] : self ? kSelf : INFINITY;
+        cand[ro * C + t] = ok ? si[t] : self ? (int32_t)ro : -1;
+        cdist[ro * C + t] = ok ? sd[t] : self ? kSelf : INFINITY;
     }
 }
 
@@ -1073,9 +1078,10 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     char* extra = ws;
     int rc;
     int Gu = 1;                      // lists per row the sweep filled
+    const int32_t* perm = nullptr;   // the sweep's row order, when not the rows' own
     if (mf) {
         rc = sweep_mfma_run(X, x_dtype, n, dim, metric, Cs, cap, G, bkey, bid, bcnt, extra, st,
-                            &Gu);
+                            &Gu, &perm);
     } else {
         const unsigned nb = (unsigned)((n + 3) / 4);
         if (metric == SWANN_METRIC_L2)
@@ -1096,11 +1102,11 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     while (np < most) np <<= 1;
     if (Cs == C) {
         hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
-                           bcnt, n, cap, Gu, C, mf ? 1 : 0, cand, cdist);
+                           bcnt, n, cap, Gu, C, mf ? 1 : 0, perm, cand, cdist);
         return launch_status("sweep final");
     }
     hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
-                       bcnt, n, cap, Gu, Cs, mf ? 1 : 0, scand, scd);
+                       bcnt, n, cap, Gu, Cs, mf ? 1 : 0, perm, scand, scd);
     rc = launch_status("sweep final");
     if (rc) return rc;
     // the re-rank's row order, in the sweep's lists (free once sweep_final has

@@ -18,6 +18,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <vector>
+
 #include "common.h"
 #include "lanes.h"
 #include "panel_order.h"
@@ -187,6 +189,10 @@ struct MfmaSweepArgs {
     const float* gthr;           // [n] a row's threshold when the launch began
     int* ovf;                    // foreign appends that found no room
     int fcap;                    // room in list 1 (<= cap; smaller only as a test hook)
+    // one-sided sweep of listed row panels only (the repair of rows whose
+    // second list overflowed): workgroup g takes panel plist[g / G]
+    const int* plist;
+    int npl;
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -813,8 +819,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     // its rows and starts from the thresholds and lists the last merge left;
     // sym_panel spreads the band's short panels over the XCDs
     const int lid = a.sym ? sym_panel((int)blockIdx.x, (int)gridDim.x, (int)(a.b1 - a.b0))
-                          : (int)xcd_remap(blockIdx.x, (int64_t)ntile * G);
-    const int r0 = (a.sym ? lid : lid / G) * kBM2;
+                          : (int)xcd_remap(blockIdx.x, (int64_t)(a.plist ? a.npl : ntile) * G);
+    const int r0 = (a.sym ? lid : a.plist ? a.plist[lid / G] : lid / G) * kBM2;
     const int split = a.sym ? 0 : lid % G;
 
     if (tid < kBM2) {
@@ -1115,7 +1121,8 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
                                                  int32_t* __restrict__ bcnt,
                                                  float* __restrict__ gthr, int* ovf, int64_t n,
                                                  int cap, int fcap, int C,
-                                                 const float* __restrict__ seed) {
+                                                 const float* __restrict__ seed,
+                                                 int* __restrict__ flag) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= n) return;
     const int lane = threadIdx.x & 63;
@@ -1125,8 +1132,11 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
     const int32_t* i1 = i0 + cap;
     const int c0 = __builtin_amdgcn_readfirstlane(bcnt[r * 2]);
     int c1 = __builtin_amdgcn_readfirstlane(bcnt[r * 2 + 1]);
-    if (c1 > fcap) {                     // appends were dropped: the caller redoes the sweep
-        if (lane == 0) atomicAdd(ovf, 1);
+    if (c1 > fcap) {                     // appends were dropped: the caller redoes the row
+        if (lane == 0) {
+            atomicAdd(ovf, 1);
+            if (flag) flag[r] = 1;
+        }
         c1 = fcap;
     }
     const int cnt = c0 + c1;
@@ -1243,9 +1253,11 @@ __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
 // row's survivors in few tiles, but a row whose seed stayed loose then
 // meets its neighbours in one burst that can overflow its second list.)
 constexpr int kSketch = 64;          // sketch coordinates a row
-constexpr int kMaxPivots = 1024;
+constexpr int kMaxPivots = 2048;
 constexpr int kPivChunk = 256;       // pivots staged in LDS at a time (64 KB)
 constexpr int64_t kSeedBand = 4;     // the pre-pass scores tiles (I, I + b), b < kSeedBand
+constexpr int kKmeanSteps = 2;       // refinements of the pivots' sketches
+constexpr float kClusterRatio = 0.3f;  // nearest-pivot / arbitrary-pivot distance for an order
 
 // Coordinates l * dim / 64 of each row, as float (zeros past dim).
 template <typename XT>
@@ -1262,12 +1274,20 @@ __global__ __launch_bounds__(256) void row_sketch(const XT* __restrict__ X, int6
 // the lower p), and the rows per pivot.  One thread a row; the pivots'
 // sketches are staged in LDS, kPivChunk at a time, read by every lane at
 // once (broadcast).
+// With acc, also adds up (over all rows) the distance to the nearest pivot
+// and to pivot r % P, a stand-in for an arbitrary one: their ratio says how
+// clustered the rows are.
 __global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ sk, int64_t n,
-                                                     int P, int* __restrict__ lab,
-                                                     int* __restrict__ pcnt) {
+                                                     int P, const float* __restrict__ psk,
+                                                     int* __restrict__ lab,
+                                                     int* __restrict__ pcnt,
+                                                     float* __restrict__ acc) {
     __shared__ __align__(16) float sp[kPivChunk * kSketch];
+    __shared__ float red[2][4];
     const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const bool ok = r < n;
+    const int pr = (int)(r % P);
+    float drand = 0.f;
     float x[kSketch];
 #pragma unroll
     for (int k = 0; k < kSketch; k += 4) {
@@ -1281,8 +1301,12 @@ __global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ s
         const int pc = P - p0 < kPivChunk ? P - p0 : kPivChunk;
         __syncthreads();
         for (int i = threadIdx.x; i < pc * kSketch; i += 256) {
-            const int64_t pr = (int64_t)(p0 + i / kSketch) * n / P;
-            sp[i] = sk[pr * kSketch + i % kSketch];
+            if (psk) {
+                sp[i] = psk[(int64_t)p0 * kSketch + i];
+            } else {
+                const int64_t pr = (int64_t)(p0 + i / kSketch) * n / P;
+                sp[i] = sk[pr * kSketch + i % kSketch];
+            }
         }
         __syncthreads();
         for (int p = 0; p < pc; ++p) {
@@ -1298,11 +1322,27 @@ __global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ s
                 t = x[4 * k + 3] - v.w; d = __builtin_fmaf(t, t, d);
             }
             if (d < best) { best = d; bi = p0 + p; }
+            if (p0 + p == pr) drand = d;
         }
     }
     if (ok) {
         lab[r] = bi;
         atomicAdd(&pcnt[bi], 1);
+    }
+    if (acc) {
+        float b0 = ok ? best : 0.f, b1 = ok ? drand : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            b0 += __shfl_xor(b0, off, 64);
+            b1 += __shfl_xor(b1, off, 64);
+        }
+        const int wv = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) { red[0][wv] = b0; red[1][wv] = b1; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            atomicAdd(&acc[0], red[0][0] + red[0][1] + red[0][2] + red[0][3]);
+            atomicAdd(&acc[1], red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+        }
     }
 }
 
@@ -1311,20 +1351,69 @@ __global__ void fill_zero(int* p, int n) {
     if (i < n) p[i] = 0;
 }
 
-// Exclusive scan of the P <= 1024 counts in place: each pivot's first slot.
-__global__ __launch_bounds__(1024) void pivot_scan(int* pcnt, int P) {
+// Exclusive scan of the P <= 2048 counts: each pivot's first slot, into
+// pstart (P + 1 entries, the last n) and into pcnt (the cursor pivot_place
+// advances).
+__global__ __launch_bounds__(1024) void pivot_scan(int* pcnt, int* pstart, int P) {
     __shared__ int s[kMaxPivots];
     const int t = threadIdx.x;
-    const int v = t < P ? pcnt[t] : 0;
-    s[t] = v;
+    const int v0 = 2 * t < P ? pcnt[2 * t] : 0, v1 = 2 * t + 1 < P ? pcnt[2 * t + 1] : 0;
+    s[t] = v0 + v1;
     __syncthreads();
-    for (int off = 1; off < kMaxPivots; off <<= 1) {
+    for (int off = 1; off < 1024; off <<= 1) {
         const int u = t >= off ? s[t - off] : 0;
         __syncthreads();
         s[t] += u;
         __syncthreads();
     }
-    if (t < P) pcnt[t] = s[t] - v;
+    const int e = s[t] - v0 - v1;                  // exclusive start of the pair
+    if (2 * t < P) { pcnt[2 * t] = e; if (pstart) pstart[2 * t] = e; }
+    if (2 * t + 1 < P) { pcnt[2 * t + 1] = e + v0; if (pstart) pstart[2 * t + 1] = e + v0; }
+    if (pstart && t == 1023) pstart[P] = s[t];
+}
+
+// The mean sketch of each pivot's rows (rows perm[pstart[p] .. pstart[p+1])):
+// one workgroup a pivot, one thread a coordinate; a pivot with no rows keeps
+// its sketch.
+__global__ __launch_bounds__(kSketch) void group_mean(const float* __restrict__ sk,
+                                                      const int* __restrict__ perm,
+                                                      const int* __restrict__ pstart,
+                                                      float* __restrict__ psk) {
+    const int p = blockIdx.x, k = threadIdx.x;
+    const int b = pstart[p], e = pstart[p + 1];
+    if (e <= b) return;
+    float acc = 0.f;
+    for (int i = b; i < e; ++i) acc += sk[(int64_t)perm[i] * kSketch + k];
+    psk[(int64_t)p * kSketch + k] = acc / (float)(e - b);
+}
+
+// The pivots' initial sketches: rows p * n / P.
+__global__ void pivot_init(const float* __restrict__ sk, int64_t n, int P, float* __restrict__ psk) {
+    const int p = blockIdx.x, k = threadIdx.x;
+    psk[(int64_t)p * kSketch + k] = sk[((int64_t)p * n / P) * kSketch + k];
+}
+
+// Squared sketch distances between pivots: D[p][q].
+__global__ void pivot_dist(const float* __restrict__ psk, int P, float* __restrict__ D) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)P * P) return;
+    const int p = (int)(i / P), q = (int)(i % P);
+    float d = 0.f;
+    for (int k = 0; k < kSketch; ++k) {
+        const float t = psk[(int64_t)p * kSketch + k] - psk[(int64_t)q * kSketch + k];
+        d = __builtin_fmaf(t, t, d);
+    }
+    D[i] = d;
+}
+
+// Rows' sort key: their pivot's place in the chain.
+__global__ void relabel(int* __restrict__ lab, int64_t n, const int* __restrict__ rank,
+                        int* __restrict__ pcnt) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= n) return;
+    const int v = rank[lab[r]];
+    lab[r] = v;
+    atomicAdd(&pcnt[v], 1);
 }
 
 // perm[i]: the row at position i of the locality order (rows of one pivot
@@ -1367,11 +1456,35 @@ __global__ void seed_map(const float* __restrict__ gthr, const int* __restrict__
     seed[r] = t < INFINITY ? t + (fabsf(t) + fabsf(xn[r])) * (1.f / 65536.f) + 1e-30f : INFINITY;
 }
 
+// seed[i]: ordered row i's pre-pass threshold plus the margin (the sweep in
+// locality order keeps its rows in that order).
+__global__ void seed_widen(const float* __restrict__ gthr, const float* __restrict__ xn,
+                           int64_t n, float* __restrict__ seed) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float t = gthr[i];
+    seed[i] = t < INFINITY ? t + (fabsf(t) + fabsf(xn[i])) * (1.f / 65536.f) + 1e-30f : INFINITY;
+}
+
+// The row panels holding a flagged row (one thread a panel), listed in plist
+// with their count in *npl.
+__global__ void flag_panels(const int* __restrict__ flag, int64_t n, int ntile,
+                            int* __restrict__ plist, int* npl) {
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= ntile) return;
+    int any = 0;
+    for (int64_t r = (int64_t)p * kBM2; r < n && r < (int64_t)(p + 1) * kBM2; ++r) any |= flag[r];
+    if (any) plist[atomicAdd(npl, 1)] = p;
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 inline int64_t seed_bytes(int64_t n, int dim) {
-    return al256(n * kSketch * 4) + al256(n * 4) * 6 + al256(kMaxPivots * 4) +
-           al256(n * (int64_t)dim * 2);
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    return al256(n * kSketch * 4) + al256(n * 4) * 7 + al256(kMaxPivots * 4) +
+           al256(n * (int64_t)dim * 2) + al256(ntile * 4) + 256 +
+           al256((int64_t)kMaxPivots * kSketch * 4) + al256((kMaxPivots + 1) * 4) +
+           al256((int64_t)kMaxPivots * kMaxPivots * 4) + al256(kMaxPivots * 4);
 }
 
 // Widest band of the symmetric sweep.  Wider bands mean fewer launches and
@@ -1411,7 +1524,8 @@ inline int sweep_waves() {
 // fills one), which is what the merge must read.
 int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, int C, int cap,
                    int splits, float* bkey, int32_t* bid, int32_t* bcnt, char* extra,
-                   hipStream_t st, int* used) {
+                   hipStream_t st, int* used, const int32_t** perm_out) {
+    *perm_out = nullptr;
     float* xn = (float*)extra; extra += al256(n * 4);
     float* scale = (float*)extra; extra += al256(n * 4);
     const _Float16* hi;
@@ -1475,7 +1589,8 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 if (f >= 1 && f < cap) s.fcap = f;
             }
             // the launches of bands [b0, bend), each followed by a merge
-            auto bands = [&](MfmaSweepArgs& sa, int64_t bend, const float* seed) -> int {
+            auto bands = [&](MfmaSweepArgs& sa, int64_t bend, const float* seed,
+                             int* flag) -> int {
                 for (int64_t b0 = 0; b0 < bend;) {
                     const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
                     sa.b0 = b0;
@@ -1489,7 +1604,8 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(grid), dim3(1024), 0, st, sa);
                     }
                     hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
-                                       bkey, bid, bcnt, gthr, ovf, n, cap, sa.fcap, C, seed);
+                                       bkey, bid, bcnt, gthr, ovf, n, cap, sa.fcap, C, seed,
+                                       flag);
                     const int rc = launch_status("sweep (mfma, symmetric)");
                     if (rc) return rc;
                     b0 = sa.b1;
@@ -1498,7 +1614,12 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             };
             const unsigned nb256 = (unsigned)((n + 255) / 256);
             float* seed = nullptr;
+            int* flag = nullptr;         // rows whose second list overflowed (ordered sweep)
+            int* plist = nullptr;
+            int* npl = nullptr;
+            const int32_t* ordered = nullptr;
             if (ntile > 2 * kSeedBand && !getenv_flag("SWANN_SWEEP_NOSEED")) {
+                bool clustered = false;
                 // the pre-pass (seed_bytes of workspace)
                 float* sk = (float*)extra; extra += al256(n * kSketch * 4);
                 int* lab = (int*)extra; extra += al256(n * 4);
@@ -1508,7 +1629,14 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 float* scp = (float*)extra; extra += al256(n * 4) * 2;
                 int* pcnt = (int*)extra; extra += al256(kMaxPivots * 4);
                 _Float16* hp = (_Float16*)extra; extra += al256(n * (int64_t)dim * 2);
-                const int64_t pw = n / 1024;
+                flag = (int*)extra; extra += al256(n * 4);
+                plist = (int*)extra; extra += al256(ntile * 4);
+                npl = (int*)extra; extra += 256;
+                float* psk = (float*)extra; extra += al256((int64_t)kMaxPivots * kSketch * 4);
+                int* pstart = (int*)extra; extra += al256((kMaxPivots + 1) * 4);
+                float* pd = (float*)extra; extra += al256((int64_t)kMaxPivots * kMaxPivots * 4);
+                int* prank = (int*)extra; extra += al256(kMaxPivots * 4);
+                const int64_t pw = n / 512;
                 const int P = (int)(pw < 1 ? 1 : pw > kMaxPivots ? kMaxPivots : pw);
                 if (x_dtype == SWANN_DTYPE_F16)
                     hipLaunchKernelGGL(row_sketch<_Float16>, dim3(nrb), dim3(256), 0, st,
@@ -1516,12 +1644,86 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 else
                     hipLaunchKernelGGL(row_sketch<float>, dim3(nrb), dim3(256), 0, st,
                                        (const float*)X, n, dim, sk);
-                hipLaunchKernelGGL(fill_zero, dim3(kMaxPivots / 256), dim3(256), 0, st, pcnt,
-                                   kMaxPivots);
-                hipLaunchKernelGGL(nearest_pivot, dim3(nb256), dim3(256), 0, st, sk, n, P, lab,
-                                   pcnt);
-                hipLaunchKernelGGL(pivot_scan, dim3(1), dim3(1024), 0, st, pcnt, P);
-                hipLaunchKernelGGL(pivot_place, dim3(nb256), dim3(256), 0, st, lab, n, pcnt, perm);
+                hipLaunchKernelGGL(pivot_init, dim3(P), dim3(kSketch), 0, st, sk, n, P, psk);
+                // two k-means steps on the sketches, then the final grouping;
+                // after the first assignment, rows that do not cluster (mean
+                // distance to the nearest pivot above kClusterRatio of that to
+                // an arbitrary one) gain nothing from an order or seeds: the
+                // sweep then runs plain
+                float* cacc = (float*)npl + 2;
+                for (int it = 0; it <= kKmeanSteps; ++it) {
+                    hipLaunchKernelGGL(fill_zero, dim3(kMaxPivots / 256), dim3(256), 0, st, pcnt,
+                                       kMaxPivots);
+                    if (it == 0)
+                        hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)cacc, 2);
+                    hipLaunchKernelGGL(nearest_pivot, dim3(nb256), dim3(256), 0, st, sk, n, P,
+                                       (const float*)psk, lab, pcnt, it == 0 ? cacc : nullptr);
+                    if (it == 0) {
+                        float ca[2] = {0.f, 0.f};
+                        if (hipMemcpyAsync(ca, cacc, sizeof(ca), hipMemcpyDeviceToHost, st) !=
+                                hipSuccess ||
+                            hipStreamSynchronize(st) != hipSuccess) {
+                            set_error("sweep (mfma): reading the clustering ratio failed");
+                            return SWANN_E_LAUNCH;
+                        }
+                        if (!(ca[0] < kClusterRatio * ca[1])) break;
+                        clustered = true;
+                    }
+                    hipLaunchKernelGGL(pivot_scan, dim3(1), dim3(1024), 0, st, pcnt, pstart, P);
+                    hipLaunchKernelGGL(pivot_place, dim3(nb256), dim3(256), 0, st, lab, n, pcnt,
+                                       perm);
+                    if (it < kKmeanSteps)
+                        hipLaunchKernelGGL(group_mean, dim3(P), dim3(kSketch), 0, st, sk,
+                                           (const int*)perm, (const int*)pstart, psk);
+                }
+                const char* oe = getenv("SWANN_SWEEP_ORDER");
+                const bool in_order = clustered && !(oe && *oe == '0');
+                if (in_order) {
+                    // pivots chained nearest to nearest (on the host: P^2
+                    // distances), rows ordered by their pivot's place in it
+                    hipLaunchKernelGGL(pivot_dist, dim3((unsigned)(((int64_t)P * P + 255) / 256)),
+                                       dim3(256), 0, st, (const float*)psk, P, pd);
+                    std::vector<float> dh((size_t)P * P);
+                    std::vector<int> rank(P), seen(P, 0);
+                    if (hipMemcpyAsync(dh.data(), pd, dh.size() * 4, hipMemcpyDeviceToHost, st) !=
+                            hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma): reading the pivot distances failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    int cur = 0;
+                    seen[0] = 1;
+                    rank[0] = 0;
+                    for (int i = 1; i < P; ++i) {
+                        int best = -1;
+                        float bd = INFINITY;
+                        const float* row = dh.data() + (size_t)cur * P;
+                        for (int q = 0; q < P; ++q)
+                            if (!seen[q] && (best < 0 || row[q] < bd)) { best = q; bd = row[q]; }
+                        seen[best] = 1;
+                        rank[best] = i;
+                        cur = best;
+                    }
+                    if (hipMemcpyAsync(prank, rank.data(), (size_t)P * 4, hipMemcpyHostToDevice,
+                                       st) != hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma): writing the pivot chain failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    hipLaunchKernelGGL(fill_zero, dim3(kMaxPivots / 256), dim3(256), 0, st, pcnt,
+                                       kMaxPivots);
+                    hipLaunchKernelGGL(relabel, dim3(nb256), dim3(256), 0, st, lab, n,
+                                       (const int*)prank, pcnt);
+                    hipLaunchKernelGGL(pivot_scan, dim3(1), dim3(1024), 0, st, pcnt,
+                                       (int*)nullptr, P);
+                    hipLaunchKernelGGL(pivot_place, dim3(nb256), dim3(256), 0, st, lab, n, pcnt,
+                                       perm);
+                }
+                if (!clustered) {
+                    seed = nullptr;
+                    flag = nullptr;
+                    goto plain;
+                }
                 hipLaunchKernelGGL(gather_rows, dim3(nrb), dim3(256), 0, st, hi, n, dim, perm, xn,
                                    scaled ? scale : nullptr, hp, xnp, scp);
                 hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
@@ -1532,14 +1734,27 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 pre.scale = scp;
                 int rc = launch_status("sweep (mfma, seed order)");
                 if (rc) return rc;
-                rc = bands(pre, kSeedBand, nullptr);
+                rc = bands(pre, kSeedBand, nullptr, nullptr);
                 if (rc) return rc;
-                hipLaunchKernelGGL(seed_map, dim3(nb256), dim3(256), 0, st, gthr, perm, xn, n, seed);
+                if (in_order) {
+                    // the main sweep in the locality order too: seeds stay in
+                    // that order, the lists come out in ordered ids
+                    hipLaunchKernelGGL(seed_widen, dim3(nb256), dim3(256), 0, st, gthr, xnp, n,
+                                       seed);
+                    hipLaunchKernelGGL(fill_zero, dim3(nb256), dim3(256), 0, st, flag, (int)n);
+                    s = pre;
+                    ordered = perm;
+                } else {
+                    hipLaunchKernelGGL(seed_map, dim3(nb256), dim3(256), 0, st, gthr, perm, xn, n,
+                                       seed);
+                    flag = nullptr;
+                }
             }
+        plain:
             hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
                                (const float*)seed);
             {
-                const int rc = bands(s, ntile, seed);
+                const int rc = bands(s, ntile, seed, flag);
                 if (rc) return rc;
             }
             // a list that overflowed lost candidates: redo the sweep the
@@ -1554,6 +1769,42 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             }
             if (dropped == 0) {
                 *used = 2;
+                *perm_out = ordered;
+                return SWANN_OK;
+            }
+            if (ordered) {
+                // the ordered sweep's repair: the row panels holding a row
+                // whose second list overflowed are swept again one-sided
+                // (two column halves, lists 0 and 1 of each row written from
+                // scratch), so those rows' lists are exact again
+                hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, npl, 1);
+                hipLaunchKernelGGL(flag_panels, dim3((unsigned)((ntile + 255) / 256)), dim3(256), 0,
+                                   st, flag, n, (int)ntile, plist, npl);
+                int np = 0;
+                if (hipMemcpyAsync(&np, npl, sizeof(int), hipMemcpyDeviceToHost, st) !=
+                        hipSuccess ||
+                    hipStreamSynchronize(st) != hipSuccess) {
+                    set_error("sweep (mfma, symmetric): reading the repair count failed");
+                    return SWANN_E_LAUNCH;
+                }
+                SWANN_REQUIRE(np >= 1 && np <= ntile, "sweep: repair panel count out of range");
+                MfmaSweepArgs rep = s;
+                rep.sym = 0;
+                rep.splits = 2;
+                rep.plist = plist;
+                rep.npl = np;
+                const unsigned rg = (unsigned)(np * 2);
+                if (scaled) {
+                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                } else {
+                    if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                    else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                }
+                const int rc = launch_status("sweep (mfma, ordered repair)");
+                if (rc) return rc;
+                *used = 2;
+                *perm_out = ordered;
                 return SWANN_OK;
             }
         }

@@ -277,14 +277,20 @@ def test_mfma_sweep_picks_the_row_scaled_plane_from_the_range(metric, spread):
         assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=4e-6 * scale)
 
 
+@pytest.mark.parametrize("mode", ["order", "seeds", "order-overflow"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype):
-    """The symmetric sweep starts from seeded thresholds, found by a pre-pass
-    over a locality-ordered copy of the rows (n = 20,000 of a 60-cluster
-    mixture, so the order groups rows and the seeds bite): its lists must be
-    those of the sweep without seeds (SWANN_SWEEP_NOSEED) and the oracle's."""
+def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype, mode):
+    """On clustered rows (n = 20,000 of a 60-cluster mixture) the symmetric
+    sweep runs on a locality-ordered copy from seeded thresholds ("order", the
+    default), or in the rows' own order from the same seeds
+    (SWANN_SWEEP_ORDER=0); with room for only 4 foreign candidates a row,
+    every panel overflows and is repaired by the one-sided re-sweep of its
+    panel ("order-overflow").  The lists, mapped back to the rows' own ids,
+    must be those of the plain sweep (SWANN_SWEEP_NOSEED) and the oracle's."""
     monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
+    if mode == "seeds":
+        monkeypatch.setenv("SWANN_SWEEP_ORDER", "0")
     n, d, C = 20000, 64, 24
     rng = np.random.default_rng(451 + metric)
     centres = rng.standard_normal((60, d)).astype(np.float32)
@@ -296,18 +302,21 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype)
     X = np.ascontiguousarray(X)
     Xg = torch.from_numpy(X).cuda()
     m = "ip" if metric == 0 else "l2"
-    note("mfma sweep seeds", dtype, m)
+    note("mfma sweep seeds", mode, dtype, m)
+    if mode == "order-overflow":
+        monkeypatch.setenv("SWANN_SWEEP_SYM_FCAP", "4")
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
+    monkeypatch.delenv("SWANN_SWEEP_SYM_FCAP", raising=False)
     monkeypatch.setenv("SWANN_SWEEP_NOSEED", "1")
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     monkeypatch.delenv("SWANN_SWEEP_NOSEED")
     same = (cand == c0).float().mean().item()
-    note("mfma sweep seeds vs none", dtype, m, same)
+    note("mfma sweep seeds vs none", mode, dtype, m, same)
     assert same > 0.999
     assert torch.allclose(cdist, d0, rtol=1e-6, atol=1e-6)
     oc, od = O.knn_candidates(X.astype(np.float32), C, metric, nthreads=8)
     agree = (cand.cpu().numpy() == oc).mean()
-    note("mfma sweep seeds vs oracle", dtype, m, agree)
+    note("mfma sweep seeds vs oracle", mode, dtype, m, agree)
     assert agree > 0.995
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
     assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
