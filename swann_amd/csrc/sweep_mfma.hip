@@ -1477,6 +1477,71 @@ __global__ void flag_panels(const int* __restrict__ flag, int64_t n, int ntile,
     if (any) plist[atomicAdd(npl, 1)] = p;
 }
 
+// The repair of one row panel in kRepairSplits column ranges (its rows' lists
+// in a scratch area, row-panel relative), then per row: the entries of those
+// lists sorted by (d, the rows' own ids) and the first C written as the row's
+// list 0 (list 1 emptied).  One workgroup a row.
+constexpr int kRepairSplits = 16;
+constexpr int kRepairSort = 4096;    // >= kRepairSplits * C for C <= 256
+
+__global__ __launch_bounds__(256) void repair_merge(const float* __restrict__ rkey,
+                                                    const int32_t* __restrict__ rid,
+                                                    const int32_t* __restrict__ rcnt, int r0,
+                                                    int64_t n, int cap, int C,
+                                                    const int32_t* __restrict__ perm,
+                                                    float* __restrict__ bkey,
+                                                    int32_t* __restrict__ bid,
+                                                    int32_t* __restrict__ bcnt) {
+    __shared__ float sd[kRepairSort];
+    __shared__ int si[kRepairSort];
+    __shared__ int so[kRepairSort];
+    const int rl = blockIdx.x;
+    const int64_t r = (int64_t)r0 + rl;
+    if (r >= n) return;
+    int segc[kRepairSplits], cnt = 0;
+    for (int sg = 0; sg < kRepairSplits; ++sg) {
+        segc[sg] = rcnt[rl * kRepairSplits + sg];
+        cnt += segc[sg];
+    }
+    int np = 2;
+    while (np < cnt) np <<= 1;
+    for (int i = threadIdx.x; i < np; i += 256) {
+        int sg = 0, off = i;
+        while (sg < kRepairSplits - 1 && off >= segc[sg]) { off -= segc[sg]; ++sg; }
+        const bool real = i < cnt;
+        const int64_t at = ((int64_t)rl * kRepairSplits + sg) * cap + off;
+        sd[i] = real ? rkey[at] : INFINITY;
+        si[i] = real ? rid[at] : INT32_MAX;
+        so[i] = real ? perm[rid[at]] : INT32_MAX;    // the order of ties
+    }
+    __syncthreads();
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < np; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const bool lt = sd[j] < sd[i] || (sd[j] == sd[i] && so[j] < so[i]);
+                    if (up == lt) {
+                        const float td = sd[i]; sd[i] = sd[j]; sd[j] = td;
+                        const int ti = si[i]; si[i] = si[j]; si[j] = ti;
+                        const int to = so[i]; so[i] = so[j]; so[j] = to;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    const int kept = cnt < C ? cnt : C;
+    for (int t = threadIdx.x; t < kept; t += 256) {
+        bkey[r * 2 * (int64_t)cap + t] = sd[t];
+        bid[r * 2 * (int64_t)cap + t] = si[t];
+    }
+    if (threadIdx.x == 0) {
+        bcnt[r * 2] = kept;
+        bcnt[r * 2 + 1] = 0;
+    }
+}
+
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 inline int64_t seed_bytes(int64_t n, int dim) {
@@ -1485,6 +1550,11 @@ inline int64_t seed_bytes(int64_t n, int dim) {
            al256(n * (int64_t)dim * 2) + al256(ntile * 4) + 256 +
            al256((int64_t)kMaxPivots * kSketch * 4) + al256((kMaxPivots + 1) * 4) +
            al256((int64_t)kMaxPivots * kMaxPivots * 4) + al256(kMaxPivots * 4);
+}
+
+// The few-panel repair's scratch: lists of one panel in kRepairSplits ranges.
+inline int64_t repair_bytes(int cap) {
+    return al256((int64_t)kBM2 * kRepairSplits * cap * 4) * 2 + al256(kBM2 * kRepairSplits * 4);
 }
 
 // Widest band of the symmetric sweep.  Wider bands mean fewer launches and
@@ -1617,6 +1687,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             int* flag = nullptr;         // rows whose second list overflowed (ordered sweep)
             int* plist = nullptr;
             int* npl = nullptr;
+            float* rkey = nullptr;       // the few-panel repair's scratch lists
+            int32_t* rid = nullptr;
+            int32_t* rcnt = nullptr;
             const int32_t* ordered = nullptr;
             if (ntile > 2 * kSeedBand && !getenv_flag("SWANN_SWEEP_NOSEED")) {
                 bool clustered = false;
@@ -1636,6 +1709,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 int* pstart = (int*)extra; extra += al256((kMaxPivots + 1) * 4);
                 float* pd = (float*)extra; extra += al256((int64_t)kMaxPivots * kMaxPivots * 4);
                 int* prank = (int*)extra; extra += al256(kMaxPivots * 4);
+                rkey = (float*)extra; extra += al256((int64_t)kBM2 * kRepairSplits * cap * 4);
+                rid = (int32_t*)extra; extra += al256((int64_t)kBM2 * kRepairSplits * cap * 4);
+                rcnt = (int32_t*)extra; extra += al256(kBM2 * kRepairSplits * 4);
                 const int64_t pw = n / 512;
                 const int P = (int)(pw < 1 ? 1 : pw > kMaxPivots ? kMaxPivots : pw);
                 if (x_dtype == SWANN_DTYPE_F16)
@@ -1788,6 +1864,50 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     return SWANN_E_LAUNCH;
                 }
                 SWANN_REQUIRE(np >= 1 && np <= ntile, "sweep: repair panel count out of range");
+                int rmax = 4;                    // panels repaired one at a time, 16 ways
+                if (const char* e = getenv("SWANN_SWEEP_REPAIR_MAX")) rmax = atoi(e);
+                if (np <= rmax && C * kRepairSplits <= kRepairSort) {
+                    std::vector<int> ph(np);
+                    if (hipMemcpyAsync(ph.data(), plist, (size_t)np * 4, hipMemcpyDeviceToHost,
+                                       st) != hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma, symmetric): reading the repair panels failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    for (int i = 0; i < np; ++i) {
+                        SWANN_REQUIRE(ph[i] >= 0 && ph[i] < ntile, "sweep: repair panel out of range");
+                        // the one-sided sweep of panel ph[i] into the scratch:
+                        // its list addresses are row-absolute, so the bases
+                        // are shifted by the panel's first row (only rows of
+                        // this panel are touched)
+                        const int64_t rb = (int64_t)ph[i] * kBM2;
+                        MfmaSweepArgs rep = s;
+                        rep.sym = 0;
+                        rep.splits = kRepairSplits;
+                        rep.plist = plist + i;
+                        rep.npl = 1;
+                        rep.bkey = rkey - rb * kRepairSplits * cap;
+                        rep.bid = rid - rb * kRepairSplits * cap;
+                        rep.bcnt = rcnt - rb * kRepairSplits;
+                        const unsigned rg = (unsigned)kRepairSplits;
+                        if (scaled) {
+                            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                        } else {
+                            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(rg), dim3(1024), 0, st, rep);
+                        }
+                        hipLaunchKernelGGL(repair_merge, dim3(kBM2), dim3(256), 0, st,
+                                           (const float*)rkey, (const int32_t*)rid,
+                                           (const int32_t*)rcnt, (int)rb, n, cap, C, ordered, bkey,
+                                           bid, bcnt);
+                        const int rc = launch_status("sweep (mfma, ordered repair)");
+                        if (rc) return rc;
+                    }
+                    *used = 2;
+                    *perm_out = ordered;
+                    return SWANN_OK;
+                }
                 MfmaSweepArgs rep = s;
                 rep.sym = 0;
                 rep.splits = 2;
@@ -1843,7 +1963,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
     return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) + al256(n * 4) + 256 +
-           seed_bytes(n, dim);
+           seed_bytes(n, dim) + repair_bytes(1024);      // cap <= 1024
 }
 
 // Column splits of the direct-load sweep: enough workgroups to give every

@@ -277,7 +277,7 @@ def test_mfma_sweep_picks_the_row_scaled_plane_from_the_range(metric, spread):
         assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=4e-6 * scale)
 
 
-@pytest.mark.parametrize("mode", ["order", "seeds", "order-overflow"])
+@pytest.mark.parametrize("mode", ["order", "seeds", "order-overflow", "order-overflow-16"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype, mode):
@@ -286,8 +286,11 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     default), or in the rows' own order from the same seeds
     (SWANN_SWEEP_ORDER=0); with room for only 4 foreign candidates a row,
     every panel overflows and is repaired by the one-sided re-sweep of its
-    panel ("order-overflow").  The lists, mapped back to the rows' own ids,
-    must be those of the plain sweep (SWANN_SWEEP_NOSEED) and the oracle's."""
+    panel, two column halves for all panels at once ("order-overflow") or
+    sixteen column ranges a panel at a time with a per-row merge of the
+    sixteen lists ("order-overflow-16", forced by SWANN_SWEEP_REPAIR_MAX).
+    The lists, mapped back to the rows' own ids, must be those of the plain
+    sweep (SWANN_SWEEP_NOSEED) and the oracle's."""
     monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
     if mode == "seeds":
         monkeypatch.setenv("SWANN_SWEEP_ORDER", "0")
@@ -303,10 +306,12 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     Xg = torch.from_numpy(X).cuda()
     m = "ip" if metric == 0 else "l2"
     note("mfma sweep seeds", mode, dtype, m)
-    if mode == "order-overflow":
+    if mode.startswith("order-overflow"):
         monkeypatch.setenv("SWANN_SWEEP_SYM_FCAP", "4")
+        monkeypatch.setenv("SWANN_SWEEP_REPAIR_MAX", "1000" if mode.endswith("16") else "0")
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
     monkeypatch.delenv("SWANN_SWEEP_SYM_FCAP", raising=False)
+    monkeypatch.delenv("SWANN_SWEEP_REPAIR_MAX", raising=False)
     monkeypatch.setenv("SWANN_SWEEP_NOSEED", "1")
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     monkeypatch.delenv("SWANN_SWEEP_NOSEED")
