@@ -1257,6 +1257,7 @@ constexpr int kMaxPivots = 2048;
 constexpr int kPivChunk = 256;       // pivots staged in LDS at a time (64 KB)
 constexpr int64_t kSeedBand = 4;     // the pre-pass scores tiles (I, I + b), b < kSeedBand
 constexpr int kKmeanSteps = 2;       // refinements of the pivots' sketches
+constexpr int64_t kSampleStride = 8; // rows of the k-means steps: every 8th
 constexpr float kClusterRatio = 0.3f;  // nearest-pivot / arbitrary-pivot distance for an order
 
 // Coordinates l * dim / 64 of each row, as float (zeros past dim).
@@ -1277,15 +1278,19 @@ __global__ __launch_bounds__(256) void row_sketch(const XT* __restrict__ X, int6
 // With acc, also adds up (over all rows) the distance to the nearest pivot
 // and to pivot r % P, a stand-in for an arbitrary one: their ratio says how
 // clustered the rows are.
-__global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ sk, int64_t n,
-                                                     int P, const float* __restrict__ psk,
+// Rows r = i * stride for i < m (every row, or a sample for the k-means
+// steps); lab and the counts are by i.
+__global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ sk, int64_t m,
+                                                     int64_t stride, int P,
+                                                     const float* __restrict__ psk,
                                                      int* __restrict__ lab,
                                                      int* __restrict__ pcnt,
                                                      float* __restrict__ acc) {
     __shared__ __align__(16) float sp[kPivChunk * kSketch];
     __shared__ float red[2][4];
-    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const bool ok = r < n;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool ok = i < m;
+    const int64_t r = i * stride;
     const int pr = (int)(r % P);
     float drand = 0.f;
     float x[kSketch];
@@ -1300,14 +1305,7 @@ __global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ s
     for (int p0 = 0; p0 < P; p0 += kPivChunk) {
         const int pc = P - p0 < kPivChunk ? P - p0 : kPivChunk;
         __syncthreads();
-        for (int i = threadIdx.x; i < pc * kSketch; i += 256) {
-            if (psk) {
-                sp[i] = psk[(int64_t)p0 * kSketch + i];
-            } else {
-                const int64_t pr = (int64_t)(p0 + i / kSketch) * n / P;
-                sp[i] = sk[pr * kSketch + i % kSketch];
-            }
-        }
+        for (int t = threadIdx.x; t < pc * kSketch; t += 256) sp[t] = psk[(int64_t)p0 * kSketch + t];
         __syncthreads();
         for (int p = 0; p < pc; ++p) {
             const float4* s4 = reinterpret_cast<const float4*>(sp + p * kSketch);
@@ -1326,7 +1324,7 @@ __global__ __launch_bounds__(256) void nearest_pivot(const float* __restrict__ s
         }
     }
     if (ok) {
-        lab[r] = bi;
+        lab[i] = bi;
         atomicAdd(&pcnt[bi], 1);
     }
     if (acc) {
@@ -1378,12 +1376,12 @@ __global__ __launch_bounds__(1024) void pivot_scan(int* pcnt, int* pstart, int P
 __global__ __launch_bounds__(kSketch) void group_mean(const float* __restrict__ sk,
                                                       const int* __restrict__ perm,
                                                       const int* __restrict__ pstart,
-                                                      float* __restrict__ psk) {
+                                                      int64_t stride, float* __restrict__ psk) {
     const int p = blockIdx.x, k = threadIdx.x;
     const int b = pstart[p], e = pstart[p + 1];
     if (e <= b) return;
     float acc = 0.f;
-    for (int i = b; i < e; ++i) acc += sk[(int64_t)perm[i] * kSketch + k];
+    for (int i = b; i < e; ++i) acc += sk[(int64_t)perm[i] * stride * kSketch + k];
     psk[(int64_t)p * kSketch + k] = acc / (float)(e - b);
 }
 
@@ -1726,14 +1724,20 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 // distance to the nearest pivot above kClusterRatio of that to
                 // an arbitrary one) gain nothing from an order or seeds: the
                 // sweep then runs plain
+                // (the check and the k-means steps on every kSampleStride-th
+                // row; the final grouping on all of them)
                 float* cacc = (float*)npl + 2;
                 for (int it = 0; it <= kKmeanSteps; ++it) {
+                    const bool fin = it == kKmeanSteps;
+                    const int64_t stride = fin ? 1 : kSampleStride;
+                    const int64_t m = fin ? n : (n + kSampleStride - 1) / kSampleStride;
                     hipLaunchKernelGGL(fill_zero, dim3(kMaxPivots / 256), dim3(256), 0, st, pcnt,
                                        kMaxPivots);
                     if (it == 0)
                         hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)cacc, 2);
-                    hipLaunchKernelGGL(nearest_pivot, dim3(nb256), dim3(256), 0, st, sk, n, P,
-                                       (const float*)psk, lab, pcnt, it == 0 ? cacc : nullptr);
+                    hipLaunchKernelGGL(nearest_pivot, dim3((unsigned)((m + 255) / 256)), dim3(256),
+                                       0, st, sk, m, stride, P, (const float*)psk, lab, pcnt,
+                                       it == 0 ? cacc : nullptr);
                     if (it == 0) {
                         float ca[2] = {0.f, 0.f};
                         if (hipMemcpyAsync(ca, cacc, sizeof(ca), hipMemcpyDeviceToHost, st) !=
@@ -1746,11 +1750,11 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         clustered = true;
                     }
                     hipLaunchKernelGGL(pivot_scan, dim3(1), dim3(1024), 0, st, pcnt, pstart, P);
-                    hipLaunchKernelGGL(pivot_place, dim3(nb256), dim3(256), 0, st, lab, n, pcnt,
-                                       perm);
-                    if (it < kKmeanSteps)
+                    hipLaunchKernelGGL(pivot_place, dim3((unsigned)((m + 255) / 256)), dim3(256), 0,
+                                       st, lab, m, pcnt, perm);
+                    if (!fin)
                         hipLaunchKernelGGL(group_mean, dim3(P), dim3(kSketch), 0, st, sk,
-                                           (const int*)perm, (const int*)pstart, psk);
+                                           (const int*)perm, (const int*)pstart, stride, psk);
                 }
                 const char* oe = getenv("SWANN_SWEEP_ORDER");
                 const bool in_order = clustered && !(oe && *oe == '0');
