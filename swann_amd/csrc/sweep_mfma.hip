@@ -1454,16 +1454,6 @@ __global__ void seed_map(const float* __restrict__ gthr, const int* __restrict__
     seed[r] = t < INFINITY ? t + (fabsf(t) + fabsf(xn[r])) * (1.f / 65536.f) + 1e-30f : INFINITY;
 }
 
-// seed[i]: ordered row i's pre-pass threshold plus the margin (the sweep in
-// locality order keeps its rows in that order).
-__global__ void seed_widen(const float* __restrict__ gthr, const float* __restrict__ xn,
-                           int64_t n, float* __restrict__ seed) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float t = gthr[i];
-    seed[i] = t < INFINITY ? t + (fabsf(t) + fabsf(xn[i])) * (1.f / 65536.f) + 1e-30f : INFINITY;
-}
-
 // The row panels holding a flagged row (one thread a panel), listed in plist
 // with their count in *npl.
 __global__ void flag_panels(const int* __restrict__ flag, int64_t n, int ntile,
@@ -1657,9 +1647,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 if (f >= 1 && f < cap) s.fcap = f;
             }
             // the launches of bands [b0, bend), each followed by a merge
-            auto bands = [&](MfmaSweepArgs& sa, int64_t bend, const float* seed,
+            auto bands = [&](MfmaSweepArgs& sa, int64_t bstart, int64_t bend, const float* seed,
                              int* flag) -> int {
-                for (int64_t b0 = 0; b0 < bend;) {
+                for (int64_t b0 = bstart; b0 < bend;) {
                     const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
                     sa.b0 = b0;
                     sa.b1 = b0 + B < bend ? b0 + B : bend;
@@ -1808,22 +1798,26 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                                    scaled ? scale : nullptr, hp, xnp, scp);
                 hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
                                    (const float*)nullptr);
+                if (in_order)
+                    hipLaunchKernelGGL(fill_zero, dim3(nb256), dim3(256), 0, st, flag, (int)n);
                 MfmaSweepArgs pre = s;
                 pre.hi = hp;
                 pre.xn = xnp;
                 pre.scale = scp;
                 int rc = launch_status("sweep (mfma, seed order)");
                 if (rc) return rc;
-                rc = bands(pre, kSeedBand, nullptr, nullptr);
+                rc = bands(pre, 0, kSeedBand, nullptr, in_order ? flag : nullptr);
                 if (rc) return rc;
                 if (in_order) {
-                    // the main sweep in the locality order too: seeds stay in
-                    // that order, the lists come out in ordered ids
-                    hipLaunchKernelGGL(seed_widen, dim3(nb256), dim3(256), 0, st, gthr, xnp, n,
-                                       seed);
-                    hipLaunchKernelGGL(fill_zero, dim3(nb256), dim3(256), 0, st, flag, (int)n);
+                    // the main sweep in the locality order too: the pre-pass
+                    // was its first bands, so it goes on from there, its lists
+                    // and thresholds as the last merge left them (ordered ids)
+                    rc = bands(pre, kSeedBand, ntile, nullptr, flag);
+                    if (rc) return rc;
                     s = pre;
+                    seed = nullptr;
                     ordered = perm;
+                    goto swept;
                 } else {
                     hipLaunchKernelGGL(seed_map, dim3(nb256), dim3(256), 0, st, gthr, perm, xn, n,
                                        seed);
@@ -1834,9 +1828,10 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
                                (const float*)seed);
             {
-                const int rc = bands(s, ntile, seed, flag);
+                const int rc = bands(s, 0, ntile, seed, flag);
                 if (rc) return rc;
             }
+        swept:
             // a list that overflowed lost candidates: redo the sweep the
             // one-sided way (one small read-back; the build is not on the
             // search path)
