@@ -1237,25 +1237,36 @@ __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
 }
 
 // ---------------------------------------------------------------------------
-// Seeds for the symmetric sweep's thresholds.  A row's threshold only falls
-// as the bands reach its neighbours; until then it appends much of what it
-// sees.  A short pre-pass gives every row a bound first: rows are put in a
-// locality order (grouped by the nearest of P evenly spaced pivot rows,
-// measured on a 64-coordinate sketch), the tiles within kSeedBand panels of
-// the diagonal of that ordered copy are swept, and each row's resulting
-// threshold -- the C-th best of real distances, so an upper bound of its
-// true C-th -- seeds the main sweep, which runs on the rows in their own
-// order.  A seed holds back (in both directions) only candidates that could
-// not be among the row's C best, so the lists come out as without it.  The
-// margin added to a seed (2^-16 of |t| + |x|^2) lies far above any
-// difference in how the accumulators round the same pair in another tile
-// position.  (Sweeping in the ordered copy itself would concentrate each
-// row's survivors in few tiles, but a row whose seed stayed loose then
-// meets its neighbours in one burst that can overflow its second list.)
+// Locality order for the symmetric sweep.  A row's threshold only falls as
+// the bands reach its neighbours; until then it appends much of what it
+// sees, and in row order its survivors spread over many tiles, sending many
+// 32 x 32 blocks down the epilogue's slow path.  So rows are first grouped by
+// the nearest of P evenly spaced pivot rows, measured on a 64-coordinate
+// sketch.  The first assignment (on every kSampleStride-th row) also tells
+// whether the rows cluster at all: if their mean distance to the nearest
+// pivot is not under kClusterRatio of that to an arbitrary pivot, an order
+// would not help and the sweep runs plain.  Otherwise kKmeanSteps k-means
+// steps refine the pivots, the pivots are chained nearest to nearest, and
+// the rows, sorted by their pivot's place in the chain, are gathered into an
+// ordered copy that the whole sweep runs on: a row's neighbours then sit in
+// few tiles near the diagonal, its threshold falls within the first
+// launches, and most blocks have no survivor.  The lists come out as in row
+// order (the sweep is exact in any order), in ordered ids that sweep_final
+// maps back.  A row whose threshold stayed loose can still meet its
+// neighbours in one burst that overflows its second list; the merge flags
+// it and its row panel is swept again one-sided (repair_merge).
+// SWANN_SWEEP_ORDER=0 keeps the rows' own order and uses the first
+// kSeedBand bands of the ordered copy as a pre-pass instead: each row's
+// resulting threshold -- the C-th best of real distances, an upper bound of
+// its true C-th -- seeds its threshold in the sweep in row order.  A seed
+// holds back (in both directions) only candidates that could not be among
+// the row's C best; the margin added to it (2^-16 of |t| + |x|^2) lies far
+// above any difference in how the accumulators round the same pair in
+// another tile position.
 constexpr int kSketch = 64;          // sketch coordinates a row
 constexpr int kMaxPivots = 2048;
 constexpr int kPivChunk = 256;       // pivots staged in LDS at a time (64 KB)
-constexpr int64_t kSeedBand = 4;     // the pre-pass scores tiles (I, I + b), b < kSeedBand
+constexpr int64_t kSeedBand = 4;     // first bands: tiles (I, I + b), b < kSeedBand
 constexpr int kKmeanSteps = 2;       // refinements of the pivots' sketches
 constexpr int64_t kSampleStride = 8; // rows of the k-means steps: every 8th
 constexpr float kClusterRatio = 0.3f;  // nearest-pivot / arbitrary-pivot distance for an order
@@ -1681,7 +1692,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             const int32_t* ordered = nullptr;
             if (ntile > 2 * kSeedBand && !getenv_flag("SWANN_SWEEP_NOSEED")) {
                 bool clustered = false;
-                // the pre-pass (seed_bytes of workspace)
+                // the order's workspace (seed_bytes, repair_bytes)
                 float* sk = (float*)extra; extra += al256(n * kSketch * 4);
                 int* lab = (int*)extra; extra += al256(n * 4);
                 int* perm = (int*)extra; extra += al256(n * 4);
