@@ -28,6 +28,13 @@ def gaussian(n, d, seed, normalise):
     return np.ascontiguousarray(X)
 
 
+def norm_spread(X, sigma, seed):
+    """Rows scaled by exp(sigma * N(0,1)) in float64, then cast
+    (tests/golden/make_golden.py's recipe for the degree-96 ip corpus)."""
+    s = np.exp(sigma * np.random.default_rng(seed).standard_normal((X.shape[0], 1)))
+    return np.ascontiguousarray((X.astype(np.float64) * s).astype(np.float32))
+
+
 def golden(name):
     path = GOLDEN / name
     if not path.exists():
@@ -38,5 +45,18 @@ def golden(name):
 def regen(n, d, seed, normalise, want_sha):
     X = gaussian(n, d, seed, normalise)
     if sha(X) != str(want_sha):
+        pytest.skip("regenerated inputs differ from the golden inputs on this platform")
+    return X
+
+
+def deg96_corpus(tag, g):
+    """The degree-96 golden's corpus (tests/golden/refbuild_deg96.npz):
+    l2 is 2,000 x 128 N(0,1); ip is 2,000 x 256 unit rows scaled by
+    exp(0.2 N(0,1))."""
+    if tag == "l2":
+        X = gaussian(2000, 128, 961, False)
+    else:
+        X = norm_spread(gaussian(2000, 256, 962, True), 0.2, 963)
+    if sha(X) != str(g[f"{tag}_X_sha"]):
         pytest.skip("regenerated inputs differ from the golden inputs on this platform")
     return X

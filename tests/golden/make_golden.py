@@ -76,6 +76,13 @@ def gaussian(n, d, seed, normalise):
     return np.ascontiguousarray(X)
 
 
+def norm_spread(X, sigma, seed):
+    """Rows of X scaled by exp(sigma * N(0,1)) in float64, then cast: an
+    inner-product corpus whose norms differ, so hubs collect many in-edges."""
+    s = np.exp(sigma * np.random.default_rng(seed).standard_normal((X.shape[0], 1)))
+    return np.ascontiguousarray((X.astype(np.float64) * s).astype(np.float32))
+
+
 def knn_graph(X, deg, metric):
     """Exact kNN graph in float64 (the reference toy graph, tests/test_engine.py:24-34)."""
     X64 = X.astype(np.float64)
@@ -192,6 +199,72 @@ def make_build_small(build):
     print("refbuild_small.npz written")
 
 
+def reverse_cut_case(metric, n=300, d=100):
+    """A hand-made graph on which add_reverse's cut and in-edge order decide
+    the result.  Node 0 lists the 96 cluster nodes 1..96, which sit close
+    together and block one another in the prune; the 70 far nodes 97..166
+    each list node 0, so node 0 has 70 in-sources, of which the first 64 in
+    source order join its union; the far nodes lie in orthogonal directions
+    and block nothing.  The union is 160 wide: the cut to 128 keeps the
+    nearest 32 far nodes, so node 0 ends with 1 + 32 neighbours (1 + 64
+    without the cut, others with another in-edge order).  Other rows link
+    at random, never to node 0."""
+    rng = np.random.default_rng(971 + (metric == "ip"))
+    X = np.zeros((n, d), np.float64)
+    e = np.eye(d)
+    if metric == "l2":
+        X[0] = 0.001 * rng.standard_normal(d)
+        X[1:97] = e[1] + 0.05 * rng.standard_normal((96, d))
+        for k in range(70):
+            X[97 + k] = (2.0 + 0.01 * k) * e[2 + k]
+        X[167:] = rng.standard_normal((n - 167, d))
+    else:
+        X[0] = e[0]
+        c = (e[0] + e[1]) / np.sqrt(2.0)
+        X[1:97] = c + 0.02 * rng.standard_normal((96, d))
+        for k in range(70):
+            a = 0.3 - 0.002 * k
+            X[97 + k] = a * e[0] + np.sqrt(1 - a * a) * e[2 + k]
+        X[167:] = rng.standard_normal((n - 167, d))
+        X /= np.linalg.norm(X, axis=1, keepdims=True)
+    G = np.full((n, 96), -1, np.int32)
+    G[0] = np.arange(1, 97)
+    for u in range(1, n):
+        row = rng.choice(np.arange(1, n), size=40, replace=False)
+        row = row[row != u][:39]
+        if 97 <= u < 167:
+            row = np.r_[0, row[:38]]
+        G[u, :len(row)] = row
+    return np.ascontiguousarray(X.astype(np.float32)), G
+
+
+def make_build_deg96(build):
+    """The build at the reference API's defaults (build.py:153-171,
+    index.py:76): candidates=128, degree=96, alpha=1.2, max_in=64.  The
+    reverse pass's union is then 96 + 64 = 160 wide and add_reverse cuts it
+    to its 128 nearest before the re-prune (build.py:138-148); both corpora
+    are chosen so that cut binds on many rows (l2: 200 of 2,000; ip: 136)."""
+    import torch
+    out = {}
+    cases = (("l2", "l2", gaussian(2000, 128, 961, False)),
+             ("ip", "ip", norm_spread(gaussian(2000, 256, 962, True), 0.2, 963)))
+    for tag, m, X in cases:
+        Xt = torch.from_numpy(X)
+        cand, cdist = build.knn_candidates(Xt, 128, metric=m)
+        Gp = build.robust_prune(Xt, cand, cdist, 96, alpha=1.2, metric=m)
+        Gf = build.add_reverse(Xt, Gp, 96, alpha=1.2, metric=m)
+        out.update({f"{tag}_X_sha": np.array(sha(X)), f"{tag}_cand": cand.numpy().astype(np.int16),
+                    f"{tag}_cdist": cdist.numpy(), f"{tag}_Gp": Gp.numpy().astype(np.int16),
+                    f"{tag}_Gf": Gf.numpy().astype(np.int16)})
+    for tag, m in (("adv_l2", "l2"), ("adv_ip", "ip")):
+        X, G = reverse_cut_case(m)
+        Gf = build.add_reverse(torch.from_numpy(X), torch.from_numpy(G), 96, alpha=1.2, metric=m)
+        out.update({f"{tag}_X": X, f"{tag}_G": G.astype(np.int16),
+                    f"{tag}_Gf": Gf.numpy().astype(np.int16)})
+    np.savez_compressed(OUT / "refbuild_deg96.npz", **out)
+    print("refbuild_deg96.npz written")
+
+
 _C1 = {}
 
 
@@ -283,8 +356,10 @@ def make_c1(refcpu, build, select, engine):
           float(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(mi.numpy(), gt)])))
 
 
-def main(which=("branch", "distance", "build", "extras", "c1")):
+def main(which=("branch", "distance", "build", "extras", "c1", "deg96")):
     refcpu, build, select, engine, _ = ref_modules()
+    if "deg96" in which:
+        make_build_deg96(build)
     if "extras" in which:
         make_build_extras(build, ref_offline())
     if "distance" in which:
