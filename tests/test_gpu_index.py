@@ -8,8 +8,9 @@ import pytest
 import torch
 
 import oracle as O
-from conftest import ROOT, gaussian, golden, regen
-from test_oracle_helpers import exact_topk, recall
+from conftest import ROOT, deg96_corpus, gaussian, golden, regen
+from test_oracle_helpers import (describe_rows, exact_topk, recall, untied_graph_rows,
+                                 untied_prune_rows, untied_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -21,6 +22,19 @@ from swann_amd import build as B  # noqa: E402
 def note(*a):
     print("[case]", *a, flush=True)
     sys.stdout.flush()
+
+
+def same_lists(tag, cand, cdist, oc, od, atol, rtol):
+    """The GPU's candidate lists equal the oracle's up to ties: within each
+    run of oracle distances closer than the distance tolerance (atol + rtol
+    |d|, the bound the same test holds the GPU distances to) the ids may come
+    in another order, and at the cut another tied row may take the place."""
+    cand = cand.cpu().numpy() if torch.is_tensor(cand) else cand
+    cdist = cdist.cpu().numpy() if torch.is_tensor(cdist) else cdist
+    bad = untied_rows(cand, oc, od, cdist, atol=atol, rtol=rtol)
+    note(tag, "rows differing", int((cand != oc).any(1).sum()), "beyond ties", len(bad),
+         describe_rows(bad, cand, oc, od, cdist))
+    assert bad == [], describe_rows(bad, cand, oc, od, cdist)
 
 
 def corpus(n=8000, d=128, nq=200, seed=0, normalise=True):
@@ -110,34 +124,98 @@ def test_select_matches_oracle():
     for metric in (0, 1):
         idx = S.select_nearest(torch.from_numpy(g["Q"]).cuda(), Vp, 8, metric=metric)
         want, _ = O.select_nearest(g["Q"], X[cat], 8, metric, nthreads=8)
-        agree = (idx.cpu().numpy() == want).mean()
-        note("select", metric, agree)
-        assert agree > 0.995
+        got = idx.cpu().numpy()
+        Q64, V64 = g["Q"].astype(np.float64), X[cat].astype(np.float64)
         if metric == 0:
-            assert (cat[idx.cpu().numpy()] == g["seeds"].astype(np.int64)).mean() > 0.995
+            dist = lambda e: 1.0 - np.einsum("qd,qkd->qk", Q64, V64[e])  # noqa: E731
+        else:
+            dist = lambda e: ((V64[e] - Q64[:, None, :]) ** 2).sum(-1)  # noqa: E731
+        bad = untied_rows(got, want, dist(want), dist(got))
+        note("select", metric, "rows beyond ties", bad)
+        assert bad == []
+        if metric == 0:
+            ref = g["seeds"].astype(np.int64)
+            pos = np.searchsorted(cat, ref)
+            assert untied_rows(got, pos, dist(pos), dist(got)) == []
 
 
 @pytest.mark.parametrize("tag,metric", [("ip", 0), ("l2", 1)])
 def test_build_stages_match_reference(tag, metric):
+    """The three stages against the reference's CPU-torch build.py
+    (tests/golden/refbuild_small.npz): the sweep equal up to ties within
+    1e-6, the prune identical, the reverse pass equal up to the order of
+    tied neighbours."""
     g = golden("refbuild_small.npz")
     X = torch.from_numpy(g[f"{tag}_X"]).cuda()
     m = "ip" if metric == 0 else "l2"
     cand, cdist = B.knn_candidates(X, 32, metric=m)
     rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
-    c_same = (cand.cpu().numpy() == rc).mean()
-    note("sweep", tag, c_same)
-    assert c_same > 0.99
+    bad = untied_rows(cand.cpu().numpy(), rc, rd, cdist.cpu().numpy())
+    note("sweep", tag, "untied rows", bad)
+    assert bad == []
     assert np.allclose(cdist.cpu().numpy(), rd, atol=3e-5, rtol=1e-5)
     Gp = B.robust_prune(X, torch.from_numpy(rc).cuda(), torch.from_numpy(rd).cuda(), 16,
                         alpha=1.2, metric=m).cpu().numpy()
-    rows_p = (Gp == g[f"{tag}_Gp"].astype(np.int32)).all(1).mean()
-    note("prune", tag, rows_p)
-    assert rows_p > 0.98
+    assert np.array_equal(Gp, g[f"{tag}_Gp"].astype(np.int32))
     Gf = B.add_reverse(X, torch.from_numpy(g[f"{tag}_Gp"].astype(np.int32)).cuda(), 16,
                        alpha=1.2, metric=m).cpu().numpy()
-    same_sets = np.mean([set(a) == set(b) for a, b in zip(Gf, g[f"{tag}_Gf"].astype(np.int32))])
-    note("reverse", tag, same_sets)
-    assert same_sets > 0.97
+    bad = untied_graph_rows(Gf, g[f"{tag}_Gf"].astype(np.int32), g[f"{tag}_X"], metric)
+    note("reverse", tag, "untied rows", bad)
+    assert bad == []
+
+
+@pytest.mark.parametrize("tag,metric", [("ip", 0), ("l2", 1)])
+def test_build_at_default_degree_matches_reference(tag, metric):
+    """Index.build with the reference API's defaults (candidates 128, degree
+    96, alpha 1.2; index.py:76, build.py:153-171), where add_reverse cuts
+    its 160-wide union to 128 (build.py:138-148), against the reference's
+    CPU-torch stages (tests/golden/refbuild_deg96.npz) stage by stage, and
+    the whole build against the oracle's prune and reverse of the GPU's own
+    candidate lists, row for row."""
+    g = golden("refbuild_deg96.npz")
+    X = deg96_corpus(tag, g)
+    Xg = torch.from_numpy(X).cuda()
+    m = "ip" if metric == 0 else "l2"
+    note("deg96", tag)
+    rc = g[f"{tag}_cand"].astype(np.int32); rd = g[f"{tag}_cdist"]
+    cand, cdist = B.knn_candidates(Xg, 128, metric=m)
+    cand, cdist = cand.cpu().numpy(), cdist.cpu().numpy()
+    bad = untied_rows(cand, rc, rd, cdist)
+    note("deg96 sweep untied rows", bad)
+    assert bad == []
+    want_p = g[f"{tag}_Gp"].astype(np.int32)
+    Gp = B.robust_prune(Xg, torch.from_numpy(rc).cuda(), torch.from_numpy(rd).cuda(), 96,
+                        alpha=1.2, metric=m).cpu().numpy()
+    note("deg96 prune rows differing", int((Gp != want_p).any(1).sum()))
+    assert np.array_equal(Gp, want_p)
+    want_f = g[f"{tag}_Gf"].astype(np.int32)
+    Gf = B.add_reverse(Xg, torch.from_numpy(want_p).cuda(), 96, alpha=1.2, metric=m).cpu().numpy()
+    bad = untied_graph_rows(Gf, want_f, X, metric)
+    note("deg96 reverse untied rows", bad)
+    assert bad == []
+    index = swann.Index.build(Xg, metric=m)
+    G = index.G.cpu().numpy()
+    assert G.shape == (X.shape[0], 96)
+    Op = O.robust_prune(X, cand, cdist, 96, 1.2, metric, nthreads=8)
+    Of = O.add_reverse(X, Op, 96, 1.2, 64, metric, nthreads=8)
+    bad = untied_graph_rows(G, Of, X, metric)
+    note("deg96 Index.build vs oracle untied rows", bad)
+    assert bad == []
+
+
+@pytest.mark.parametrize("tag,metric", [("adv_l2", 1), ("adv_ip", 0)])
+def test_reverse_cut_and_in_edge_order_match_reference(tag, metric):
+    """add_reverse at degree 96 on the hand-made graph whose node 0 keeps
+    1 + 32 neighbours only through the cut to 128 and the ascending-source
+    in-edges (tests/golden/refbuild_deg96.npz): every row as the reference."""
+    g = golden("refbuild_deg96.npz")
+    X = g[f"{tag}_X"]
+    want = g[f"{tag}_Gf"].astype(np.int32)
+    Gf = B.add_reverse(torch.from_numpy(X).cuda(),
+                       torch.from_numpy(g[f"{tag}_G"].astype(np.int32)).cuda(), 96, alpha=1.2,
+                       metric="ip" if metric == 0 else "l2").cpu().numpy()
+    assert (Gf[0] >= 0).sum() == 33
+    assert untied_graph_rows(Gf, want, X, metric) == []
 
 
 def test_build_matches_oracle_exactly_where_it_can():
@@ -147,11 +225,11 @@ def test_build_matches_oracle_exactly_where_it_can():
     Xg = torch.from_numpy(X).cuda()
     cand, cdist = B.knn_candidates(Xg, 48, metric="l2")
     oc, od = O.knn_candidates(X, 48, O.METRIC_L2, nthreads=8)
-    assert (cand.cpu().numpy() == oc).mean() > 0.995
+    same_lists("sweep l2 d40", cand, cdist, oc, od, 1e-6, 1e-6)
     Gp = B.robust_prune(Xg, torch.from_numpy(oc).cuda(), torch.from_numpy(od).cuda(), 24,
                         metric="l2").cpu().numpy()
     Op = O.robust_prune(X, oc, od, 24, 1.2, O.METRIC_L2, nthreads=8)
-    assert (Gp == Op).all(1).mean() > 0.99
+    assert np.array_equal(Gp, Op)
 
 
 def test_c1_built_graph_recall_matches_reference_graph():
@@ -174,7 +252,7 @@ def test_c1_built_graph_recall_matches_reference_graph():
                              stop_eps=0.05)
         rs.append(recall(ids.cpu().numpy(), truth, 10))
     note("C1 graph recall gpu-built / reference-built", rs)
-    assert rs[0] >= rs[1] - 0.005
+    assert abs(rs[0] - rs[1]) <= 0.005
 
 
 @pytest.mark.parametrize("metric", [0, 1])
@@ -194,10 +272,8 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     note("mfma sweep", dtype, m)
     cand, cdist = B.knn_candidates(Xg, 40, metric=m)
     oc, od = O.knn_candidates(X.astype(np.float32), 40, metric, nthreads=8)
-    same = (cand.cpu().numpy() == oc).mean()
-    note("mfma sweep agreement", dtype, m, same)
-    assert same > 0.995
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    same_lists(f"mfma sweep {dtype} {m}", cand, cdist, oc, od, 2e-6 * scale, 2e-5)
     assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
     # self is never a candidate, rows are ascending
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
@@ -232,10 +308,8 @@ def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtyp
     note("mfma sweep layout", switch, dtype, m)
     cand, cdist = B.knn_candidates(Xg, 40, metric=m)
     oc, od = O.knn_candidates(X.astype(np.float32), 40, metric, nthreads=8)
-    same = (cand.cpu().numpy() == oc).mean()
-    note("mfma sweep layout agreement", switch, dtype, m, same)
-    assert same > 0.995
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    same_lists(f"mfma sweep layout {switch} {dtype} {m}", cand, cdist, oc, od, 2e-6 * scale, 2e-5)
     assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
@@ -267,20 +341,30 @@ def test_mfma_sweep_picks_the_row_scaled_plane_from_the_range(metric, spread):
         note("mfma sweep plane choice", spread, m, d)
         cand, cdist = B.knn_candidates(Xg, 40, metric=m)
         oc, od = O.knn_candidates(X, 40, metric, nthreads=8)
-        same = (cand.cpu().numpy() == oc).mean()
-        note("mfma sweep plane choice agreement", spread, m, d, same)
-        assert same > 0.995
         assert np.isfinite(cdist.cpu().numpy()).all()
         # rounding of (|a|^2 + |b|^2) - 2 a.b in fp32 scales with the norms
         nrm = (X.astype(np.float64) ** 2).sum(1)
         scale = nrm[:, None] + nrm[oc] if metric == 1 else np.abs(od).max()
+        same_lists(f"mfma sweep plane choice {spread} {m} {d}", cand, cdist, oc, od,
+                   4e-6 * scale, 2e-5)
         assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=4e-6 * scale)
 
 
+_ORACLE_LISTS = {}
+
+
+def oracle_lists(X, C, metric, key):
+    """The oracle's top-C lists of X, computed once per corpus key."""
+    if key not in _ORACLE_LISTS:
+        _ORACLE_LISTS[key] = O.knn_candidates(X.astype(np.float32), C, metric, nthreads=16)
+    return _ORACLE_LISTS[key]
+
+
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("mode", ["order", "seeds", "order-overflow", "order-overflow-16"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype, mode):
+def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype, mode, d):
     """On clustered rows (n = 20,000 of a 60-cluster mixture) the symmetric
     sweep runs on a locality-ordered copy from seeded thresholds ("order", the
     default), or in the rows' own order from the same seeds
@@ -290,11 +374,13 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     sixteen column ranges a panel at a time with a per-row merge of the
     sixteen lists ("order-overflow-16", forced by SWANN_SWEEP_REPAIR_MAX).
     The lists, mapped back to the rows' own ids, must be those of the plain
-    sweep (SWANN_SWEEP_NOSEED) and the oracle's."""
+    sweep (SWANN_SWEEP_NOSEED) and the oracle's.  d = 256 takes four K
+    steps a tile: the staged foreign queue, its drain after the loop and the
+    deferred threshold wait run only there."""
     monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
     if mode == "seeds":
         monkeypatch.setenv("SWANN_SWEEP_ORDER", "0")
-    n, d, C = 20000, 64, 24
+    n, C = 20000, 24
     rng = np.random.default_rng(451 + metric)
     centres = rng.standard_normal((60, d)).astype(np.float32)
     X = centres[rng.integers(0, 60, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
@@ -305,7 +391,7 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     X = np.ascontiguousarray(X)
     Xg = torch.from_numpy(X).cuda()
     m = "ip" if metric == 0 else "l2"
-    note("mfma sweep seeds", mode, dtype, m)
+    note("mfma sweep seeds", mode, dtype, m, d)
     if mode.startswith("order-overflow"):
         monkeypatch.setenv("SWANN_SWEEP_SYM_FCAP", "4")
         monkeypatch.setenv("SWANN_SWEEP_REPAIR_MAX", "1000" if mode.endswith("16") else "0")
@@ -315,30 +401,29 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     monkeypatch.setenv("SWANN_SWEEP_NOSEED", "1")
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     monkeypatch.delenv("SWANN_SWEEP_NOSEED")
-    same = (cand == c0).float().mean().item()
-    note("mfma sweep seeds vs none", mode, dtype, m, same)
-    assert same > 0.999
+    same_lists(f"mfma sweep seeds vs none {mode} {dtype} {m}", cand, cdist, c0.cpu().numpy(),
+               d0.cpu().numpy(), 1e-6, 1e-6)
     assert torch.allclose(cdist, d0, rtol=1e-6, atol=1e-6)
-    oc, od = O.knn_candidates(X.astype(np.float32), C, metric, nthreads=8)
-    agree = (cand.cpu().numpy() == oc).mean()
-    note("mfma sweep seeds vs oracle", mode, dtype, m, agree)
-    assert agree > 0.995
+    oc, od = oracle_lists(X, C, metric, ("seeded", metric, dtype, d))
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    same_lists(f"mfma sweep seeds vs oracle {mode} {dtype} {m} {d}", cand, cdist, oc, od,
+               2e-6 * scale, 2e-5)
     assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("sym", ["0", "1"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_with_duplicate_rows_matches_oracle(monkeypatch, metric, dtype, sym):
+def test_mfma_sweep_with_duplicate_rows_matches_oracle(monkeypatch, metric, dtype, sym, d):
     """A larger sweep (n = 12,000: 47 row panels, 47 column tiles, several
     compactions per row) with rows 0..999 duplicated at 6000..6999, so many
     rows hold exact ties, some of them at the C-th place: the lists must be
     the oracle's, and each duplicated row must find its twin -- one-sided
     and symmetric (47 panels, 9 band launches)."""
     monkeypatch.setenv("SWANN_SWEEP_SYM", sym)
-    n, d, C = 12000, 64, 16
+    n, C = 12000, 16
     X = gaussian(n, d, 421 + metric, metric == 0)
     if metric == 1:
         X = X * 2.0 + 0.5
@@ -347,14 +432,13 @@ def test_mfma_sweep_with_duplicate_rows_matches_oracle(monkeypatch, metric, dtyp
         X = X.astype(np.float16)
     Xg = torch.from_numpy(X).cuda()
     m = "ip" if metric == 0 else "l2"
-    note("mfma sweep with duplicates", dtype, m)
+    note("mfma sweep with duplicates", dtype, m, d)
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
-    oc, od = O.knn_candidates(X.astype(np.float32), C, metric, nthreads=8)
+    oc, od = oracle_lists(X, C, metric, ("dup", metric, dtype, d))
     cc, cd = cand.cpu().numpy(), cdist.cpu().numpy()
-    same = (cc == oc).mean()
-    note("mfma sweep with duplicates agreement", dtype, m, same)
-    assert same > 0.995
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
+    same_lists(f"mfma sweep with duplicates {dtype} {m} sym={sym}", cc, cd, oc, od, 2e-6 * scale,
+               2e-5)
     assert np.allclose(cd, od, rtol=2e-5, atol=2e-6 * scale)
     assert ((cc >= 0) & (cc < n)).all()
     assert not (cc == np.arange(n)[:, None]).any()
@@ -386,7 +470,7 @@ def test_mfma_sweep_self_is_last_when_candidates_cover_the_corpus(metric, dtype)
     assert (oc[:, -1] == np.arange(n)).all()
     for r in range(n):
         assert sorted(c[r, :-1].tolist()) == sorted(set(range(n)) - {r})
-    assert (c == oc).mean() > 0.99
+    same_lists(f"mfma sweep C = n {dtype} {metric}", c, cdist.cpu().numpy(), oc, od, 2e-6, 2e-5)
 
 
 def test_captured_search_replays_exactly():
@@ -480,9 +564,16 @@ def test_select_small_and_large_batches_match_oracle(nq, metric):
         idx = S.select_nearest(torch.from_numpy(Q).cuda(), torch.from_numpy(V).cuda(), E,
                                metric=metric).cpu().numpy()
         want, _ = O.select_nearest(Q, V, E, metric, nthreads=8)
-        note("select", nq, metric, P, d, E, (idx == want).mean())
         assert idx.shape == (nq, E)
-        assert (idx == want).mean() > 0.995
+        Q64, V64 = Q.astype(np.float64), V.astype(np.float64)
+
+        def dist(e):
+            if metric == 0:
+                return 1.0 - np.einsum("qd,qkd->qk", Q64, V64[e])
+            return ((V64[e] - Q64[:, None, :]) ** 2).sum(-1)
+        wd = dist(want)
+        same_lists(f"select {nq} {metric} {P} {d} {E}", idx, dist(idx), want, wd,
+                   2e-6 * float(np.abs(wd).max()), 2e-5)
         assert (np.sort(idx, 1)[:, 1:] != np.sort(idx, 1)[:, :-1]).all()   # distinct
         if metric == 1:
             # q = V[7], which has an exact duplicate at P//2 + 7: a tie at the
@@ -510,16 +601,16 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
         got = B.robust_prune(Xg, rcg, rdg, 12, alpha=1.2, metric=m, **kw).cpu().numpy()
         want = g[f"{tag}_{key}"].astype(np.int32)
         assert got.shape == want.shape
-        rows = (got == want).all(1).mean()
         ora = O.robust_prune(X, rc, rd, 12, 1.2, metric, nthreads=8, **okw)
-        note("prune extras", tag, key, rows, (got == ora).all(1).mean())
-        assert rows > 0.98
-        assert (got == ora).all(1).mean() > 0.99
+        note("prune extras", tag, key, int((got != want).any(1).sum()),
+             int((got != ora).any(1).sum()))
+        assert np.array_equal(got, want), key
+        assert np.array_equal(got, ora), key
     Rd = B.add_reverse(Xg, torch.from_numpy(g[f"{tag}_Gd"].astype(np.int32)).cuda(), 12,
                        alpha=1.2, deg_per_node=dpng, metric=m).cpu().numpy()
-    same = np.mean([set(a) == set(b) for a, b in zip(Rd, g[f"{tag}_Rd"].astype(np.int32))])
-    note("reverse dpn", tag, same)
-    assert same > 0.97
+    bad = untied_graph_rows(Rd, g[f"{tag}_Rd"].astype(np.int32), X, metric)
+    note("reverse dpn", tag, bad)
+    assert bad == []
 
 
 @pytest.mark.parametrize("C", [48, 100])
@@ -554,9 +645,13 @@ def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
     g_simt = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
     ora = O.robust_prune(X16.astype(np.float32), cand.cpu().numpy(), cdist.cpu().numpy(), 24,
                          1.2, metric, nthreads=8, deg_per_node=dpn, protect=prot)
-    a, b = (g_mfma == g_simt).all(1).mean(), (g_mfma == ora).all(1).mean()
-    note("prune mfma vs simt / oracle", dtype, m, a, b)
-    assert a > 0.99 and b > 0.99
+    Xo, cn, cdn = X16.astype(np.float32), cand.cpu().numpy(), cdist.cpu().numpy()
+    kw = dict(alpha=1.2, metric=metric, deg_per_node=dpn, protect=prot)
+    a = untied_prune_rows(g_mfma, g_simt, Xo, cn, cdn, 24, **kw)
+    b = untied_prune_rows(g_mfma, ora, Xo, cn, cdn, 24, **kw)
+    note("prune mfma vs simt / oracle: rows differing", int((g_mfma != g_simt).any(1).sum()),
+         int((g_mfma != ora).any(1).sum()), "beyond near-ties", a, b)
+    assert a == [] and b == []
 
 
 def test_many_branches_keep_recall_in_every_layout(monkeypatch):
