@@ -422,18 +422,17 @@ def run_code_sweep(index, Q, truth, k, cfg, nq):
     return rows, frontier, codes_s
 
 
-def run_c4(a, dev):
+def c4_rows(dev, n, npool, reps_scale=1.0):
     """Config C4: p50/p99 latency of one batch (1, 8, 64, 512 queries) at
     branches 32 and 128, queue 12, team 32, the other knobs at their defaults,
-    each batch drawn uniformly from a 2,048-query pool.  The search is
-    captured once per (branches, batch) as a HIP graph (`Index.capture`, no
-    overflow guard) and replayed; the eager search is timed beside it.  A
-    latency is the host's wall clock from replay to completion."""
+    each batch drawn uniformly from a pool of queries (bench/batch_torch.py:
+    24-41).  The search is captured once per (branches, batch) as a HIP graph
+    (`Index.capture`, no overflow guard) and replayed; the eager search is
+    timed beside it.  A latency is the host's wall clock from replay to
+    completion.  Returns (rows, build seconds, workload text)."""
     import swann_amd
     from swann_amd.build import build_graph
     cfg = dict(CONFIGS["c4"])
-    n = a.n or cfg["n"]
-    npool = a.nq or cfg["nq"]
     k = 10
     t0 = time.perf_counter()
     X32, Qpool = generate(cfg, n, npool, dev)
@@ -455,7 +454,7 @@ def run_c4(a, dev):
         for b in C4_BATCHES:
             knobs = dict(branches=J, queue=12, team=cfg["team"])
             cs = index.capture(b, k=k, **knobs)
-            reps = {1: 200, 8: 100, 64: 40, 512: 12}[b]
+            reps = max(5, int({1: 200, 8: 100, 64: 40, 512: 12}[b] * reps_scale))
             lat_g, lat_e, hits = [], [], 0.0
             for r in range(reps + 2):
                 idx = torch.from_numpy(rng.choice(npool, size=b, replace=False)).to(dev)
@@ -484,18 +483,84 @@ def run_c4(a, dev):
             rows.append(row)
             del cs
             torch.cuda.empty_cache()
+    workload = (f"C4: n={n:,} x d={cfg['d']} fp16 ip (lowrank {cfg['rank']}), "
+                f"pool of {npool:,} fp32 queries, D={cfg['D']}, k={k}, queue=12, "
+                f"team={cfg['team']}, budget=64, stop_eps=0.05, overflow guard off")
+    del index, G, X, Qpool, truth
+    torch.cuda.empty_cache()
+    return rows, build_s, workload
+
+
+def run_c4(a, dev):
+    """`--config c4`: the C4 latency table as its own JSON line."""
+    cfg = CONFIGS["c4"]
+    rows, build_s, workload = c4_rows(dev, a.n or cfg["n"], a.nq or cfg["nq"])
     out = {
         "metric": "C4 per-batch latency p50/p99 (hipGraph replay) and recall@10",
         "unit": "ms", "higher_is_better": False, "n_gpus": 1, "dtype": "f32",
         "data": "synthetic (generated on the GPU from fixed seeds; graph built by this library)",
-        "config": {"workload": f"C4: n={n:,} x d={cfg['d']} fp16 ip (lowrank {cfg['rank']}), "
-                               f"pool of {npool:,} fp32 queries, D={cfg['D']}, k={k}, "
-                               f"queue=12, team={cfg['team']}, budget=64, stop_eps=0.05, "
-                               f"overflow guard off"},
+        "config": {"workload": workload},
         "build_s": round(build_s, 2),
         "rows": rows,
     }
     print(json.dumps(out), flush=True)
+
+
+def advance_bytes(st, nq, J, d, elem, D):
+    """Algorithmic bytes of one advance launch from the kernel's own counters:
+    rows scored x d x element size + expansions x D x 4 (the reference's
+    convention, bench/batch_torch.py:121-128); init scored the seeds."""
+    evals = int(st.dist_evals.sum()) - int(nq * J)
+    exps = int(st.expansions.sum())
+    return evals * d * elem + exps * D * 4
+
+
+def c2_rows(dev, n, nq, steps=3):
+    """Config C2 beside the headline: 1M x 960 fp32 l2 mixture, graph D = 64
+    from C = 128, the search at the config's knobs (32 branches, queue 12,
+    budget 64) over its stop_eps sweep.  Each row: QPS over `steps` timed
+    searches of the whole batch (select + init + advance + merge), recall@10
+    against exact fp32 ground truth, and the advance kernel's algorithmic
+    bytes over its HIP-event time against 8 TB/s."""
+    import swann_amd
+    cfg = dict(CONFIGS["c2"], queue=12, budget=64)
+    k = 10
+    t0 = time.perf_counter()
+    X, Q = generate(cfg, n, nq, dev)
+    truth = ground_truth(X, Q, k, cfg["metric"])
+    torch.cuda.synchronize()
+    log(f"c2: generated n={n} d={cfg['d']} nq={nq} in {time.perf_counter() - t0:.1f}s")
+    G, build_s, stages = timed_build(X, cfg)
+    log(f"c2: graph built in {build_s:.2f}s {stages}")
+    index = swann_amd.Index(X, G, metric="l2")
+    srch = Searcher(index, Q, k, cfg)
+    rows = []
+    for eps in EPS_SWEEP:
+        srch.step(eps)
+        torch.cuda.synchronize()
+        adv, t1 = [], time.perf_counter()
+        for _ in range(steps):
+            ids, _, st = srch.step(eps, record=True)
+            torch.cuda.synchronize()
+            adv.append(srch.phase_ms()["advance"])
+        dt = (time.perf_counter() - t1) / steps
+        adv_s = float(np.mean(adv)) / 1e3
+        nbytes = advance_bytes(st, nq, cfg["branches"], cfg["d"], 4, G.shape[1])
+        row = dict(branches=cfg["branches"], queue=12, budget=64, stop_eps=eps,
+                   recall=round(recall(ids, truth, k), 4), qps=round(nq / dt, 1),
+                   roofline={"bound": "hbm", "achieved": round(nbytes / adv_s / 1e9, 1),
+                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                             "frac": round(nbytes / adv_s / HBM_PEAK, 4),
+                             "kernel": "advance_kernel", "bytes_per_launch": nbytes,
+                             "launch_ms": round(adv_s * 1e3, 3)})
+        log("c2", row)
+        rows.append(row)
+    workload = (f"C2: n={n:,} x d={cfg['d']} fp32 l2 (gmm), {nq:,} fp32 queries, "
+                f"D={cfg['D']}, C={cfg['cand']}, k={k}, team={cfg['team']}")
+    del srch, index, G, X, Q, truth
+    torch.cuda.empty_cache()
+    return dict(workload=workload, build_s=round(build_s, 2), build_stages_s=stages,
+                eps_sweep=rows, best_at_0_95=cheapest(rows, TARGET_RECALL))
 
 
 def main():
@@ -515,6 +580,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c5-build", action="store_true",
                     help="skip the C5 graph build reported beside the C3 headline")
+    ap.add_argument("--no-c2", action="store_true",
+                    help="skip the C2 search rows reported beside the C3 headline")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="skip the C4 latency rows reported beside the C3 headline")
     ap.add_argument("--sweep", action="store_true",
                     help="print the recall-QPS grid and its frontier instead of the headline")
     ap.add_argument("--sweep-codes", action="store_true",
@@ -650,9 +719,7 @@ def main():
 
     # algorithmic bytes of the advance kernel, from its own counters
     elem = 2 if cfg["dtype"] == "f16" else 4
-    evals = int(st.dist_evals.sum()) - int(nq * cfg["branches"])   # init scored the seeds
-    exps = int(st.expansions.sum())
-    adv_bytes = evals * cfg["d"] * elem + exps * G.shape[1] * 4
+    adv_bytes = advance_bytes(st, nq, cfg["branches"], cfg["d"], elem, G.shape[1])
     adv_s = float(np.mean(adv_ms)) / 1e3
     achieved = adv_bytes / adv_s
     ph_mean = {k2: round(float(np.mean([p[k2] for p in phases])), 3) for k2 in phases[0]}
@@ -717,6 +784,15 @@ def main():
         del X5
         torch.cuda.empty_cache()
 
+    # configs C2 and C4 at their own shapes, beside the headline
+    c2 = c4 = None
+    if a.config == "c3" and not a.no_c2:
+        c2 = c2_rows(dev, a.n or CONFIGS["c2"]["n"], a.nq or CONFIGS["c2"]["nq"])
+    if a.config == "c3" and not a.no_c4:
+        rows4, b4_s, w4 = c4_rows(dev, a.n // 2 or CONFIGS["c4"]["n"], CONFIGS["c4"]["nq"],
+                                  reps_scale=0.5)
+        c4 = dict(workload=w4, build_s=round(b4_s, 2), rows=rows4)
+
     out = {
         "metric": "QPS at recall@10=0.95 (1 GPU) + achieved HBM GB/s fraction; build s/1M rows",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
@@ -746,6 +822,8 @@ def main():
         "cpu_baseline": cpu,
         "with_codes": with_codes,
         "build_c5": build_c5,
+        "c2": c2,
+        "c4": c4,
     }
     print(json.dumps(out), flush=True)
 

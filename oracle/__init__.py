@@ -32,7 +32,7 @@ LIB = HERE / "_build" / "libswann_oracle.so"
 METRIC_IP, METRIC_L2 = 0, 1
 POLICY_BEST, POLICY_ROUND_ROBIN = 0, 1
 # when a branch's step reads the shared bound (so_search_query)
-SCHEDULES = {"serial": 0, "rounds": 1}
+SCHEDULES = {"serial": 0, "rounds": 1, "rounds2": 2}
 NCTR = 10
 F32, F16 = 0, 1
 

@@ -44,6 +44,7 @@
 #define SO_CPROBE 32
 #define SO_SCHED_SERIAL 0   /* so_search_query: bound read as the previous step left it */
 #define SO_SCHED_ROUNDS 1   /* ... as it was when the round began */
+#define SO_SCHED_ROUNDS2 2  /* ... as it was when the round before began */
 #define SO_MAXD 128
 #define SO_MAXL 512
 
@@ -567,10 +568,13 @@ void so_search_query(const void* X, int dt, int dim, const int32_t* G, int D,
     }
     so_locals* lo = (so_locals*)malloc(sizeof(so_locals) * (size_t)J);
     for (int j = 0; j < J; ++j) so_locals_reset(&lo[j]);
+    float prev = bound;                     /* the bound when the previous round began */
     for (int s = 0; s < B; ++s) {
         int alive = 0;
         const float snap = bound;
-        c.bound_rd = (sched == SO_SCHED_ROUNDS) ? &snap : NULL;
+        const float lag2 = prev;
+        prev = snap;
+        c.bound_rd = (sched == SO_SCHED_ROUNDS) ? &snap : (sched == SO_SCHED_ROUNDS2) ? &lag2 : NULL;
         for (int j = 0; j < J; ++j) {
             if (lo[j].done) continue;
             if (!so_step(&c, ids + (int64_t)j * L, dist + (int64_t)j * L,

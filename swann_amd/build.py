@@ -38,15 +38,6 @@ def _rows(X):
     return X.contiguous()
 
 
-def pairwise(A, B, metric, bn=None):
-    """Distances from every row of A to every row of B (swann/build.py:14-25)."""
-    if _m(metric) == 0:
-        return 1.0 - (A @ B.T)
-    if bn is None:
-        bn = (B * B).sum(1)
-    return (bn.view(1, -1) - 2.0 * (A @ B.T) + (A * A).sum(1).view(-1, 1)).clamp(min=0)
-
-
 @torch.no_grad()
 def knn_candidates(Xg, C, chunk=4096, metric="ip"):
     """Exact top-C neighbours by the corpus's metric, self excluded

@@ -1017,9 +1017,15 @@ int sweep_cap(int C) {
 
 bool use_mfma(int dim) { return dim % 8 == 0; }
 
-// Candidates the fp32 screen keeps per row before the exact re-rank.
+// An fp32 corpus on the MFMA path is swept on an fp16 screen and its lists
+// re-ranked in exact fp32; fp16 corpora and the fp32 SIMT sweep are exact.
+bool screened(int x_dtype, int dim) { return x_dtype == SWANN_DTYPE_F32 && use_mfma(dim); }
+
+// Candidates the fp32 screen keeps per row before the exact re-rank (at
+// least C: when C + 32 exceeds n or the sweep's list limit the screen keeps
+// what it can, and the re-rank still replaces every distance by the exact one).
 int screen_count(int C, int64_t n, int x_dtype, int dim) {
-    if (x_dtype == SWANN_DTYPE_F16 || !use_mfma(dim)) return C;
+    if (!screened(x_dtype, dim)) return C;
     int64_t cs = C + 32;
     if (cs > kMaxC) cs = kMaxC;
     if (cs > n) cs = n;
@@ -1041,7 +1047,7 @@ int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C) {
     const int cap = use_mfma(dim) ? sweep_mfma_cap(Cs) : sweep_cap(C);
     const int64_t G = use_mfma(dim) ? sweep_mfma_splits(n, dim) : 1;
     int64_t b = align256(n * 4) + align256(n * G * cap * 4) * 2 + align256(n * G * 4);
-    if (Cs != C) b += align256(n * (int64_t)Cs * 4) * 2;
+    if (screened(x_dtype, dim)) b += align256(n * (int64_t)Cs * 4) * 2;
     if (use_mfma(dim)) b += sweep_mfma_extra_bytes(n, dim, x_dtype);
     return b;
 }
@@ -1061,7 +1067,8 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     hipStream_t st = (hipStream_t)stream;
     const bool mf = use_mfma(dim);
     const int Cs = screen_count(C, n, x_dtype, dim);
-    SWANN_REQUIRE(Cs == C || dim * 4 <= 64 * 1024, "sweep: dimension too large for the re-rank");
+    const bool rerank = screened(x_dtype, dim);
+    SWANN_REQUIRE(!rerank || dim * 4 <= 64 * 1024, "sweep: dimension too large for the re-rank");
     const int cap = mf ? sweep_mfma_cap(Cs) : sweep_cap(C);
     const int G = mf ? sweep_mfma_splits(n, dim) : 1;
     char* ws = (char*)workspace;
@@ -1071,7 +1078,7 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     int32_t* bcnt = (int32_t*)ws; ws += align256(n * (int64_t)G * 4);
     int32_t* scand = nullptr;
     float* scd = nullptr;
-    if (Cs != C) {
+    if (rerank) {
         scand = (int32_t*)ws; ws += align256(n * (int64_t)Cs * 4);
         scd = (float*)ws; ws += align256(n * (int64_t)Cs * 4);
     }
@@ -1100,7 +1107,7 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
     const int most = Gu > 1 ? Gu * Cs : cap;
     int np = 2;
     while (np < most) np <<= 1;
-    if (Cs == C) {
+    if (!rerank) {
         hipLaunchKernelGGL(sweep_final, dim3((unsigned)n), dim3(256), (size_t)np * 8, st, bkey, bid,
                            bcnt, n, cap, Gu, C, mf ? 1 : 0, perm, cand, cdist);
         return launch_status("sweep final");

@@ -167,9 +167,11 @@ def main(argv=None):
     t3 = time.perf_counter()
     Gc = G.cpu().numpy().astype(np.int32)
     filled = (Gc >= 0).sum(1)
-    print(f"candidates {t1 - t0:.2f}s  prune {t2 - t1:.2f}s  reverse {t3 - t2:.2f}s  "
-          f"total {t3 - t0:.2f}s")
-    print(f"out-degree: min/med/max {filled.min()}/{int(np.median(filled))}/{filled.max()}")
+    stages = {"candidates": t1 - t0, "prune": t2 - t1, "reverse+extras": t3 - t2}
+    print("[build] " + ", ".join(f"{k} {v:.2f} s" for k, v in stages.items()) +
+          f" (total {t3 - t0:.2f} s)")
+    print(f"[build] out-degree range {filled.min()}..{filled.max()}, "
+          f"median {int(np.median(filled))}")
     np.save(a.data / a.out, Gc)
     np.save(a.data / (Path(a.out).stem + "_deg.npy"), filled.astype(np.int32))
     (a.data / (Path(a.out).stem + ".json")).write_text(json.dumps(
@@ -179,7 +181,7 @@ def main(argv=None):
              seconds=round(t3 - t0, 2),
              stage_seconds=dict(candidates=round(t1 - t0, 2), prune=round(t2 - t1, 2),
                                 reverse=round(t3 - t2, 2))), indent=2))
-    print(f"wrote {a.data / a.out}")
+    print(f"[build] graph saved to {a.data / a.out}")
 
 
 if __name__ == "__main__":

@@ -201,12 +201,25 @@ def test_c3_headline_knobs_match_the_oracle_rounds_schedule(c3):
 
 
 @pytest.mark.parametrize("eps", [0.02, 0.05, 0.1, 0.2])
-def test_c3_stated_knobs_match_the_oracle_rounds_schedule(c3, eps):
+def test_c3_stated_knobs_match_the_oracle_schedules(c3, eps):
     """C3 at the knobs the config states (32 branches, team 16) with the
     reference's queue 12 and budget 64 (swann/index.py:40-45), over the
-    stop_eps sweep: Index.search (claim bits) against the oracle's rounds
-    schedule with claim bits on the same seeds, recall@10 within 0.005 over
-    2,000 queries; distances equal an fp64 recomputation, no id twice."""
+    stop_eps sweep, 2,000 queries, Index.search (claim bits) against the
+    oracle with claim bits on the same seeds.
+
+    The shared bound is racy: a step reads it at some point after other
+    branches' steps lowered it (local_search.cu:466-469, :655-658), so
+    where a tight stop_eps lets it end branches early the recall depends on
+    how stale the bound a step reads is.  Two legal schedules bracket the
+    concurrent launch: every step of round s reading the bound as round s
+    began ("rounds") and as round s - 1 began ("rounds2"); the GPU's recall
+    must lie between them, widened by 0.005 -- within 0.005 of both where
+    they agree.  At eps 0.02, where they differ most, the bound's part is
+    separated out: with the bound off (claims kept) the GPU and the oracle
+    must agree within 0.005.  Distances equal an fp64 recomputation, no id
+    twice."""
+    import os
+    from swann_amd import _engine as E
     from swann_amd import _select as S
     X16, G = c3["X16"], c3["G"]
     Q = torch.cat([c3["Q"], c3["Q2"]])
@@ -218,17 +231,29 @@ def test_c3_stated_knobs_match_the_oracle_rounds_schedule(c3, eps):
     def rec(ids):
         return float(np.mean([len(set(a) & set(b)) / 10 for a, b in zip(ids.tolist(),
                                                                         truth.tolist())]))
-    import os
-    oi, _ = O.search_batch(X16.cpu().numpy(), G.cpu().numpy(), Q.cpu().numpy(),
-                           seeds.cpu().numpy(), k=10, L=L, B=Bud, metric=0, team=16,
-                           stop_eps=eps, H=1, Hc=None, bound=True, exclusive=True,
-                           nthreads=len(os.sched_getaffinity(0)), schedule="rounds",
-                           claim_bits=True)
+    Xh, Gh, Qh, Sh = X16.cpu().numpy(), G.cpu().numpy(), Q.cpu().numpy(), seeds.cpu().numpy()
+    cores = len(os.sched_getaffinity(0))
+
+    def oracle(schedule, bound=True):
+        oi, _ = O.search_batch(Xh, Gh, Qh, Sh, k=10, L=L, B=Bud, metric=0, team=16,
+                               stop_eps=eps, H=1, Hc=None, bound=bound, exclusive=True,
+                               nthreads=cores, schedule=schedule, claim_bits=True)
+        return rec(oi)
+    r1, r2 = oracle("rounds"), oracle("rounds2")
     ids, dist = index.search(Q, k=10, branches=J, queue=L, budget=Bud, stop_eps=eps, team=16)
-    r_gpu, r_oracle = rec(ids), rec(oi)
+    r_gpu = rec(ids)
     note("c3 stated knobs eps", eps, "queries", Q.shape[0], "Index.search", r_gpu,
-         "oracle rounds", r_oracle)
-    assert abs(r_gpu - r_oracle) <= 0.005
+         "oracle rounds", r1, "rounds2", r2)
+    assert min(r1, r2) - 0.005 <= r_gpu <= max(r1, r2) + 0.005
+    if eps == 0.02:
+        r_off = oracle("rounds", bound=False)
+        ids_off, _, _ = E.search(X16, G, Q, seeds, k=10, L=L, B=Bud, metric=0, team_size=16,
+                                 stop_eps=eps, shared_cache=True, shared_bound=False,
+                                 exclusive=True, elide_visited=True, check=False,
+                                 claim_bits=True)
+        r_gpu_off = rec(ids_off.cpu().numpy())
+        note("c3 stated knobs eps", eps, "bound off: gpu", r_gpu_off, "oracle", r_off)
+        assert abs(r_gpu_off - r_off) <= 0.005
     assert (ids >= 0).all() and all(len(set(r)) == 10 for r in ids.tolist())
     ids_t = torch.from_numpy(ids.astype(np.int64)).cuda()
     exact = 1.0 - (X16[ids_t.reshape(-1)].double().reshape(-1, 10, DIM)

@@ -266,7 +266,7 @@ def test_claims_keep_branches_disjoint():
         assert r["cache_d"][slot] == O.team_distance(q, X, v, O.METRIC_IP, 32)
 
 
-@pytest.mark.parametrize("schedule", ["serial", "rounds"])
+@pytest.mark.parametrize("schedule", ["serial", "rounds", "rounds2"])
 def test_claim_bits_decide_like_a_table_that_never_fails(schedule):
     """Exclusive claims as one bit per row equal the (id, d) table wherever
     the table's probes never fail: every queue, lineage and counter.  A
@@ -296,7 +296,7 @@ def test_claim_bits_decide_like_a_table_that_never_fails(schedule):
         O.search_query(X, G, Q[0], seeds, claim_bits=True, L=12, B=24, H=1, exclusive=False)
 
 
-@pytest.mark.parametrize("schedule", ["serial", "rounds"])
+@pytest.mark.parametrize("schedule", ["serial", "rounds", "rounds2"])
 @pytest.mark.parametrize("kstop", [1, 5, 10, 40])
 @pytest.mark.parametrize("exclusive", [False, True])
 def test_bound_is_the_least_kth_distance_any_branch_reached(kstop, exclusive, schedule):
@@ -343,7 +343,7 @@ def _bound_case():
     return X, G, np.zeros(4, np.float32)
 
 
-@pytest.mark.parametrize("schedule", ["serial", "rounds"])
+@pytest.mark.parametrize("schedule", ["serial", "rounds", "rounds2"])
 @pytest.mark.parametrize("near_first", [True, False])
 def test_bound_stops_a_branch_its_own_radius_would_not(near_first, schedule):
     """Two branches of one query, the near one seeded at node 0, the far one
@@ -355,8 +355,10 @@ def test_bound_stops_a_branch_its_own_radius_would_not(near_first, schedule):
     before it left it: stepped after the near branch the far one expands
     nothing; stepped before it, exactly one node.  In rounds, both branches'
     first steps read the bound the round began with (FLT_MAX), so the far
-    branch expands exactly one node in either order.  A bound that is read
-    but ignored, or never lowered, gives 4."""
+    branch expands exactly one node in either order; in rounds2 a step reads
+    the bound as the round before began, so the far branch's second step
+    still reads FLT_MAX and it expands exactly two.  A bound that is read but
+    ignored, or never lowered, gives 4."""
     X, G, q = _bound_case()
     seeds = np.array([0, 5] if near_first else [5, 0], np.int32)
     far = 1 if near_first else 0
@@ -364,13 +366,32 @@ def test_bound_stops_a_branch_its_own_radius_would_not(near_first, schedule):
     alone = O.search_query(X, G, q, seeds, bound=False, **kw)
     assert alone["counters"][far, 0] == 4
     r = O.search_query(X, G, q, seeds, bound=True, **kw)
-    want = (0 if near_first else 1) if schedule == "serial" else 1
+    want = {"serial": 0 if near_first else 1, "rounds": 1, "rounds2": 2}[schedule]
     assert r["counters"][far, 0] == want
     assert r["counters"][far, 3] == 1
     assert r["counters"][1 - far, 0] == 2          # node 0, then node 1
     assert r["bound"] == np.float32(0.25)
     # the near branch is untouched by the bound: it owns the bound's value
     assert np.array_equal(r["ids"][1 - far], alone["ids"][1 - far])
+
+
+def test_schedules_agree_without_a_bound():
+    """The three schedules differ only in when a branch sees the shared
+    bound: with the bound off they give the same queues, bit for bit (claims
+    land at once in all three)."""
+    X = gaussian(3000, 32, 95, True)
+    from test_oracle_helpers import knn_graph
+    G = knn_graph(X, 16, 0)
+    Q = gaussian(4, 32, 96, True)
+    seeds = np.random.default_rng(97).integers(0, 3000, (4, 8)).astype(np.int32)
+    out = {}
+    for sch in ("serial", "rounds", "rounds2"):
+        oi, od = O.search_batch(X, G, Q, seeds, k=10, L=12, B=20, team=16, stop_eps=0.05,
+                                H=1, Hc=None, bound=False, exclusive=True, schedule=sch,
+                                claim_bits=True, nthreads=2)
+        out[sch] = (oi, od.tobytes())
+    assert all(np.array_equal(out[s][0], out["serial"][0]) and out[s][1] == out["serial"][1]
+               for s in out)
 
 
 # -- merge ----------------------------------------------------------------------
