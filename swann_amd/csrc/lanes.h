@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace swann {
 
 // The value held by lane l + OFF, for lane l of an aligned group of 2*OFF
@@ -55,6 +57,21 @@ __device__ __forceinline__ float team_fold_add(float acc) {
     if constexpr (TEAM >= 8) acc = acc + lane_up<4>(acc);
     if constexpr (TEAM >= 4) acc = acc + lane_up<2>(acc);
     if constexpr (TEAM >= 2) acc = acc + lane_up<1>(acc);
+    return acc;
+}
+
+// The same fold for integers (exact in any order): lane_up moves bits only.
+template <int TEAM>
+__device__ __forceinline__ int team_fold_add_i32(int acc) {
+    auto up = [](int v, auto off) {
+        return __builtin_bit_cast(int, lane_up<decltype(off)::value>(__builtin_bit_cast(float, v)));
+    };
+    if constexpr (TEAM >= 64) acc += up(acc, std::integral_constant<int, 32>{});
+    if constexpr (TEAM >= 32) acc += up(acc, std::integral_constant<int, 16>{});
+    if constexpr (TEAM >= 16) acc += up(acc, std::integral_constant<int, 8>{});
+    if constexpr (TEAM >= 8) acc += up(acc, std::integral_constant<int, 4>{});
+    if constexpr (TEAM >= 4) acc += up(acc, std::integral_constant<int, 2>{});
+    if constexpr (TEAM >= 2) acc += up(acc, std::integral_constant<int, 1>{});
     return acc;
 }
 

@@ -228,6 +228,63 @@ __device__ __forceinline__ float team_code_ip(const float* __restrict__ sq,
     return 1.f - (alpha * (2.f * acc - qsum) + qmu);
 }
 
+// A cheap, bounded stand-in for the estimate's sum, so that the exact
+// summation above runs only where the decision is close.  The query is
+// quantised once per call to integers k_i = rint(q_i / s), |k_i| <= 2047,
+// s = max |q| / 2047, stored as twelve bit planes of u_i = k_i + 2048 (plane
+// b of code word w: bit j set when bit b of u_{32w + j} is), so that over a
+// code word's set bits sum k_i = sum_b 2^b popcount(bits & plane_b) - 2048
+// popcount(bits): two VALU a plane and word (and, count) where the exact sum
+// takes three a bit.  Integer sums are exact, so S' = s * K differs from the
+// exact real sum S over the set bits by at most E = sum_i |q_i - s k_i|, and
+// S from the reference-order fp32 sum by at most (dim + 64) u sum |q_i|
+// (u = 2^-24; no summation path in the lane loop and team fold is longer).
+// The estimate 1 - (alpha (2 S - sum q) + <q, mu>) is monotone in S in fp32
+// too (every operation rounds monotonically), so evaluating it at
+// S' + delta and S' - delta brackets the value the reference computes:
+// when both ends fall on one side of the line the decision is the
+// reference's, bit for bit; otherwise the exact sum decides.
+constexpr int kPlanes = 12;
+constexpr int kPlaneOff = 1 << (kPlanes - 1);
+
+// Sum of k_i over the set bits of a lane's words (w = tl, tl + TEAM, ...)
+// folded over the team: exact integer arithmetic, the total in lane 0.
+template <int TEAM>
+__device__ __forceinline__ int team_code_k(const uint32_t* __restrict__ cpl,
+                                           const int32_t* __restrict__ code, int nw32, int dim,
+                                           int tl) {
+    uint32_t cnt[kPlanes];
+#pragma unroll
+    for (int b = 0; b < kPlanes; ++b) cnt[b] = 0u;
+    uint32_t nb = 0u;
+    for (int w0 = tl; w0 < nw32; w0 += kCodeWords * TEAM) {
+        unsigned wb[kCodeWords];
+        code_fetch<TEAM>(code, w0, nw32, wb);
+#pragma unroll
+        for (int j = 0; j < kCodeWords; ++j) {
+            const int w = w0 + j * TEAM;
+            if (w >= nw32) break;
+            uint32_t bits = wb[j];
+            const int base = w * 32;
+            if (base + 32 > dim) bits &= (1u << (dim - base)) - 1u;
+            const uint4* p4 = reinterpret_cast<const uint4*>(cpl + w * kPlanes);
+#pragma unroll
+            for (int c = 0; c < kPlanes / 4; ++c) {
+                const uint4 p = p4[c];
+                cnt[4 * c + 0] += __builtin_popcount(bits & p.x);
+                cnt[4 * c + 1] += __builtin_popcount(bits & p.y);
+                cnt[4 * c + 2] += __builtin_popcount(bits & p.z);
+                cnt[4 * c + 3] += __builtin_popcount(bits & p.w);
+            }
+            nb += __builtin_popcount(bits);
+        }
+    }
+    int k = -kPlaneOff * (int)nb;
+#pragma unroll
+    for (int b = 0; b < kPlanes; ++b) k += (int)(cnt[b] << b);
+    return team_fold_add_i32<TEAM>(k);
+}
+
 // Per-branch visited set: open addressing, linear probe, slot = key + 1
 // (local_search.cu:94-110).  Private to the workgroup.
 __device__ __forceinline__ int vis_insert(int* tab, int H, int key, int* fail) {
@@ -522,7 +579,10 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
 
     // LDS carve-up; sizes must match advance_lds() on the host
     float* sq = reinterpret_cast<float*>(smem);
-    int* qa_id = reinterpret_cast<int*>(sq + dimp);
+    // the query's bit planes for the code estimate (code_planes words)
+    const int nw32 = (a.dim + 31) >> 5;
+    uint32_t* cpl = reinterpret_cast<uint32_t*>(sq + dimp);
+    int* qa_id = reinterpret_cast<int*>(cpl + (a.codes ? nw32 * kPlanes : 0));
     float* qa_d = reinterpret_cast<float*>(qa_id + L);
     int* qb_id = reinterpret_cast<int*>(qa_d + L);
     float* qb_d = reinterpret_cast<float*>(qb_id + L);
@@ -548,6 +608,8 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     __shared__ int s_npass;
     __shared__ unsigned s_retired[8];
     __shared__ float s_best_k, s_rad, s_qmu, s_qsum;
+    __shared__ float s_cscale, s_cdelta;
+    __shared__ int s_namb;
 
     int32_t* vis = a.visited + flat * (int64_t)a.H;
     int32_t* ctr = a.counters + flat * kNctr;
@@ -583,6 +645,53 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         m = team_fold_add<64>(m);
         s = team_fold_add<64>(s);
         if (lane == 0) { s_qmu = m; s_qsum = s; }
+        // the cheap estimate's quantisation: scale, bit planes, error bound
+        // (any summation order: these only bound, they decide nothing alone)
+        float amax = 0.f, sabs = 0.f;
+        for (int t = lane; t < a.dim; t += 64) {
+            const float qt = fabsf(sq[qpad(t)]);
+            amax = fmaxf(amax, qt);
+            sabs = sabs + qt;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            sabs = sabs + __shfl_xor(sabs, off, 64);
+        }
+        const float cs = amax / (float)(kPlaneOff - 1);
+        const float inv = cs > 0.f ? 1.f / cs : 0.f;
+        float err = 0.f;
+        for (int w = lane; w < nw32; w += 64) {
+            uint32_t pl[kPlanes];
+#pragma unroll
+            for (int b = 0; b < kPlanes; ++b) pl[b] = 0u;
+            for (int j = 0; j < 32 && w * 32 + j < a.dim; ++j) {
+                const float qt = sq[qpad(w * 32 + j)];
+                float kq = rintf(qt * inv);
+                kq = fminf(fmaxf(kq, -(float)(kPlaneOff - 1)), (float)(kPlaneOff - 1));
+                err = err + fabsf(qt - cs * kq);
+                const uint32_t u = (uint32_t)((int)kq + kPlaneOff);
+#pragma unroll
+                for (int b = 0; b < kPlanes; ++b) pl[b] |= ((u >> b) & 1u) << j;
+            }
+#pragma unroll
+            for (int b = 0; b < kPlanes; ++b) cpl[w * kPlanes + b] = pl[b];
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) err = err + __shfl_xor(err, off, 64);
+        if (lane == 0) {
+            // E as summed here rounds: bound it from above (dim u relative for
+            // the sum, 4 u |q_i| a term for the rounded products and
+            // differences), then add the reference sum's own rounding
+            const float u = 5.9604645e-08f;
+            const float e = err * 1.002f + 8.f * u * sabs;
+            const float dl = (e + ((float)a.dim + 64.f) * u * 1.01f * sabs + u * (sabs + e)) *
+                             1.001f;
+            s_cscale = cs;
+            // a query with a NaN or infinity leaves no usable bound: every
+            // decision then takes the exact sum
+            s_cdelta = (dl == dl && dl < INFINITY && cs == cs && cs < INFINITY) ? dl : INFINITY;
+        }
     }
     if (a.codes) __syncthreads();
 
@@ -653,7 +762,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                 } else {
                     s_ctr[3] = 1;
                 }
-                s_nwork = 0; s_nkeep = 0; s_nbr = 0; s_cov = 0; s_npass = 0;
+                s_nwork = 0; s_nkeep = 0; s_nbr = 0; s_cov = 0; s_npass = 0; s_namb = 0;
             }
         }
         for (int i = tid; i < nsort; i += BLOCK) { c_id[i] = -1; c_d[i] = FLT_MAX; c_l[i] = 0; }
@@ -720,12 +829,45 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         } else {
             // decide from the code before reading the row (:560-575); a
             // skipped neighbour stays a candidate at FLT_MAX, unscored, with
-            // its table slot claimed but never filled.  Two passes: every
-            // item is estimated and the ones to read are listed (in u_id,
-            // free until the keep step), then the teams score only those,
-            // so no team waits on a row that another team's item needs.
+            // its table slot claimed but never filled.  Three passes: every
+            // item is bracketed by the cheap estimate (team_code_k) and is
+            // skipped, listed to read (u_id) or, when the bracket straddles
+            // the line, listed for the exact estimate (k_id; both free until
+            // the keep step); then the exact estimate decides those; then the
+            // teams score the listed rows, so no team waits on a row that
+            // another team's item needs.
             const float rad = s_rad;
+            const float line = rad + a.cmargin;
+            auto skip = [&](int w, int v) {
+                const int nidx = w_nidx[w] & 0xffff;
+                atomicAdd(&s_ctr[3], 1);
+                c_id[nidx] = v; c_d[nidx] = FLT_MAX; c_l[nidx] = plin;
+            };
             for (int w = team; w < nw; w += NT) {
+                const int v = w_v[w];
+                if (rad == FLT_MAX) {            // no line yet: nothing is skipped
+                    if (tl == 0) u_id[atomicAdd(&s_npass, 1)] = w;
+                    continue;
+                }
+                const int kt = team_code_k<TEAM>(cpl, a.codes + (int64_t)v * a.cwords, nw32,
+                                                 a.dim, tl);
+                if (tl == 0) {
+                    const float al = a.calpha[v];
+                    const float sc = s_cscale * (float)kt;
+                    const float dl = s_cdelta + 1e-6f * (fabsf(sc) + s_cdelta) + 1e-30f;
+                    auto est = [&](float sum) { return 1.f - (al * (2.f * sum - s_qsum) + s_qmu); };
+                    // the two ends bracket the reference's value for either
+                    // sign of alpha; a NaN end fails both tests
+                    const float e1 = est(sc + dl), e2 = est(sc - dl);
+                    if (e1 > line && e2 > line) skip(w, v);
+                    else if (e1 <= line && e2 <= line) u_id[atomicAdd(&s_npass, 1)] = w;
+                    else k_id[atomicAdd(&s_namb, 1)] = w;
+                }
+            }
+            __syncthreads();
+            const int namb = s_namb;
+            for (int k = team; k < namb; k += NT) {
+                const int w = k_id[k];
                 const int v = w_v[w];
                 unsigned head[kCodeWords];
                 code_fetch<TEAM>(a.codes + (int64_t)v * a.cwords, tl, a.cwords, head);
@@ -733,13 +875,8 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
                                                      head, a.calpha[v], s_qmu, s_qsum, a.dim,
                                                      a.cwords, tl);
                 if (tl == 0) {                   // the team's total is in its lane 0
-                    if (rad != FLT_MAX && est > rad + a.cmargin) {
-                        const int nidx = w_nidx[w] & 0xffff;
-                        atomicAdd(&s_ctr[3], 1);
-                        c_id[nidx] = v; c_d[nidx] = FLT_MAX; c_l[nidx] = plin;
-                    } else {
-                        u_id[atomicAdd(&s_npass, 1)] = w;
-                    }
+                    if (est > line) skip(w, v);
+                    else u_id[atomicAdd(&s_npass, 1)] = w;
                 }
             }
             __syncthreads();
@@ -986,10 +1123,12 @@ size_t init_lds(int dim, int V) {
     return (size_t)qpad_floats(dim) * 4 + (size_t)nsort * (4 + 4 + 4 + 4 + 1 + 1 + 1);
 }
 
-size_t advance_lds(int dim, int D, int L) {
+// `codes`: the sign-code filter is on (the query's bit planes join the LDS)
+size_t advance_lds(int dim, int D, int L, bool codes) {
     const int nsort = pow2_at_least(D, 2, kMaxD);
-    return (size_t)qpad_floats(dim) * 4 + (size_t)L * (4 + 4 + 4 + 4) +
-           (size_t)nsort * (4 * 9) + (size_t)L * 4 + (size_t)nsort * 3;
+    return (size_t)qpad_floats(dim) * 4 + (codes ? (size_t)((dim + 31) / 32) * kPlanes * 4 : 0) +
+           (size_t)L * (4 + 4 + 4 + 4) + (size_t)nsort * (4 * 9) + (size_t)L * 4 +
+           (size_t)nsort * 3;
 }
 
 // The table is interleaved (id, d) pairs when cache_d is the word right after
@@ -1174,7 +1313,7 @@ int swann_validate_advance(int64_t n, int dim, int x_dtype, int D, int64_t Q, in
                   "an unnormalised L2 corpus needs int8 codes and a stored squared norm");
     SWANN_REQUIRE(cwords == 0 || (int64_t)cwords * 32 >= dim,
                   "code words do not cover the dimension");
-    const size_t lds = advance_lds(dim, D, L);
+    const size_t lds = advance_lds(dim, D, L, cwords > 0);
     SWANN_REQUIRE(lds <= kMaxLds, "advance needs %zu B of LDS (limit %zu); lower L or the dimension",
                   lds, kMaxLds);
     return SWANN_OK;
@@ -1243,9 +1382,10 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
               codes, codes ? alpha : nullptr, codes ? cmu : nullptr, codes ? cwords : 0,
               code_margin};
     const int block = search_block_for(nb);
-    a.remap = remap_branches(J, team_size, x_dtype, block, advance_lds(dim, D, L)) ? 1 : 0;
+    const size_t lds = advance_lds(dim, D, L, codes != nullptr);
+    a.remap = remap_branches(J, team_size, x_dtype, block, lds) ? 1 : 0;
     SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
-                   advance_lds(dim, D, L), (hipStream_t)stream, a);
+                   lds, (hipStream_t)stream, a);
     return launch_status("advance");
 }
 

@@ -488,6 +488,43 @@ def test_code_filter_matches_oracle(block):
     assert skipped > 0                      # the filter did act
 
 
+@pytest.mark.parametrize("spike", [0.0, 3.0, 40.0])
+def test_code_filter_bracket_and_exact_fallback_match_oracle(spike):
+    """The kernel decides most code estimates from a bracket of the exact
+    sum (a 12-bit quantised query) and takes the exact reference-order sum
+    only where the bracket straddles the line.  A query with one large
+    component (x spike) quantises the rest coarsely, so the bracket is wide
+    and most decisions fall back to the exact sum; without one almost none
+    do.  Every decision must be the reference's: queues and counters
+    bit-exact against the oracle, for teams 4, 16, 64 and several margins."""
+    X, G = toy(seed=7)
+    codes, alpha, mu = O.build_codes(X)
+    rng = np.random.default_rng(29)
+    nq, J, L, budget = 6, 3, 16, 24
+    Qv = gaussian(nq, X.shape[1], 57, True)
+    if spike:
+        Qv[:, 3] += spike
+        Qv = np.ascontiguousarray(Qv, dtype=np.float32)
+    seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
+    Xg, Gg, Qg, Cg, Ag, Mg = to_gpu(X, G, Qv, codes, alpha, mu)
+    skipped = 0
+    for team in (4, 16, 64):
+        for margin in (0.0, 0.02, 0.1):
+            note("code bracket", spike, team, margin)
+            st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=L, B=budget, D=G.shape[1],
+                               team_size=team, stop_eps=0.1, kstop=10)
+            E.advance(Xg, Gg, Qg, st, budget, codes=(Cg, Ag, Mg, margin))
+            for qi in range(nq):
+                for j in range(J):
+                    br = O.init_branch(X, Qv[qi], [int(seeds[qi, j])], L=L, B=budget,
+                                       D=G.shape[1], team=team)
+                    O.advance_branch(X, G, Qv[qi], br, budget, budget, team=team, stop_eps=0.1,
+                                     kstop=10, codes=(codes, alpha, mu, margin))
+                    assert_queue(st, qi, j, br, ("bracket", spike, team, margin, qi, j))
+            skipped += int(st.counters[..., 3].sum())
+    assert skipped > 0
+
+
 @pytest.mark.parametrize("d", [200, 96, 1024])
 def test_code_filter_word_layouts_match_oracle(d):
     """The estimate's word handling: 200 dimensions end inside a word (the

@@ -832,3 +832,32 @@ def test_crowd_retires_a_lineage_after_two_covered_expansions():
     O.advance_branch(X, G, q, br2, 64, 64, metric=O.METRIC_L2, team=4, stop_eps=-1.0, kstop=10,
                      crowd_frac=1.5)
     assert br2.counters[0] == 5 and br2.counters[7] == 0
+
+
+# -- the tie rules the parity tests use -----------------------------------------
+def test_tie_rules_catch_planted_differences():
+    """The comparators the parity tests hold the GPU to (tests/
+    test_oracle_helpers.py) accept only differences at ties: a swap of two
+    entries at distinct distances, a dropped neighbour, or a prune at
+    another alpha (planted on the CPU, in the oracle's outputs) is reported;
+    the same lists, or a swap inside a tie, are not."""
+    from test_oracle_helpers import untied_graph_rows, untied_prune_rows, untied_rows
+    g = golden("refbuild_small.npz")
+    X = g["l2_X"]
+    rc = g["l2_cand"].astype(np.int32); rd = g["l2_cdist"]
+    assert untied_rows(rc, rc, rd, rd) == []
+    swapped = rc.copy()
+    swapped[5, [3, 4]] = swapped[5, [4, 3]]
+    assert untied_rows(swapped, rc, rd, rd) == [5]                 # distinct distances
+    tied_d = rd.copy()
+    tied_d[5, 4] = tied_d[5, 3]
+    assert untied_rows(swapped, rc, tied_d, tied_d) == []          # a tie: either order
+    Gp = O.robust_prune(X, rc, rd, 16, 1.2, O.METRIC_L2, nthreads=2)
+    assert untied_prune_rows(Gp, Gp, X, rc, rd, 16, 1.2, 1) == []
+    other = O.robust_prune(X, rc, rd, 16, 1.25, O.METRIC_L2, nthreads=2)
+    differ = int((other != Gp).any(1).sum())
+    assert differ > 100
+    assert len(untied_prune_rows(other, Gp, X, rc, rd, 16, 1.2, 1)) > 0.9 * differ
+    dropped = Gp.copy()
+    dropped[7, 0] = -1
+    assert untied_graph_rows(dropped, Gp, X, 1) == [7]
