@@ -197,8 +197,11 @@ int swann_select_nearest(const float* Q, int64_t nq, int dim, const float* Vp, i
  * no counterpart in the reference.  It is for callers that cannot allocate
  * device memory -- code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  Its workspace is the library's own
- * fixed array of SWANN_SELECT_SCRATCH_BYTES per GPU (held from the first call
- * on a GPU until the process ends); a call whose
+ * fixed array of SWANN_SELECT_SCRATCH_BYTES per GPU, a file-scope __device__
+ * array of the selection code: it is reserved on a GPU when that code object
+ * first loads there -- any swann_select_nearest call does it, so every
+ * Index.search user holds it, not only callers of this entry point -- and
+ * held until the process ends; a call whose
  * swann_select_workspace_size(nq, P) exceeds that is refused with
  * SWANN_E_INVALID (32 MiB: e.g. 2,000 queries against a 4,096-row
  * catalogue).  Every call on one GPU shares that GPU's array, so calls that

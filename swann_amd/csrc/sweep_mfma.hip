@@ -1972,8 +1972,16 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
 // symmetric sweep's thresholds and overflow count, and its seed pre-pass.
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
-    return al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) + al256(n * 4) + 256 +
-           seed_bytes(n, dim) + repair_bytes(1024);      // cap <= 1024
+    const int64_t base = al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) +
+                         al256(n * 4) + 256;
+    // the locality order, seeds and panel repair run only in the symmetric
+    // direct-load sweep past its seed bands; only a sweep that may take that
+    // path reserves their scratch (a superset of the run's conditions, so the
+    // run never finds less than it needs: a corpus the clustering check
+    // declines at run time, or SWANN_SWEEP_NOSEED, still reserves it)
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    const bool seeded = dim % kBK3 == 0 && sweep_sym(ntile) && ntile > 2 * kSeedBand;
+    return base + (seeded ? seed_bytes(n, dim) + repair_bytes(1024) : 0);   // cap <= 1024
 }
 
 // Column splits of the direct-load sweep: enough workgroups to give every
