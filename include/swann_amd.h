@@ -57,6 +57,30 @@ const char* swann_version(void);
 /* Number of HIP devices visible (0 on a machine without a GPU). */
 int swann_device_count(void);
 
+/* Options: switches that select an alternative code path of the same
+ * computation, for tests that run every path on the same inputs and for
+ * diagnosis.  No counterpart in the reference (its extension has one path
+ * per operation).  Process-wide, read at each call, defaults = the
+ * production path; the library reads no environment variable.
+ *   search_block      0 | 64 | 256 | 1024   advance workgroup size (0: chosen per batch)
+ *   prune_simt        0 | 1   prune Gram on fp32 SIMT instead of MFMA
+ *   prune_f32         0 | 1   fp32 rows' prune Gram on fp32 MFMA, not split fp16 planes
+ *   sweep_sym        -1 | 0 | 1   symmetric sweep by size, never, always (>= 2 panels)
+ *   sweep_waves       16 | 8  waves of a direct-load sweep workgroup
+ *   sweep_rowscale    0 | 1   fp32 corpus screened on a row-scaled plane always
+ *   sweep_regstage    0 | 1   register-staged sweep instead of direct loads
+ *   sweep_sym_fcap    0 | k   room of a symmetric sweep row's second list (k < cap
+ *                             forces its overflow and the recovery paths)
+ *   sweep_noseed      0 | 1   symmetric sweep without the locality order and seeds
+ *   sweep_order       1 | 0   seeded sweep on the locality-ordered copy, or in row order
+ *   sweep_repair_max  4 | k   overflowed row panels up to which each is repaired
+ *                             alone (sixteen ways); more go at once (two ways)
+ * Set an option between calls, not while a call that reads it runs on
+ * another thread.  Unknown names and out-of-range values: SWANN_E_INVALID. */
+int swann_set_option(const char* name, int value);
+int swann_get_option(const char* name, int* value);
+int swann_reset_options(void);
+
 /* ---- search state ------------------------------------------------------
  * Layout (all row-major, contiguous):
  *   X        [n, dim]  fp32 or fp16 (x_dtype)     corpus

@@ -5,15 +5,13 @@ calls raise.  Build it with `python -m swann_amd._build`.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
-import os
 import threading
 from pathlib import Path
 
-# The in-tree build; SWANN_AMD_LIB names another build of the same ABI (used to
-# compare kernel variants side by side).
-LIB_PATH = Path(os.environ.get("SWANN_AMD_LIB") or
-                Path(__file__).resolve().parent / "_lib" / "libswann_amd.so")
+# The in-tree build (swann_amd/_build.py writes it there).
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libswann_amd.so"
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -25,6 +23,9 @@ PROTOTYPES = {
     "swann_last_error": (ctypes.c_char_p, []),
     "swann_version": (ctypes.c_char_p, []),
     "swann_device_count": (I, []),
+    "swann_set_option": (I, [ctypes.c_char_p, I]),
+    "swann_get_option": (I, [ctypes.c_char_p, ctypes.POINTER(I)]),
+    "swann_reset_options": (I, []),
     "swann_validate_init": (I, [I64, I, I, I64, I, I, I, I, I, I, I]),
     "swann_validate_advance": (I, [I64, I, I, I, I64, I, I, I, I, I, I, I, I, I64, I]),
     "swann_init_states": (I, [P, I, I64, I, P, I64, P, I, I, P, P, P, P, I, P, I, P,
@@ -106,3 +107,29 @@ def ptr(t):
 def stream_of(device):
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def set_option(name: str, value: int) -> None:
+    """Select an alternative code path of the same computation (the list and
+    the values are in include/swann_amd.h: swann_set_option).  For tests and
+    diagnosis; every option defaults to the production path."""
+    call("swann_set_option", name.encode(), int(value))
+
+
+def get_option(name: str) -> int:
+    v = I(0)
+    call("swann_get_option", name.encode(), ctypes.byref(v))
+    return int(v.value)
+
+
+@contextlib.contextmanager
+def options(**values):
+    """Set options for the body of a `with`, restoring the earlier values."""
+    old = {k: get_option(k) for k in values}
+    try:
+        for k, v in values.items():
+            set_option(k, v)
+        yield
+    finally:
+        for k, v in old.items():
+            set_option(k, v)

@@ -1151,12 +1151,12 @@ int prune_run(const void* X, int x_dtype, int64_t n, int dim, int metric, const 
               hipStream_t st) {
     // the Gram on MFMA: fp16 rows with 16-byte aligned 16-wide K steps, fp32
     // rows with 16-byte aligned 8-wide K steps
-    const bool simt = getenv_flag("SWANN_PRUNE_SIMT");
+    const bool simt = option_on(kOptPruneSimt);
     const bool mfma16 = x_dtype == SWANN_DTYPE_F16 && dim % 16 == 0 && (uintptr_t)X % 16 == 0;
     const bool mfma32 = x_dtype == SWANN_DTYPE_F32 && dim % 8 == 0 && (uintptr_t)X % 16 == 0;
     // fp32 rows with a workspace for their scales: the Gram on split fp16
-    // planes (SWANN_PRUNE_F32=1 keeps the fp32 MFMA Gram)
-    const bool planes = mfma32 && rscale && !getenv_flag("SWANN_PRUNE_F32");
+    // planes (option prune_f32 keeps the fp32 MFMA Gram)
+    const bool planes = mfma32 && rscale && !option_on(kOptPruneF32);
     if (!simt && mfma16)
         hipLaunchKernelGGL((prune_kernel<_Float16, true>), dim3((unsigned)n), dim3(256), 0, st,
                            (const _Float16*)X, n, dim, metric, cand, cdist, C, deg, alpha,

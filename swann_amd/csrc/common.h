@@ -39,12 +39,27 @@ inline int launch_status(const char* what) {
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
-// A test hook: true when the environment variable is set to a non-zero value
-// (used to run an alternative code path on the same inputs).
-inline bool getenv_flag(const char* name) {
-    const char* e = getenv(name);
-    return e && *e && *e != '0';
-}
+// Switches that select an alternative code path of the same computation,
+// for tests that run every path on the same inputs and for diagnosis; set
+// through swann_set_option (include/swann_amd.h, which lists each one and
+// its values).  Every one defaults to the production path; the library reads
+// no environment variable.
+enum Option {
+    kOptSearchBlock,     // advance workgroup size: 0 chosen per batch, or 64 | 256 | 1024
+    kOptPruneSimt,       // 1: the prune's Gram on fp32 SIMT instead of MFMA
+    kOptPruneF32,        // 1: fp32 rows' prune Gram on fp32 MFMA instead of split fp16 planes
+    kOptSweepSym,        // -1 by size, 0 one-sided, 1 symmetric (from 2 row panels)
+    kOptSweepWaves,      // 16 or 8 waves a direct-load sweep workgroup
+    kOptSweepRowscale,   // 1: an fp32 corpus's screen plane always row-scaled
+    kOptSweepRegstage,   // 1: the register-staged sweep instead of direct loads
+    kOptSweepSymFcap,    // 0, or the room of a row's second list (forces its overflow)
+    kOptSweepNoseed,     // 1: the symmetric sweep without locality order and seeds
+    kOptSweepOrder,      // 1: the seeded sweep on the locality-ordered copy; 0: in row order
+    kOptSweepRepairMax,  // overflowed panels repaired one at a time (more: all at once)
+    kOptCount
+};
+int option(Option o);
+inline bool option_on(Option o) { return option(o) != 0; }
 
 inline int pow2_at_least(int x, int lo, int cap) {
     int n = lo;

@@ -1144,10 +1144,9 @@ int table_stride(const int32_t* cache_id, const float* cache_d, int Hc) {
 }
 
 int search_block_for(int64_t nbranch) {
-    // SWANN_SEARCH_BLOCK=64|256|1024 pins the workgroup size (tests use it to
-    // run every layout on the same inputs); read per call, it costs a getenv.
-    const char* e = getenv("SWANN_SEARCH_BLOCK");
-    const int forced = e ? atoi(e) : 0;
+    // option search_block = 64|256|1024 pins the workgroup size (tests use it
+    // to run every layout on the same inputs)
+    const int forced = option(kOptSearchBlock);
     if (forced == 64 || forced == 256 || forced == 1024) return forced;
     // Batch work fills 256 CUs with one-wave branches.  A batch that cannot
     // gets four waves per branch, and a grid smaller than two branches per

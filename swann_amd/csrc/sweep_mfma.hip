@@ -1255,7 +1255,7 @@ __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
 // maps back.  A row whose threshold stayed loose can still meet its
 // neighbours in one burst that overflows its second list; the merge flags
 // it and its row panel is swept again one-sided (repair_merge).
-// SWANN_SWEEP_ORDER=0 keeps the rows' own order and uses the first
+// option sweep_order = 0 keeps the rows' own order and uses the first
 // kSeedBand bands of the ordered copy as a pre-pass instead: each row's
 // resulting threshold -- the C-th best of real distances, an upper bound of
 // its true C-th -- seeds its threshold in the sweep in row order.  A seed
@@ -1565,23 +1565,16 @@ constexpr int64_t kBandMax = 512;
 
 // Whether the direct-load sweep runs symmetric: by default when there are at
 // least 1,024 row panels (n > 261,888), where every band launch still fills
-// the GPU; SWANN_SWEEP_SYM=0|1 forces it (read per call).
+// the GPU; option sweep_sym = 0|1 forces it.
 inline bool sweep_sym(int64_t ntile) {
-    const char* e = getenv("SWANN_SWEEP_SYM");
-    if (e && *e) return *e != '0' && ntile >= 2;
+    const int f = option(kOptSweepSym);
+    if (f >= 0) return f == 1 && ntile >= 2;
     return ntile >= 1024;
 }
 
-// Waves per direct-load workgroup: 8 (128 x 64 wave tiles) or 16 (64 x 64).
-// SWANN_SWEEP_WAVES=8|16 pins it.
-#ifndef SWANN_SWEEP_WAVES
-#define SWANN_SWEEP_WAVES 16
-#endif
-inline int sweep_waves() {
-    const char* e = getenv("SWANN_SWEEP_WAVES");
-    if (e && *e) return atoi(e) == 16 ? 16 : 8;
-    return SWANN_SWEEP_WAVES;
-}
+// Waves per direct-load workgroup: 16 (64 x 64 wave tiles, the default) or
+// 8 (128 x 64; option sweep_waves).
+inline int sweep_waves() { return option(kOptSweepWaves) == 8 ? 8 : 16; }
 
 }  // namespace
 
@@ -1620,7 +1613,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             return SWANN_E_LAUNCH;
         }
         const float gmax = __builtin_bit_cast(float, hr[0]), gmin = __builtin_bit_cast(float, hr[1]);
-        if (gmax <= 16384.f && gmin >= 0.0625f && !getenv_flag("SWANN_SWEEP_ROWSCALE")) {
+        if (gmax <= 16384.f && gmin >= 0.0625f && !option_on(kOptSweepRowscale)) {
             hipLaunchKernelGGL(rows_to_f16, dim3(nrb), dim3(256), 0, st, (const float*)X, n, dim,
                                h, xn);
             scaled = 0;
@@ -1637,7 +1630,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
     *used = 1;
     // the direct loads address a stage's 256 rows with 32-bit byte offsets
     const bool off32 = (int64_t)dim * 2 * kBM2 < (int64_t(1) << 32);
-    if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && off32 && !getenv_flag("SWANN_SWEEP_REGSTAGE")) {
+    if (dim % kBK3 == 0 && (uintptr_t)hi % 16 == 0 && off32 && !option_on(kOptSweepRegstage)) {
         const int64_t ntile = (n + kBM2 - 1) / kBM2;
         if (splits >= 2 && sweep_sym(ntile) && sweep_waves() == 16) {
             // symmetric sweep: tile (I, J), J >= I, scored once for the rows of
@@ -1653,8 +1646,8 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             s.gthr = gthr;
             s.ovf = ovf;
             s.fcap = cap;
-            if (const char* e = getenv("SWANN_SWEEP_SYM_FCAP")) {   // test hook: force overflow
-                const int f = atoi(e);
+            {                                       // option sweep_sym_fcap: force overflow
+                const int f = option(kOptSweepSymFcap);
                 if (f >= 1 && f < cap) s.fcap = f;
             }
             // the launches of bands [b0, bend), each followed by a merge
@@ -1690,7 +1683,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             int32_t* rid = nullptr;
             int32_t* rcnt = nullptr;
             const int32_t* ordered = nullptr;
-            if (ntile > 2 * kSeedBand && !getenv_flag("SWANN_SWEEP_NOSEED")) {
+            if (ntile > 2 * kSeedBand && !option_on(kOptSweepNoseed)) {
                 bool clustered = false;
                 // the order's workspace (seed_bytes, repair_bytes)
                 float* sk = (float*)extra; extra += al256(n * kSketch * 4);
@@ -1757,8 +1750,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         hipLaunchKernelGGL(group_mean, dim3(P), dim3(kSketch), 0, st, sk,
                                            (const int*)perm, (const int*)pstart, stride, psk);
                 }
-                const char* oe = getenv("SWANN_SWEEP_ORDER");
-                const bool in_order = clustered && !(oe && *oe == '0');
+                const bool in_order = clustered && option_on(kOptSweepOrder);
                 if (in_order) {
                     // pivots chained nearest to nearest (on the host: P^2
                     // distances), rows ordered by their pivot's place in it
@@ -1874,8 +1866,8 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     return SWANN_E_LAUNCH;
                 }
                 SWANN_REQUIRE(np >= 1 && np <= ntile, "sweep: repair panel count out of range");
-                int rmax = 4;                    // panels repaired one at a time, 16 ways
-                if (const char* e = getenv("SWANN_SWEEP_REPAIR_MAX")) rmax = atoi(e);
+                // panels repaired one at a time, 16 ways (option sweep_repair_max)
+                const int rmax = option(kOptSweepRepairMax);
                 if (np <= rmax && C * kRepairSplits <= kRepairSort) {
                     std::vector<int> ph(np);
                     if (hipMemcpyAsync(ph.data(), plist, (size_t)np * 4, hipMemcpyDeviceToHost,
@@ -1978,7 +1970,7 @@ int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     // direct-load sweep past its seed bands; only a sweep that may take that
     // path reserves their scratch (a superset of the run's conditions, so the
     // run never finds less than it needs: a corpus the clustering check
-    // declines at run time, or SWANN_SWEEP_NOSEED, still reserves it)
+    // declines at run time, or option sweep_noseed, still reserves it)
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     const bool seeded = dim % kBK3 == 0 && sweep_sym(ntile) && ntile > 2 * kSeedBand;
     return base + (seeded ? seed_bytes(n, dim) + repair_bytes(1024) : 0);   // cap <= 1024
@@ -1986,21 +1978,12 @@ int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
 
 // Column splits of the direct-load sweep: enough workgroups to give every
 // CU one (small n), and at least kMinSplits so that row panels are read from
-// L2 more than once.  SWANN_SWEEP_SPLIT=1|2|4|8 pins it (read at the first call).
+// L2 more than once.
 #ifndef SWANN_SWEEP_MIN_SPLITS
 #define SWANN_SWEEP_MIN_SPLITS 2
 #endif
 int sweep_mfma_splits(int64_t n, int dim) {
     if (dim % kBK3 != 0) return 1;
-    // read once per process: the workspace a caller sized with one value
-    // must not meet a launch that uses another
-    static const int pinned = [] {
-        const char* e = getenv("SWANN_SWEEP_SPLIT");
-        if (!e || !*e) return 0;
-        const int g = atoi(e);
-        return g == 2 || g == 4 || g == 8 ? g : 1;
-    }();
-    if (pinned) return pinned;
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     int g = SWANN_SWEEP_MIN_SPLITS;
     while (g < 8 && ntile * g < 512) g *= 2;

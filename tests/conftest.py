@@ -60,3 +60,16 @@ def deg96_corpus(tag, g):
     if sha(X) != str(g[f"{tag}_X_sha"]):
         pytest.skip("regenerated inputs differ from the golden inputs on this platform")
     return X
+
+
+@pytest.fixture
+def opt():
+    """Set library options (swann_set_option) for one test; every option is
+    back at its default afterwards."""
+    from swann_amd import _lib
+
+    def set_(**values):
+        for k, v in values.items():
+            _lib.set_option(k, v)
+    yield set_
+    _lib.lib().swann_reset_options()

@@ -37,8 +37,8 @@ def toy(n=2000, d=64, deg=32, seed=0, metric=0):
 
 
 @pytest.fixture(params=["64", "256", "1024"], autouse=False)
-def block(request, monkeypatch):
-    monkeypatch.setenv("SWANN_SEARCH_BLOCK", request.param)
+def block(request, opt):
+    opt(search_block=int(request.param))
     return int(request.param)
 
 
@@ -414,7 +414,8 @@ def test_large_batch_one_wave_layout_matches_oracle():
     Qv = gaussian(nq, 64, 103, True)
     seeds = rng.integers(0, X.shape[0], (nq, J)).astype(np.int32)
     Xg, Gg, Qg = to_gpu(X, G, Qv)
-    os.environ.pop("SWANN_SEARCH_BLOCK", None)
+    from swann_amd import _lib
+    assert _lib.get_option("search_block") == 0          # chosen per batch
     st = E.init_states(Xg, Qg, torch.from_numpy(seeds), L=12, B=30, D=32, team_size=16,
                        stop_eps=0.05)
     E.advance(Xg, Gg, Qg, st, 30)
@@ -746,13 +747,13 @@ def test_nan_distances_never_enter_a_queue():
         assert live[0].any() and live[2].any()
 
 
-def test_branches_spread_over_xcds_match_oracle(monkeypatch):
+def test_branches_spread_over_xcds_match_oracle(opt):
     """48 branches a query of 1024 threads do not fit the 32 workgroups one XCD
     holds, so the advance keeps dispatch order instead of grouping a query's
     branches on one XCD: every branch must still find its own (query,
     branch) state.  Independent branches, queues bit-exact against the
     oracle."""
-    monkeypatch.setenv("SWANN_SEARCH_BLOCK", "1024")
+    opt(search_block=1024)
     X, G = toy(seed=131)
     rng = np.random.default_rng(132)
     nq, J = 3, 48

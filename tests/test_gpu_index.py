@@ -280,12 +280,12 @@ def test_mfma_sweep_matches_oracle(metric, dtype):
     assert (np.diff(cdist.cpu().numpy(), axis=1) >= 0).all()
 
 
-@pytest.mark.parametrize("switch", [("SWANN_SWEEP_WAVES", "8"), ("SWANN_SWEEP_REGSTAGE", "1"),
-                                    ("SWANN_SWEEP_SYM", "1"), ("SWANN_SWEEP_SYM_FCAP", "4"),
-                                    ("SWANN_SWEEP_ROWSCALE", "1")])
+@pytest.mark.parametrize("switch", [("sweep_waves", 8), ("sweep_regstage", 1),
+                                    ("sweep_sym", 1), ("sweep_sym_fcap", 4),
+                                    ("sweep_rowscale", 1)])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtype):
+def test_mfma_sweep_other_layouts_match_oracle(opt, switch, metric, dtype):
     """The direct-load sweep's 8-wave layout (128 x 64 wave tiles), the
     register-staged kernel and the symmetric sweep (each tile scored once for
     both of its panels' rows, in bands of launches), all chosen by
@@ -293,10 +293,11 @@ def test_mfma_sweep_other_layouts_match_oracle(monkeypatch, switch, metric, dtyp
     layout; so does the symmetric sweep whose second lists are made to
     overflow (4 entries of room), which must redo the sweep one-sided, and an
     fp32 corpus screened on a row-scaled fp16 plane (the default takes these
-    corpora's values into fp16 unscaled)."""
-    monkeypatch.setenv(*switch)
-    if switch[0] == "SWANN_SWEEP_SYM_FCAP":
-        monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
+    corpora's values into fp16 unscaled).  Each is an option of the library
+    (swann_set_option), set for the test."""
+    opt(**{switch[0]: switch[1]})
+    if switch[0] == "sweep_sym_fcap":
+        opt(sweep_sym=1)
     n, d = 3001, 64
     X = gaussian(n, d, 431 + metric, metric == 0)
     if metric == 1:
@@ -364,22 +365,22 @@ def oracle_lists(X, C, metric, key):
 @pytest.mark.parametrize("mode", ["order", "seeds", "order-overflow", "order-overflow-16"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype, mode, d):
+def test_mfma_sweep_seeded_thresholds_keep_the_lists(opt, metric, dtype, mode, d):
     """On clustered rows (n = 20,000 of a 60-cluster mixture) the symmetric
     sweep runs on a locality-ordered copy from seeded thresholds ("order", the
     default), or in the rows' own order from the same seeds
-    (SWANN_SWEEP_ORDER=0); with room for only 4 foreign candidates a row,
+    (option sweep_order 0); with room for only 4 foreign candidates a row,
     every panel overflows and is repaired by the one-sided re-sweep of its
     panel, two column halves for all panels at once ("order-overflow") or
     sixteen column ranges a panel at a time with a per-row merge of the
-    sixteen lists ("order-overflow-16", forced by SWANN_SWEEP_REPAIR_MAX).
+    sixteen lists ("order-overflow-16", forced by option sweep_repair_max).
     The lists, mapped back to the rows' own ids, must be those of the plain
-    sweep (SWANN_SWEEP_NOSEED) and the oracle's.  d = 256 takes four K
+    sweep (option sweep_noseed) and the oracle's.  d = 256 takes four K
     steps a tile: the staged foreign queue, its drain after the loop and the
     deferred threshold wait run only there."""
-    monkeypatch.setenv("SWANN_SWEEP_SYM", "1")
+    opt(sweep_sym=1)
     if mode == "seeds":
-        monkeypatch.setenv("SWANN_SWEEP_ORDER", "0")
+        opt(sweep_order=0)
     n, C = 20000, 24
     rng = np.random.default_rng(451 + metric)
     centres = rng.standard_normal((60, d)).astype(np.float32)
@@ -393,14 +394,11 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
     m = "ip" if metric == 0 else "l2"
     note("mfma sweep seeds", mode, dtype, m, d)
     if mode.startswith("order-overflow"):
-        monkeypatch.setenv("SWANN_SWEEP_SYM_FCAP", "4")
-        monkeypatch.setenv("SWANN_SWEEP_REPAIR_MAX", "1000" if mode.endswith("16") else "0")
+        opt(sweep_sym_fcap=4, sweep_repair_max=1000 if mode.endswith("16") else 0)
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
-    monkeypatch.delenv("SWANN_SWEEP_SYM_FCAP", raising=False)
-    monkeypatch.delenv("SWANN_SWEEP_REPAIR_MAX", raising=False)
-    monkeypatch.setenv("SWANN_SWEEP_NOSEED", "1")
+    opt(sweep_sym_fcap=0, sweep_repair_max=4, sweep_noseed=1)
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
-    monkeypatch.delenv("SWANN_SWEEP_NOSEED")
+    opt(sweep_noseed=0)
     same_lists(f"mfma sweep seeds vs none {mode} {dtype} {m}", cand, cdist, c0.cpu().numpy(),
                d0.cpu().numpy(), 1e-6, 1e-6)
     assert torch.allclose(cdist, d0, rtol=1e-6, atol=1e-6)
@@ -416,13 +414,13 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(monkeypatch, metric, dtype,
 @pytest.mark.parametrize("sym", ["0", "1"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_mfma_sweep_with_duplicate_rows_matches_oracle(monkeypatch, metric, dtype, sym, d):
+def test_mfma_sweep_with_duplicate_rows_matches_oracle(opt, metric, dtype, sym, d):
     """A larger sweep (n = 12,000: 47 row panels, 47 column tiles, several
     compactions per row) with rows 0..999 duplicated at 6000..6999, so many
     rows hold exact ties, some of them at the C-th place: the lists must be
     the oracle's, and each duplicated row must find its twin -- one-sided
     and symmetric (47 panels, 9 band launches)."""
-    monkeypatch.setenv("SWANN_SWEEP_SYM", sym)
+    opt(sweep_sym=int(sym))
     n, C = 12000, 16
     X = gaussian(n, d, 421 + metric, metric == 0)
     if metric == 1:
@@ -616,18 +614,18 @@ def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
 @pytest.mark.parametrize("C", [48, 100])
 @pytest.mark.parametrize("dtype", ["f16", "f32", "f32-fp32gram"])
 @pytest.mark.parametrize("metric", [0, 1])
-def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
+def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, opt):
     """The prune's Gram on MFMA -- fp16 rows: exact products, fp32 sums
     (32x32x16 f16); fp32 rows: split fp16 planes (hi.hi + (hi.lo + lo.hi) /
-    2^11 on 32x32x16 f16), or with SWANN_PRUNE_F32=1 fp32 products and sums
+    2^11 on 32x32x16 f16), or with option prune_f32 fp32 products and sums
     (32x32x2 f32); nodes grouped by shared candidates -- keeps
-    the same rows as the fp32 SIMT Gram (SWANN_PRUNE_SIMT=1) and the oracle
+    the same rows as the fp32 SIMT Gram (option prune_simt) and the oracle
     (double dots) up to near-ties.  d = 80 leaves a ragged last K group for
     fp16; C = 48 fills two of the four 32-row blocks (three of the ten Gram
     tiles), C = 100 all four with a ragged last (every tile, every wave);
     per-node caps and protect ride along."""
     if dtype == "f32-fp32gram":
-        monkeypatch.setenv("SWANN_PRUNE_F32", "1")
+        opt(prune_f32=1)
     X = gaussian(3000, 80, 71 + metric, metric == 0)
     if metric == 1:
         X = X * 2.0 + 0.5
@@ -641,7 +639,7 @@ def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
     kw = dict(alpha=1.2, metric=m, deg_per_node=torch.from_numpy(dpn).cuda(),
               protect=torch.from_numpy(prot).cuda())
     g_mfma = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
-    monkeypatch.setenv("SWANN_PRUNE_SIMT", "1")
+    opt(prune_simt=1)
     g_simt = B.robust_prune(Xg, cand, cdist, 24, **kw).cpu().numpy()
     ora = O.robust_prune(X16.astype(np.float32), cand.cpu().numpy(), cdist.cpu().numpy(), 24,
                          1.2, metric, nthreads=8, deg_per_node=dpn, protect=prot)
@@ -654,7 +652,7 @@ def test_prune_mfma_gram_matches_simt_and_oracle(metric, dtype, C, monkeypatch):
     assert a == [] and b == []
 
 
-def test_many_branches_keep_recall_in_every_layout(monkeypatch):
+def test_many_branches_keep_recall_in_every_layout(opt):
     """128 claiming branches a query on a 100,000 x 512 low-rank corpus.  With
     1024 threads a branch one XCD holds only 32 branches at once; placing a
     query's 128 branches on one XCD made them run in rounds, the late ones
@@ -679,7 +677,7 @@ def test_many_branches_keep_recall_in_every_layout(monkeypatch):
     ix = swann.Index(X, G, metric="ip")
     rec = {}
     for blk in ("64", "256", "1024"):
-        monkeypatch.setenv("SWANN_SEARCH_BLOCK", blk)
+        opt(search_block=int(blk))
         ids = ix.search(Q, k=10, branches=128, queue=12, team=32)[0]
         rec[blk] = recall(ids, truth, 10)
     note("128 branches recall by layout", rec)

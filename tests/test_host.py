@@ -265,3 +265,29 @@ int main() {
     assert pairs > 200_000
     assert bad == 0
     assert unbalanced == 0
+
+
+def test_options_are_a_closed_documented_list():
+    """The library's code-path switches are options of the C ABI, each with
+    its documented default and values; unknown names and values are refused,
+    and the product reads no environment variable."""
+    from swann_amd import _lib
+    L = _lib.lib()
+    L.swann_reset_options()
+    want = {"search_block": 0, "prune_simt": 0, "prune_f32": 0, "sweep_sym": -1,
+            "sweep_waves": 16, "sweep_rowscale": 0, "sweep_regstage": 0, "sweep_sym_fcap": 0,
+            "sweep_noseed": 0, "sweep_order": 1, "sweep_repair_max": 4}
+    header = (ROOT / "include" / "swann_amd.h").read_text()
+    for name, default in want.items():
+        assert _lib.get_option(name) == default, name
+        assert f" *   {name} " in header, name
+    with _lib.options(search_block=256, sweep_sym=0):
+        assert _lib.get_option("search_block") == 256 and _lib.get_option("sweep_sym") == 0
+    assert _lib.get_option("search_block") == 0 and _lib.get_option("sweep_sym") == -1
+    with pytest.raises(_lib.SwannError, match="unknown option"):
+        _lib.set_option("no_such_option", 1)
+    with pytest.raises(_lib.SwannError, match="not one of its values"):
+        _lib.set_option("search_block", 128)
+    for src in (ROOT / "swann_amd" / "csrc").iterdir():
+        assert "getenv" not in src.read_text(), src.name
+    assert "os.environ" not in (ROOT / "swann_amd" / "_lib.py").read_text()
