@@ -157,6 +157,7 @@ def timed_build(X, cfg):
     cand, cdist = B.knn_candidates(Xg, cfg["cand"], metric=cfg["metric"])
     torch.cuda.synchronize()
     t.append(time.perf_counter())
+    tiles = int(_lib_tiles())
     G = B.robust_prune(Xg, cand, cdist, cfg["D"], alpha=1.2, metric=cfg["metric"])
     torch.cuda.synchronize()
     t.append(time.perf_counter())
@@ -165,8 +166,14 @@ def timed_build(X, cfg):
     t.append(time.perf_counter())
     del cand, cdist
     stages = dict(candidates=round(t[1] - t[0], 3), prune=round(t[2] - t[1], 3),
-                  reverse=round(t[3] - t[2], 3))
+                  reverse=round(t[3] - t[2], 3), sweep_tiles=tiles)
     return G, t[3] - t[0], stages
+
+
+def _lib_tiles():
+    """256 x 256 tiles the last sweep scored on MFMA (swann_sweep_tiles_scored)."""
+    from swann_amd import _lib
+    return _lib.lib().swann_sweep_tiles_scored()
 
 
 def mfma_probe(dev, seconds=0.4):
@@ -195,23 +202,23 @@ def mfma_probe(dev, seconds=0.4):
 
 
 def build_roofline(n, d, stages, measured=None):
-    """The candidate sweep against the dense fp16 MFMA peak: the exact sweep's
-    algorithmic 2 n^2 d FLOP (the full Gram, the reference's work) over the
-    candidate stage's time (sweep + list merges, + the exact re-rank for an
-    fp32 corpus).  The symmetric sweep scores each pair once for both of its
-    rows, so the MFMAs it executes are the upper triangle of 256 x 256 tiles,
-    about half: `flop_executed` and `executed_frac` report that rate."""
+    """The candidate sweep against the dense fp16 MFMA peak, on the MFMAs it
+    executes: the 256 x 256 tiles the library reports scoring
+    (swann_sweep_tiles_scored: the symmetric sweep's upper triangle, less
+    what the locality-ordered sweep proves empty on clustered rows) x
+    2 * 256 * 256 * d FLOP, over the candidate stage's time (sweep + list
+    merges + the exact re-rank of an fp32 corpus).  `reference_work` is the
+    reference's exact sweep, the full Gram's 2 n^2 d FLOP, over the same
+    time: the rate an unpruned, one-sided sweep would need to match it."""
     flop = 2.0 * n * n * d
-    nt = (n + 255) // 256
-    # the library sweeps symmetrically from 1,024 tiles of 256 rows on
-    # (sweep_mfma.hip:sweep_sym); below that, every tile of the Gram
-    executed = 2.0 * 256 * 256 * d * (nt * (nt + 1) / 2 if nt >= 1024 else nt * nt)
+    executed = 2.0 * 256 * 256 * d * stages["sweep_tiles"]
     t = stages["candidates"]
-    ach = flop / t
+    ach = executed / t
     out = {"bound": "mfma", "achieved": round(ach / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
            "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK, 4), "kernel": "sweep_dma_kernel",
-           "flop": flop, "stage_s": t, "flop_executed": executed,
-           "executed_frac": round(executed / t / MFMA_F16_PEAK, 4)}
+           "flop_executed": executed, "tiles_scored": stages["sweep_tiles"], "stage_s": t,
+           "reference_work": {"flop": flop, "rate_tflops": round(flop / t / 1e12, 1),
+                              "frac_of_peak": round(flop / t / MFMA_F16_PEAK, 4)}}
     if measured:
         # against the rate the chip sustained in this run (mfma_probe)
         out["measured_peak"] = round(measured / 1e12, 1)

@@ -251,6 +251,13 @@ int64_t swann_sweep_workspace_size(int64_t n, int dim, int x_dtype, int C);
 int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric, int C,
                       int32_t* cand, float* cdist, void* workspace, void* stream);
 
+/* Tiles of 256 x 256 rows the last swann_build_sweep on this thread scored
+ * on MFMA (the symmetric sweep's bands, less the tiles the locality-ordered
+ * sweep proved empty, plus any repair); -1 before any sweep.  No counterpart
+ * in the reference (its sweep scores every pair): a diagnostic for the
+ * executed-FLOP figure of the bench (2 * 256 * 256 * dim FLOP a tile). */
+int64_t swann_sweep_tiles_scored(void);
+
 /* Prune (build.py:46-91): keep candidate i of node u unless an already kept
  * w satisfies alpha * d(w, i) <= d(u, i); rows of `deg` ids, -1 padded.
  * C <= 128, deg <= 128.  deg_per_node [n] (or NULL) caps node u at

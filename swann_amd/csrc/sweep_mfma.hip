@@ -35,6 +35,13 @@ constexpr int kPad = 8;                       // fp16 elements of padding per LD
 constexpr int kLdsRow = kBK + kPad;           // 40 halves = 80 bytes
 constexpr int kBM2 = 256, kBN2 = 256, kT2 = 512;   // workgroup tile rows, columns; threads
 
+// Widest band of the symmetric sweep.  Wider bands mean fewer launches and
+// merges but staler column thresholds (more foreign appends); with the
+// balanced panel order (sym_panel) the candidate stage at n = 1M took 1.506 s
+// (1M x 1024 fp32, l2) and 1.959 s (1M x 1536 fp16, ip) with bands of 256,
+// 1.452 s and 1.901 s with 512, and within 1% of that with 640 to 1,024.
+constexpr int64_t kBandMax = 512;
+
 __device__ __forceinline__ uint32_t fkey(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -193,6 +200,10 @@ struct MfmaSweepArgs {
     // second list overflowed): workgroup g takes panel plist[g / G]
     const int* plist;
     int npl;
+    // the pruned ordered sweep: workgroup (panel) I scores only the column
+    // tiles tlist[I * kBandMax + k], k < tcnt[I] (ascending, inside its band)
+    const int* tlist;
+    const int* tcnt;
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -846,7 +857,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         ct0 = lid + (int)a.b0;
         ct1 = lid + a.b1 < nct ? lid + (int)a.b1 : nct;
     }
-    const int nsteps = (ct1 - ct0) * nk;
+    // with a tile list (the pruned ordered sweep) the column tiles are a
+    // subset of [ct0, ct1), in order; lid is the panel in a symmetric launch
+    const int* tls = (a.sym && a.tlist) ? a.tlist + (int64_t)lid * kBandMax : nullptr;
+    const int ntl = tls ? a.tcnt[lid] : ct1 - ct0;
+    const int nsteps = ntl * nk;
     const _Float16* X = a.hi;
 
     auto issue = [&](int t, int kt, int cb) {
@@ -883,10 +898,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
 #pragma unroll
     for (int j = 0; j < BJ; ++j) bro[j] = (wn * CW + j * 32 + (lane & 31)) * kRowBytes;
 
-    int kt_c = 0, kt_f = 0;
-    int cb_c = ct0 * kBN2, cb_f = ct0 * kBN2;
-    auto adv = [&](int& kt, int& cb) {
-        if (++kt == nk) { kt = 0; cb += kBN2; }
+    // wave-uniform (the list entry is the same for every lane): the direct
+    // loads take the tile's base address in scalar registers
+    auto tile_at = [&](int k) { return tls ? __builtin_amdgcn_readfirstlane(tls[k]) : ct0 + k; };
+    int kt_c = 0, kt_f = 0, ki_c = 0, ki_f = 0;
+    int cb_c = ntl > 0 ? tile_at(0) * kBN2 : 0, cb_f = cb_c;
+    auto adv = [&](int& kt, int& ki, int& cb) {
+        if (++kt == nk) {
+            kt = 0;
+            if (++ki < ntl) cb = tile_at(ki) * kBN2;
+        }
     };
     f32x16 acc[BI][BJ];
     // the foreign queue: staged when a tile has at least three stages, so
@@ -897,12 +918,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     int cb_prev = 0;                 // column base of the tile whose entries are queued
     int tpar = 0;                    // parity of the current column tile (its need flag)
     issue(0, kt_f, cb_f);
-    adv(kt_f, cb_f);
+    adv(kt_f, ki_f, cb_f);
 
     for (int t = 0; t < nsteps; ++t) {
         const int kt = kt_c;
         const int cbt = cb_c;
-        adv(kt_c, cb_c);
+        adv(kt_c, ki_c, cb_c);
         const int buf = t & 1;
         // column norms/scales of a finishing tile, issued before the next
         // stage's loads so the epilogue's wait does not include them
@@ -1000,7 +1021,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
             }
         }
         issue(t + 1, kt_f, cb_f);
-        adv(kt_f, cb_f);
+        adv(kt_f, ki_f, cb_f);
         const unsigned char* pA = sA[buf];
         const unsigned char* pB = sB[buf];
         f16x8 fa[2][BI], fb[2][BJ];
@@ -1221,6 +1242,162 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
         gthr[r] = cnt >= C ? funkey(T) : seed ? seed[r] : INFINITY;
         bcnt[r * 2] = w;
         bcnt[r * 2 + 1] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pruning the locality-ordered sweep's tiles.  A tile (I, J) can append a pair
+// (r in panel I, c in panel J) only if the screened distance d^(r, c) falls
+// below r's threshold (own list) or c's (foreign list); thresholds only fall
+// during a launch, so the panels' largest thresholds when it starts bound
+// both tests.  Each panel of the ordered plane gets a centre c_I (the mean of
+// its rows as the screen sees them, v = scale * fp16 row), a radius R_I
+// (largest |v - c_I|), its largest |v| (N_I) and the largest gap between a
+// row's fp32 norm, which the screen's l2 formula takes, and |v|^2 (D_I).
+// Then for every pair of the panels:
+//   l2: d^ >= (|c_I - c_J| - R_I - R_J)^2 - D_I - D_J - 2 g N_I N_J - rounding
+//   ip: d^ >= 1 - (c_I.c_J + R_I |c_J| + R_J |c_I| + R_I R_J) - g N_I N_J - rounding
+// (the triangle inequality; Cauchy-Schwarz on the rows' offsets from the
+// centres; g = (dim + 64) 2^-23 covers the screen's fp32 accumulation and
+// scale products), with the centre terms in double.  A tile whose bound
+// exceeds both panels' largest thresholds is left out of the launch: no pair
+// in it could have been appended, so the lists are the unpruned sweep's.
+// On clustered rows in locality order most tiles pair different clusters.
+
+// One workgroup per panel: pst[4 I ..] = R_I, N_I, D_I, |c_I|, each rounded up.
+__global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ hp,
+                                                   const float* __restrict__ scp,
+                                                   const float* __restrict__ xnp, int64_t n,
+                                                   int dim, int scaled, float* __restrict__ cen,
+                                                   float* __restrict__ pst) {
+    const int I = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t r0 = (int64_t)I * kBM2;
+    const int rows = (int)(n - r0 < kBM2 ? n - r0 : kBM2);
+    float* c = cen + (int64_t)I * dim;
+    for (int t = tid; t < dim; t += 256) {
+        float sum = 0.f;
+        for (int r = 0; r < rows; ++r)
+            sum += (scaled ? scp[r0 + r] : 1.f) * (float)hp[(r0 + r) * dim + t];
+        c[t] = sum / (float)rows;
+    }
+    __syncthreads();
+    double rad2 = 0.0, nrm2 = 0.0, dev = 0.0, cn2 = 0.0;
+    for (int t = lane; t < dim && w == 0; t += 64) cn2 += (double)c[t] * (double)c[t];
+    for (int r = w; r < rows; r += 4) {
+        const float sc = scaled ? scp[r0 + r] : 1.f;
+        double d2 = 0.0, v2 = 0.0;
+        for (int t = lane; t < dim; t += 64) {
+            const double v = (double)(sc * (float)hp[(r0 + r) * dim + t]);
+            const double dv = v - (double)c[t];
+            d2 += dv * dv;
+            v2 += v * v;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            d2 += __shfl_xor(d2, off, 64);
+            v2 += __shfl_xor(v2, off, 64);
+        }
+        rad2 = d2 > rad2 ? d2 : rad2;
+        nrm2 = v2 > nrm2 ? v2 : nrm2;
+        const double g = fabs((double)xnp[r0 + r] - v2);
+        dev = g > dev ? g : dev;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cn2 += __shfl_xor(cn2, off, 64);
+    __shared__ double red[4][3];
+    if (lane == 0) { red[w][0] = rad2; red[w][1] = nrm2; red[w][2] = dev; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int q = 1; q < 4; ++q) {
+            rad2 = red[q][0] > rad2 ? red[q][0] : rad2;
+            nrm2 = red[q][1] > nrm2 ? red[q][1] : nrm2;
+            dev = red[q][2] > dev ? red[q][2] : dev;
+        }
+        // double sums of dim terms are exact to ~1e-13 relative: 1e-6 up
+        // covers them and the rounding to float
+        const double up = 1.0 + 1e-6;
+        pst[4 * I + 0] = (float)(sqrt(rad2) * up);
+        pst[4 * I + 1] = (float)(sqrt(nrm2) * up);
+        pst[4 * I + 2] = (float)(dev * up + 1e-30);
+        pst[4 * I + 3] = (float)(sqrt(cn2) * up);
+    }
+}
+
+// The largest threshold of each panel's rows as the last merge published
+// them (+inf for a row with fewer than C so far, or a NaN).
+__global__ __launch_bounds__(256) void panel_thr(const float* __restrict__ gthr, int64_t n,
+                                                 float* __restrict__ pthr) {
+    const int64_t r = (int64_t)blockIdx.x * kBM2 + threadIdx.x;
+    float v = r < n ? gthr[r] : -INFINITY;
+    if (v != v) v = INFINITY;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) pthr[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// One workgroup per panel I of a band launch [b0, b1): the column tiles J it
+// must still score, ascending, into tlist[I * kBandMax ..], their count into
+// tcnt[I], and the launch's total into *tsum.  16 lanes a tile.
+__global__ __launch_bounds__(256) void tile_keep(const float* __restrict__ cen,
+                                                 const float* __restrict__ pst,
+                                                 const float* __restrict__ pthr, int ntile,
+                                                 int dim, int metric, int b0, int b1,
+                                                 int* __restrict__ tlist, int* __restrict__ tcnt,
+                                                 unsigned long long* __restrict__ tsum) {
+    const int I = blockIdx.x, tid = threadIdx.x, team = tid >> 4, tl = tid & 15;
+    const int j0 = I + b0, j1 = I + b1 < ntile ? I + b1 : ntile;
+    const int nj = j1 - j0;
+    __shared__ unsigned char keep[kBandMax];
+    const float* ci = cen + (int64_t)I * dim;
+    const double RI = pst[4 * I], NI = pst[4 * I + 1], DI = pst[4 * I + 2], CI = pst[4 * I + 3];
+    const double g = ((double)dim + 64.0) * 0x1p-23;
+    for (int j = team; j < nj; j += 16) {
+        const int J = j0 + j;
+        const float* cj = cen + (int64_t)J * dim;
+        double d2 = 0.0, dot = 0.0;
+        for (int t = tl; t < dim; t += 16) {
+            const double x = ci[t], y = cj[t];
+            d2 += (x - y) * (x - y);
+            dot += x * y;
+        }
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+            d2 += __shfl_xor(d2, off, 16);
+            dot += __shfl_xor(dot, off, 16);
+        }
+        if (tl == 0) {
+            const double RJ = pst[4 * J], NJ = pst[4 * J + 1], DJ = pst[4 * J + 2],
+                         CJ = pst[4 * J + 3];
+            double lb;
+            if (metric == SWANN_METRIC_L2) {
+                const double gap = sqrt(d2) * (1.0 - 1e-9) - RI - RJ;
+                lb = (gap > 0.0 ? gap * gap : 0.0) - DI - DJ - 2.0 * g * NI * NJ -
+                     0x1p-21 * 1.1 * (NI + NJ) * (NI + NJ);
+            } else {
+                lb = 1.0 - (dot + 1e-9 * CI * CJ + RI * CJ + RJ * CI + RI * RJ) - g * NI * NJ -
+                     0x1p-22 * (1.0 + NI * NJ);
+            }
+            const double th = fmax((double)pthr[I], (double)pthr[J]);
+            keep[j] = !(lb > th);                // a NaN keeps the tile
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        int base = 0;
+        for (int jc = 0; jc < nj; jc += 64) {
+            const int j = jc + tid;
+            const bool k = j < nj && keep[j];
+            const uint64_t m = __ballot(k);
+            if (k) tlist[(int64_t)I * kBandMax + base + __popcll(m & ((1ull << tid) - 1ull))] = j0 + j;
+            base += __popcll(m);
+        }
+        if (tid == 0) {
+            tcnt[I] = base;
+            atomicAdd(tsum, (unsigned long long)base);
+        }
     }
 }
 
@@ -1543,12 +1720,15 @@ __global__ __launch_bounds__(256) void repair_merge(const float* __restrict__ rk
 
 inline int64_t al256(int64_t b) { return ((b + 255) / 256) * 256; }
 
+inline int64_t prune_bytes(int64_t n, int dim);
+
 inline int64_t seed_bytes(int64_t n, int dim) {
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     return al256(n * kSketch * 4) + al256(n * 4) * 7 + al256(kMaxPivots * 4) +
            al256(n * (int64_t)dim * 2) + al256(ntile * 4) + 256 +
            al256((int64_t)kMaxPivots * kSketch * 4) + al256((kMaxPivots + 1) * 4) +
-           al256((int64_t)kMaxPivots * kMaxPivots * 4) + al256(kMaxPivots * 4);
+           al256((int64_t)kMaxPivots * kMaxPivots * 4) + al256(kMaxPivots * 4) +
+           prune_bytes(n, dim);
 }
 
 // The few-panel repair's scratch: lists of one panel in kRepairSplits ranges.
@@ -1556,12 +1736,26 @@ inline int64_t repair_bytes(int cap) {
     return al256((int64_t)kBM2 * kRepairSplits * cap * 4) * 2 + al256(kBM2 * kRepairSplits * 4);
 }
 
-// Widest band of the symmetric sweep.  Wider bands mean fewer launches and
-// merges but staler column thresholds (more foreign appends); with the
-// balanced panel order (sym_panel) the candidate stage at n = 1M took 1.506 s
-// (1M x 1024 fp32, l2) and 1.959 s (1M x 1536 fp16, ip) with bands of 256,
-// 1.452 s and 1.901 s with 512, and within 1% of that with 640 to 1,024.
-constexpr int64_t kBandMax = 512;
+
+// The pruned ordered sweep's scratch: panel centres and statistics, the
+// panels' largest thresholds, the launch's tile lists and counts, a counter.
+inline int64_t prune_bytes(int64_t n, int dim) {
+    const int64_t ntile = (n + kBM2 - 1) / kBM2;
+    return al256(ntile * (int64_t)dim * 4) + al256(ntile * 16) + al256(ntile * 4) +
+           al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256;
+}
+
+// 256 x 256 tiles the last sweep on this thread scored (the bands' tiles, less
+// those the pruned ordered sweep proved empty, plus any repair), -1 before.
+thread_local int64_t g_tiles_scored = -1;
+
+// Tiles of one band launch [b0, b1) over ntile panels: panel I has
+// min(b1, ntile - I) - b0 of them while that is positive.
+inline int64_t band_tiles(int64_t ntile, int64_t b0, int64_t b1) {
+    const int64_t M = ntile - b0, B = b1 - b0;
+    if (M <= 0) return 0;
+    return M <= B ? M * (M + 1) / 2 : B * (B + 1) / 2 + (M - B) * B;
+}
 
 // Whether the direct-load sweep runs symmetric: by default when there are at
 // least 1,024 row panels (n > 261,888), where every band launch still fills
@@ -1588,6 +1782,8 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                    int splits, float* bkey, int32_t* bid, int32_t* bcnt, char* extra,
                    hipStream_t st, int* used, const int32_t** perm_out) {
     *perm_out = nullptr;
+    g_tiles_scored = 0;
+    const int64_t ntile_all = (n + kBM2 - 1) / kBM2;
     float* xn = (float*)extra; extra += al256(n * 4);
     float* scale = (float*)extra; extra += al256(n * 4);
     const _Float16* hi;
@@ -1650,14 +1846,36 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 const int f = option(kOptSweepSymFcap);
                 if (f >= 1 && f < cap) s.fcap = f;
             }
-            // the launches of bands [b0, bend), each followed by a merge
+            // the pruned ordered sweep's panel data (set when it runs)
+            const float* pcen = nullptr;
+            const float* ppst = nullptr;
+            float* pthr = nullptr;
+            int* tlist = nullptr;
+            int* tcnt = nullptr;
+            unsigned long long* tsum = nullptr;
+            int64_t host_tiles = 0;      // tiles of the launches not pruned
+            // the launches of bands [b0, bend), each followed by a merge;
+            // with `prune`, each launch scores only the tiles tile_keep keeps
             auto bands = [&](MfmaSweepArgs& sa, int64_t bstart, int64_t bend, const float* seed,
-                             int* flag) -> int {
+                             int* flag, bool prune) -> int {
                 for (int64_t b0 = bstart; b0 < bend;) {
                     const int64_t B = b0 == 0 ? 1 : (b0 < kBandMax ? b0 : kBandMax);
                     sa.b0 = b0;
                     sa.b1 = b0 + B < bend ? b0 + B : bend;
                     const unsigned grid = (unsigned)(ntile - b0);
+                    if (prune) {
+                        hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
+                                           (const float*)gthr, n, pthr);
+                        hipLaunchKernelGGL(tile_keep, dim3(grid), dim3(256), 0, st, pcen, ppst,
+                                           (const float*)pthr, (int)ntile, dim, metric,
+                                           (int)sa.b0, (int)sa.b1, tlist, tcnt, tsum);
+                        sa.tlist = tlist;
+                        sa.tcnt = tcnt;
+                    } else {
+                        sa.tlist = nullptr;
+                        sa.tcnt = nullptr;
+                        host_tiles += band_tiles(ntile, sa.b0, sa.b1);
+                    }
                     if (scaled) {
                         if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(grid), dim3(1024), 0, st, sa);
                         else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(grid), dim3(1024), 0, st, sa);
@@ -1809,13 +2027,26 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 pre.scale = scp;
                 int rc = launch_status("sweep (mfma, seed order)");
                 if (rc) return rc;
-                rc = bands(pre, 0, kSeedBand, nullptr, in_order ? flag : nullptr);
+                rc = bands(pre, 0, kSeedBand, nullptr, in_order ? flag : nullptr, false);
                 if (rc) return rc;
                 if (in_order) {
                     // the main sweep in the locality order too: the pre-pass
                     // was its first bands, so it goes on from there, its lists
-                    // and thresholds as the last merge left them (ordered ids)
-                    rc = bands(pre, kSeedBand, ntile, nullptr, flag);
+                    // and thresholds as the last merge left them (ordered ids),
+                    // leaving out the tiles the panels' bounds show empty
+                    float* cen = (float*)extra; extra += al256(ntile * (int64_t)dim * 4);
+                    float* pst = (float*)extra; extra += al256(ntile * 16);
+                    pthr = (float*)extra; extra += al256(ntile * 4);
+                    tlist = (int*)extra; extra += al256(ntile * kBandMax * 4);
+                    tcnt = (int*)extra; extra += al256(ntile * 4);
+                    tsum = (unsigned long long*)extra; extra += 256;
+                    hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)tsum, 2);
+                    hipLaunchKernelGGL(panel_stats, dim3((unsigned)ntile), dim3(256), 0, st,
+                                       (const _Float16*)hp, (const float*)scp, (const float*)xnp,
+                                       n, dim, scaled, cen, pst);
+                    pcen = cen;
+                    ppst = pst;
+                    rc = bands(pre, kSeedBand, ntile, nullptr, flag, true);
                     if (rc) return rc;
                     s = pre;
                     seed = nullptr;
@@ -1831,7 +2062,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
                                (const float*)seed);
             {
-                const int rc = bands(s, 0, ntile, seed, flag);
+                const int rc = bands(s, 0, ntile, seed, flag, false);
                 if (rc) return rc;
             }
         swept:
@@ -1839,12 +2070,16 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             // one-sided way (one small read-back; the build is not on the
             // search path)
             int dropped = 0;
+            unsigned long long pruned_kept = 0;
             if (hipMemcpyAsync(&dropped, ovf, sizeof(int), hipMemcpyDeviceToHost, st) !=
                     hipSuccess ||
+                (tsum && hipMemcpyAsync(&pruned_kept, tsum, sizeof(pruned_kept),
+                                        hipMemcpyDeviceToHost, st) != hipSuccess) ||
                 hipStreamSynchronize(st) != hipSuccess) {
                 set_error("sweep (mfma, symmetric): reading the overflow count failed");
                 return SWANN_E_LAUNCH;
             }
+            g_tiles_scored += host_tiles + (int64_t)pruned_kept;
             if (dropped == 0) {
                 *used = 2;
                 *perm_out = ordered;
@@ -1876,6 +2111,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         set_error("sweep (mfma, symmetric): reading the repair panels failed");
                         return SWANN_E_LAUNCH;
                     }
+                    g_tiles_scored += (int64_t)np * ntile;
                     for (int i = 0; i < np; ++i) {
                         SWANN_REQUIRE(ph[i] >= 0 && ph[i] < ntile, "sweep: repair panel out of range");
                         // the one-sided sweep of panel ph[i] into the scratch:
@@ -1910,6 +2146,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     *perm_out = ordered;
                     return SWANN_OK;
                 }
+                g_tiles_scored += (int64_t)np * ntile;
                 MfmaSweepArgs rep = s;
                 rep.sym = 0;
                 rep.splits = 2;
@@ -1932,6 +2169,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         }
         a.splits = splits;
         *used = splits;
+        g_tiles_scored += ntile_all * ntile_all;          // every tile, one-sided
         const unsigned grid = (unsigned)((n + kBM2 - 1) / kBM2 * splits);
         if (sweep_waves() == 16) {
             if (scaled) {
@@ -1950,6 +2188,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
         }
         return launch_status("sweep (mfma, direct loads)");
     }
+    g_tiles_scored += ntile_all * ntile_all;
     if (scaled) {
         if (ip) hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_IP, 1>), dim3(grid), dim3(kT2), 0, st, a);
         else hipLaunchKernelGGL((sweep_mfma256_kernel<SWANN_METRIC_L2, 1>), dim3(grid), dim3(kT2), 0, st, a);
@@ -1997,3 +2236,5 @@ int sweep_mfma_cap(int C) {
 }
 
 }  // namespace swann
+
+extern "C" int64_t swann_sweep_tiles_scored(void) { return swann::g_tiles_scored; }
