@@ -1250,11 +1250,11 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 // (r in panel I, c in panel J) only if the screened distance d^(r, c) falls
 // below r's threshold (own list) or c's (foreign list); thresholds only fall
 // during a launch, so the panels' largest thresholds when it starts bound
-// both tests.  Each panel of the ordered plane gets a centre c_I (the mean of
-// its rows as the screen sees them, v = scale * fp16 row), a radius R_I
-// (largest |v - c_I|), its largest |v| (N_I) and the largest gap between a
-// row's fp32 norm, which the screen's l2 formula takes, and |v|^2 (D_I).
-// Then for every pair of the panels:
+// both tests.  Each panel of the ordered plane, per run of rows of one pivot
+// (panel_stats), gets a centre c_I (the mean of the rows as the screen sees
+// them, v = scale * fp16 row), a radius R_I (largest |v - c_I|), its largest
+// |v| (N_I) and the largest gap between a row's fp32 norm, which the screen's
+// l2 formula takes, and |v|^2 (D_I).  Then for every pair of runs:
 //   l2: d^ >= (|c_I - c_J| - R_I - R_J)^2 - D_I - D_J - 2 g N_I N_J - rounding
 //   ip: d^ >= 1 - (c_I.c_J + R_I |c_J| + R_J |c_I| + R_I R_J) - g N_I N_J - rounding
 // (the triangle inequality; Cauchy-Schwarz on the rows' offsets from the
@@ -1264,26 +1264,74 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 // in it could have been appended, so the lists are the unpruned sweep's.
 // On clustered rows in locality order most tiles pair different clusters.
 
-// One workgroup per panel: pst[4 I ..] = R_I, N_I, D_I, |c_I|, each rounded up.
+// A panel's rows come in runs of one pivot each (the order groups rows by
+// pivot); its statistics are kept per run, up to kSegs runs (a panel with
+// more folds the rest into its last), so that a panel straddling two
+// clusters is two tight groups, not one wide one.  One workgroup per panel:
+// nseg[I] runs; for run a, centre cen[(I kSegs + a) dim ..] and
+// pst[4 (I kSegs + a) ..] = R, N, D, |c|, each rounded up.
+constexpr int kSegs = 4;
+
 __global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ hp,
                                                    const float* __restrict__ scp,
-                                                   const float* __restrict__ xnp, int64_t n,
+                                                   const float* __restrict__ xnp,
+                                                   const int* __restrict__ lab,
+                                                   const int* __restrict__ perm, int64_t n,
                                                    int dim, int scaled, float* __restrict__ cen,
-                                                   float* __restrict__ pst) {
+                                                   float* __restrict__ pst,
+                                                   int* __restrict__ nseg) {
     const int I = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t r0 = (int64_t)I * kBM2;
     const int rows = (int)(n - r0 < kBM2 ? n - r0 : kBM2);
-    float* c = cen + (int64_t)I * dim;
-    for (int t = tid; t < dim; t += 256) {
-        float sum = 0.f;
-        for (int r = 0; r < rows; ++r)
-            sum += (scaled ? scp[r0 + r] : 1.f) * (float)hp[(r0 + r) * dim + t];
-        c[t] = sum / (float)rows;
+    // run of each row: the number of label changes before it, capped
+    __shared__ int lb[kBM2];
+    __shared__ unsigned char seg[kBM2];
+    __shared__ int cnt[kSegs];
+    __shared__ int s_ns;
+    if (tid < rows) lb[tid] = lab[perm[r0 + tid]];
+    if (tid < kSegs) cnt[tid] = 0;
+    __syncthreads();
+    if (tid == 0) {
+        int sgi = 0;
+        for (int r = 0; r < rows; ++r) {
+            if (r > 0 && lb[r] != lb[r - 1] && sgi < kSegs - 1) ++sgi;
+            seg[r] = (unsigned char)sgi;
+            cnt[sgi] += 1;
+        }
+        s_ns = sgi + 1;
+        nseg[I] = sgi + 1;
     }
     __syncthreads();
-    double rad2 = 0.0, nrm2 = 0.0, dev = 0.0, cn2 = 0.0;
-    for (int t = lane; t < dim && w == 0; t += 64) cn2 += (double)c[t] * (double)c[t];
+    const int ns = s_ns;
+    for (int t = tid; t < dim; t += 256) {
+        float sum[kSegs];
+#pragma unroll
+        for (int q = 0; q < kSegs; ++q) sum[q] = 0.f;
+        for (int r = 0; r < rows; ++r) {
+            const float v = (scaled ? scp[r0 + r] : 1.f) * (float)hp[(r0 + r) * dim + t];
+#pragma unroll
+            for (int q = 0; q < kSegs; ++q) sum[q] += seg[r] == q ? v : 0.f;
+        }
+        for (int q = 0; q < ns; ++q)
+            cen[((int64_t)I * kSegs + q) * dim + t] = sum[q] / (float)cnt[q];
+    }
+    __syncthreads();
+    double rad2[kSegs], nrm2[kSegs], dev[kSegs], cn2[kSegs];
+#pragma unroll
+    for (int q = 0; q < kSegs; ++q) { rad2[q] = 0.0; nrm2[q] = 0.0; dev[q] = 0.0; cn2[q] = 0.0; }
+    if (w == 0) {
+        for (int q = 0; q < ns; ++q) {
+            const float* c = cen + ((int64_t)I * kSegs + q) * dim;
+            double acc = 0.0;
+            for (int t = lane; t < dim; t += 64) acc += (double)c[t] * (double)c[t];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+            cn2[q] = acc;
+        }
+    }
     for (int r = w; r < rows; r += 4) {
+        const int q = seg[r];
+        const float* c = cen + ((int64_t)I * kSegs + q) * dim;
         const float sc = scaled ? scp[r0 + r] : 1.f;
         double d2 = 0.0, v2 = 0.0;
         for (int t = lane; t < dim; t += 64) {
@@ -1297,30 +1345,41 @@ __global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ 
             d2 += __shfl_xor(d2, off, 64);
             v2 += __shfl_xor(v2, off, 64);
         }
-        rad2 = d2 > rad2 ? d2 : rad2;
-        nrm2 = v2 > nrm2 ? v2 : nrm2;
         const double g = fabs((double)xnp[r0 + r] - v2);
-        dev = g > dev ? g : dev;
-    }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) cn2 += __shfl_xor(cn2, off, 64);
-    __shared__ double red[4][3];
-    if (lane == 0) { red[w][0] = rad2; red[w][1] = nrm2; red[w][2] = dev; }
+        for (int s2 = 0; s2 < kSegs; ++s2)
+            if (s2 == q) {
+                rad2[s2] = d2 > rad2[s2] ? d2 : rad2[s2];
+                nrm2[s2] = v2 > nrm2[s2] ? v2 : nrm2[s2];
+                dev[s2] = g > dev[s2] ? g : dev[s2];
+            }
+    }
+    __shared__ double red[4][kSegs][3];
+    if (lane == 0)
+#pragma unroll
+        for (int q = 0; q < kSegs; ++q) { red[w][q][0] = rad2[q]; red[w][q][1] = nrm2[q]; red[w][q][2] = dev[q]; }
     __syncthreads();
-    if (tid == 0) {
-        for (int q = 1; q < 4; ++q) {
-            rad2 = red[q][0] > rad2 ? red[q][0] : rad2;
-            nrm2 = red[q][1] > nrm2 ? red[q][1] : nrm2;
-            dev = red[q][2] > dev ? red[q][2] : dev;
+    if (tid < ns) {
+        const int q = tid;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0;
+        for (int ww = 0; ww < 4; ++ww) {
+            a0 = red[ww][q][0] > a0 ? red[ww][q][0] : a0;
+            a1 = red[ww][q][1] > a1 ? red[ww][q][1] : a1;
+            a2 = red[ww][q][2] > a2 ? red[ww][q][2] : a2;
         }
         // double sums of dim terms are exact to ~1e-13 relative: 1e-6 up
         // covers them and the rounding to float
         const double up = 1.0 + 1e-6;
-        pst[4 * I + 0] = (float)(sqrt(rad2) * up);
-        pst[4 * I + 1] = (float)(sqrt(nrm2) * up);
-        pst[4 * I + 2] = (float)(dev * up + 1e-30);
-        pst[4 * I + 3] = (float)(sqrt(cn2) * up);
+        float* o = pst + 4 * ((int64_t)I * kSegs + q);
+        o[0] = (float)(sqrt(a0) * up);
+        o[1] = (float)(sqrt(a1) * up);
+        o[2] = (float)(a2 * up + 1e-30);
+        o[3] = 0.f;
     }
+    __syncthreads();
+    if (w == 0 && lane < ns)
+        for (int q = 0; q < ns; ++q)
+            if (lane == q) pst[4 * ((int64_t)I * kSegs + q) + 3] = (float)(sqrt(cn2[q]) * (1.0 + 1e-6));
 }
 
 // The largest threshold of each panel's rows as the last merge published
@@ -1340,9 +1399,12 @@ __global__ __launch_bounds__(256) void panel_thr(const float* __restrict__ gthr,
 
 // One workgroup per panel I of a band launch [b0, b1): the column tiles J it
 // must still score, ascending, into tlist[I * kBandMax ..], their count into
-// tcnt[I], and the launch's total into *tsum.  16 lanes a tile.
+// tcnt[I], and the launch's total into *tsum.  16 lanes a tile; a tile is
+// kept as soon as one pair of runs (one of I's, one of J's) may hold a pair
+// of rows within the thresholds.
 __global__ __launch_bounds__(256) void tile_keep(const float* __restrict__ cen,
                                                  const float* __restrict__ pst,
+                                                 const int* __restrict__ nseg,
                                                  const float* __restrict__ pthr, int ntile,
                                                  int dim, int metric, int b0, int b1,
                                                  int* __restrict__ tlist, int* __restrict__ tcnt,
@@ -1351,26 +1413,32 @@ __global__ __launch_bounds__(256) void tile_keep(const float* __restrict__ cen,
     const int j0 = I + b0, j1 = I + b1 < ntile ? I + b1 : ntile;
     const int nj = j1 - j0;
     __shared__ unsigned char keep[kBandMax];
-    const float* ci = cen + (int64_t)I * dim;
-    const double RI = pst[4 * I], NI = pst[4 * I + 1], DI = pst[4 * I + 2], CI = pst[4 * I + 3];
+    const int nsI = nseg[I];
     const double g = ((double)dim + 64.0) * 0x1p-23;
     for (int j = team; j < nj; j += 16) {
         const int J = j0 + j;
-        const float* cj = cen + (int64_t)J * dim;
-        double d2 = 0.0, dot = 0.0;
-        for (int t = tl; t < dim; t += 16) {
-            const double x = ci[t], y = cj[t];
-            d2 += (x - y) * (x - y);
-            dot += x * y;
-        }
+        const int nsJ = nseg[J];
+        const double th = fmax((double)pthr[I], (double)pthr[J]);
+        bool k = false;
+        for (int pa = 0; pa < nsI * nsJ && !k; ++pa) {
+            const int ia = I * kSegs + pa / nsJ, jb = J * kSegs + pa % nsJ;
+            const float* ci = cen + (int64_t)ia * dim;
+            const float* cj = cen + (int64_t)jb * dim;
+            double d2 = 0.0, dot = 0.0;
+            for (int t = tl; t < dim; t += 16) {
+                const double x = ci[t], y = cj[t];
+                d2 += (x - y) * (x - y);
+                dot += x * y;
+            }
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1) {
-            d2 += __shfl_xor(d2, off, 16);
-            dot += __shfl_xor(dot, off, 16);
-        }
-        if (tl == 0) {
-            const double RJ = pst[4 * J], NJ = pst[4 * J + 1], DJ = pst[4 * J + 2],
-                         CJ = pst[4 * J + 3];
+            for (int off = 8; off > 0; off >>= 1) {
+                d2 += __shfl_xor(d2, off, 16);
+                dot += __shfl_xor(dot, off, 16);
+            }
+            const double RI = pst[4 * ia], NI = pst[4 * ia + 1], DI = pst[4 * ia + 2],
+                         CI = pst[4 * ia + 3];
+            const double RJ = pst[4 * jb], NJ = pst[4 * jb + 1], DJ = pst[4 * jb + 2],
+                         CJ = pst[4 * jb + 3];
             double lb;
             if (metric == SWANN_METRIC_L2) {
                 const double gap = sqrt(d2) * (1.0 - 1e-9) - RI - RJ;
@@ -1380,9 +1448,9 @@ __global__ __launch_bounds__(256) void tile_keep(const float* __restrict__ cen,
                 lb = 1.0 - (dot + 1e-9 * CI * CJ + RI * CJ + RJ * CI + RI * RJ) - g * NI * NJ -
                      0x1p-22 * (1.0 + NI * NJ);
             }
-            const double th = fmax((double)pthr[I], (double)pthr[J]);
-            keep[j] = !(lb > th);                // a NaN keeps the tile
+            k = !(lb > th);                      // a NaN keeps the tile
         }
+        if (tl == 0) keep[j] = k;
     }
     __syncthreads();
     if (tid < 64) {
@@ -1741,8 +1809,8 @@ inline int64_t repair_bytes(int cap) {
 // panels' largest thresholds, the launch's tile lists and counts, a counter.
 inline int64_t prune_bytes(int64_t n, int dim) {
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
-    return al256(ntile * (int64_t)dim * 4) + al256(ntile * 16) + al256(ntile * 4) +
-           al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256;
+    return al256(ntile * kSegs * (int64_t)dim * 4) + al256(ntile * kSegs * 16) +
+           al256(ntile * 4) * 2 + al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256;
 }
 
 // 256 x 256 tiles the last sweep on this thread scored (the bands' tiles, less
@@ -1849,6 +1917,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             // the pruned ordered sweep's panel data (set when it runs)
             const float* pcen = nullptr;
             const float* ppst = nullptr;
+            const int* pnsg = nullptr;
             float* pthr = nullptr;
             int* tlist = nullptr;
             int* tcnt = nullptr;
@@ -1867,7 +1936,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
                                            (const float*)gthr, n, pthr);
                         hipLaunchKernelGGL(tile_keep, dim3(grid), dim3(256), 0, st, pcen, ppst,
-                                           (const float*)pthr, (int)ntile, dim, metric,
+                                           pnsg, (const float*)pthr, (int)ntile, dim, metric,
                                            (int)sa.b0, (int)sa.b1, tlist, tcnt, tsum);
                         sa.tlist = tlist;
                         sa.tcnt = tcnt;
@@ -2034,8 +2103,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     // was its first bands, so it goes on from there, its lists
                     // and thresholds as the last merge left them (ordered ids),
                     // leaving out the tiles the panels' bounds show empty
-                    float* cen = (float*)extra; extra += al256(ntile * (int64_t)dim * 4);
-                    float* pst = (float*)extra; extra += al256(ntile * 16);
+                    float* cen = (float*)extra; extra += al256(ntile * kSegs * (int64_t)dim * 4);
+                    float* pst = (float*)extra; extra += al256(ntile * kSegs * 16);
+                    int* nsg = (int*)extra; extra += al256(ntile * 4);
                     pthr = (float*)extra; extra += al256(ntile * 4);
                     tlist = (int*)extra; extra += al256(ntile * kBandMax * 4);
                     tcnt = (int*)extra; extra += al256(ntile * 4);
@@ -2043,9 +2113,11 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)tsum, 2);
                     hipLaunchKernelGGL(panel_stats, dim3((unsigned)ntile), dim3(256), 0, st,
                                        (const _Float16*)hp, (const float*)scp, (const float*)xnp,
-                                       n, dim, scaled, cen, pst);
+                                       (const int*)lab, (const int*)perm, n, dim, scaled, cen, pst,
+                                       nsg);
                     pcen = cen;
                     ppst = pst;
+                    pnsg = nsg;
                     rc = bands(pre, kSeedBand, ntile, nullptr, flag, true);
                     if (rc) return rc;
                     s = pre;
