@@ -204,6 +204,10 @@ struct MfmaSweepArgs {
     // tiles tlist[I * kBandMax + k], k < tcnt[I] (ascending, inside its band)
     const int* tlist;
     const int* tcnt;
+    // symmetric sweep: each row's list-0 count as the last merge left it; a
+    // launch that compacts a row's list sets it to -1, so that the next merge
+    // cannot take the row for unchanged (sym_merge)
+    int* mcnt;
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -986,6 +990,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
                                       a.bid + (r * G + split) * a.cap, cnt[rl], a.C, &thr[rl],
                                       &cnt[rl]);
                         if (lane == 0) sthr[rl] = screen_thr<METRIC>(thr[rl], rnorm[rl]);
+                        if (lane == 0 && a.sym && a.mcnt) a.mcnt[r] = -1;
                     }
                 }
                 // let the compaction's stores finish here: left pending, the
@@ -1137,13 +1142,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
 // entry among the C smallest of the whole is among the C smallest of its own
 // list, and whatever a first compaction drops has C entries ahead of it.
 // With seeds (below), a row under C entries keeps its seed as threshold.
+// A row the launch left as the last merge did (list 1 empty, list 0 of the
+// count that merge wrote and not compacted since: mcnt) is a fixed point of
+// the merge and is skipped; in the pruned bands that is most rows.
 __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
                                                  int32_t* __restrict__ bid,
                                                  int32_t* __restrict__ bcnt,
                                                  float* __restrict__ gthr, int* ovf, int64_t n,
                                                  int cap, int fcap, int C,
                                                  const float* __restrict__ seed,
-                                                 int* __restrict__ flag) {
+                                                 int* __restrict__ flag,
+                                                 int* __restrict__ mcnt) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= n) return;
     const int lane = threadIdx.x & 63;
@@ -1153,6 +1162,7 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
     const int32_t* i1 = i0 + cap;
     const int c0 = __builtin_amdgcn_readfirstlane(bcnt[r * 2]);
     int c1 = __builtin_amdgcn_readfirstlane(bcnt[r * 2 + 1]);
+    if (c1 == 0 && c0 == __builtin_amdgcn_readfirstlane(mcnt[r])) return;
     if (c1 > fcap) {                     // appends were dropped: the caller redoes the row
         if (lane == 0) {
             atomicAdd(ovf, 1);
@@ -1242,6 +1252,7 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
         gthr[r] = cnt >= C ? funkey(T) : seed ? seed[r] : INFINITY;
         bcnt[r * 2] = w;
         bcnt[r * 2 + 1] = 0;
+        mcnt[r] = w;
     }
 }
 
@@ -1250,11 +1261,11 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 // (r in panel I, c in panel J) only if the screened distance d^(r, c) falls
 // below r's threshold (own list) or c's (foreign list); thresholds only fall
 // during a launch, so the panels' largest thresholds when it starts bound
-// both tests.  Each panel of the ordered plane, per run of rows of one pivot
+// both tests.  Each panel of the ordered plane, per group of its rows
 // (panel_stats), gets a centre c_I (the mean of the rows as the screen sees
 // them, v = scale * fp16 row), a radius R_I (largest |v - c_I|), its largest
 // |v| (N_I) and the largest gap between a row's fp32 norm, which the screen's
-// l2 formula takes, and |v|^2 (D_I).  Then for every pair of runs:
+// l2 formula takes, and |v|^2 (D_I).  Then for every pair of groups:
 //   l2: d^ >= (|c_I - c_J| - R_I - R_J)^2 - D_I - D_J - 2 g N_I N_J - rounding
 //   ip: d^ >= 1 - (c_I.c_J + R_I |c_J| + R_J |c_I| + R_I R_J) - g N_I N_J - rounding
 // (the triangle inequality; Cauchy-Schwarz on the rows' offsets from the
@@ -1264,42 +1275,96 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 // in it could have been appended, so the lists are the unpruned sweep's.
 // On clustered rows in locality order most tiles pair different clusters.
 
-// A panel's rows come in runs of one pivot each (the order groups rows by
-// pivot); its statistics are kept per run, up to kSegs runs (a panel with
-// more folds the rest into its last), so that a panel straddling two
-// clusters is two tight groups, not one wide one.  One workgroup per panel:
-// nseg[I] runs; for run a, centre cen[(I kSegs + a) dim ..] and
+// A panel's rows are split into up to kSegs groups, each bounded on its own,
+// so that a panel holding two clusters is two tight groups, not one wide one.
+// The groups are the rows nearest to farthest-point seeds: the first seed is
+// the panel's first row, and while some row lies farther than kSplit times
+// the panel's largest threshold (in squared l2 of v; a threshold in ip is
+// half that) from every seed so far, the farthest such row becomes the next
+// seed.  Rows of one cluster lie within about its threshold of each other,
+// so a panel of one cluster stays one group, and a panel whose rows came
+// under one pivot from two clusters (the k-means leaves some clusters
+// without a pivot of their own) splits along them.  Any grouping gives a
+// valid bound; this one only decides how tight.  One workgroup per panel:
+// nseg[I] groups; for group a, centre cen[(I kSegs + a) dim ..] and
 // pst[4 (I kSegs + a) ..] = R, N, D, |c|, each rounded up.
 constexpr int kSegs = 4;
+constexpr float kSplit = 2.0f;
 
 __global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ hp,
                                                    const float* __restrict__ scp,
                                                    const float* __restrict__ xnp,
-                                                   const int* __restrict__ lab,
-                                                   const int* __restrict__ perm, int64_t n,
-                                                   int dim, int scaled, float* __restrict__ cen,
+                                                   const float* __restrict__ pthr, int metric,
+                                                   int64_t n, int dim, int scaled,
+                                                   float* __restrict__ cen,
                                                    float* __restrict__ pst,
                                                    int* __restrict__ nseg) {
     const int I = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t r0 = (int64_t)I * kBM2;
     const int rows = (int)(n - r0 < kBM2 ? n - r0 : kBM2);
-    // run of each row: the number of label changes before it, capped
-    __shared__ int lb[kBM2];
     __shared__ unsigned char seg[kBM2];
+    __shared__ float mind[kBM2];
+    __shared__ float rmax[4];
+    __shared__ int rarg[4];
     __shared__ int cnt[kSegs];
     __shared__ int s_ns;
-    if (tid < rows) lb[tid] = lab[perm[r0 + tid]];
+    __shared__ int s_seed;
     if (tid < kSegs) cnt[tid] = 0;
+    if (tid == 0) { s_ns = 0; s_seed = 0; }
+    const float th = pthr[I];
+    const float tau = kSplit * (metric == SWANN_METRIC_IP ? 2.0f * th : th);
     __syncthreads();
-    if (tid == 0) {
-        int sgi = 0;
-        for (int r = 0; r < rows; ++r) {
-            if (r > 0 && lb[r] != lb[r - 1] && sgi < kSegs - 1) ++sgi;
-            seg[r] = (unsigned char)sgi;
-            cnt[sgi] += 1;
+    for (int k = 0; k < kSegs; ++k) {
+        const int sr = s_seed;
+        const float ssc = scaled ? scp[r0 + sr] : 1.f;
+        // every row's squared distance to seed sr; a nearer seed takes the row
+        for (int r = w; r < rows; r += 4) {
+            const float sc = scaled ? scp[r0 + r] : 1.f;
+            float d2 = 0.f;
+            for (int t = lane; t < dim; t += 64) {
+                const float dv = sc * (float)hp[(r0 + r) * dim + t] -
+                                 ssc * (float)hp[(r0 + sr) * dim + t];
+                d2 = __builtin_fmaf(dv, dv, d2);
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) d2 += __shfl_xor(d2, off, 64);
+            if (lane == 0 && (k == 0 || d2 < mind[r])) {
+                mind[r] = d2;
+                seg[r] = (unsigned char)k;
+            }
         }
-        s_ns = sgi + 1;
-        nseg[I] = sgi + 1;
+        __syncthreads();
+        if (k + 1 == kSegs) break;
+        // the farthest row from every seed so far (lowest index on ties)
+        float v = tid < rows ? mind[tid] : -1.f;
+        int at = tid;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(v, off, 64);
+            const int oa = __shfl_xor(at, off, 64);
+            if (ov > v || (ov == v && oa < at)) { v = ov; at = oa; }
+        }
+        if (lane == 0) { rmax[w] = v; rarg[w] = at; }
+        __syncthreads();
+        if (tid == 0) {
+            float bv = rmax[0];
+            int ba = rarg[0];
+            for (int q = 1; q < 4; ++q)
+                if (rmax[q] > bv || (rmax[q] == bv && rarg[q] < ba)) { bv = rmax[q]; ba = rarg[q]; }
+            // a NaN or infinite threshold never splits (every tile is kept)
+            s_seed = (bv > tau && tau < INFINITY) ? ba : -1;
+        }
+        __syncthreads();
+        if (s_seed < 0) break;
+    }
+    if (tid == 0) {
+        int ns = 0;
+        for (int r = 0; r < rows; ++r) {
+            cnt[seg[r]] += 1;
+            ns = seg[r] + 1 > ns ? seg[r] + 1 : ns;
+        }
+        s_ns = ns;
+        nseg[I] = ns;
     }
     __syncthreads();
     const int ns = s_ns;
@@ -1397,86 +1462,188 @@ __global__ __launch_bounds__(256) void panel_thr(const float* __restrict__ gthr,
     if (threadIdx.x == 0) pthr[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// One workgroup per panel I of a band launch [b0, b1): the column tiles J it
-// must still score, ascending, into tlist[I * kBandMax ..], their count into
-// tcnt[I], and the launch's total into *tsum.  16 lanes a tile; a tile is
-// kept as soon as one pair of runs (one of I's, one of J's) may hold a pair
-// of rows within the thresholds.
-__global__ __launch_bounds__(256) void tile_keep(const float* __restrict__ cen,
-                                                 const float* __restrict__ pst,
-                                                 const int* __restrict__ nseg,
-                                                 const float* __restrict__ pthr, int ntile,
-                                                 int dim, int metric, int b0, int b1,
-                                                 int* __restrict__ tlist, int* __restrict__ tcnt,
-                                                 unsigned long long* __restrict__ tsum) {
-    const int I = blockIdx.x, tid = threadIdx.x, team = tid >> 4, tl = tid & 15;
-    const int j0 = I + b0, j1 = I + b1 < ntile ? I + b1 : ntile;
-    const int nj = j1 - j0;
-    __shared__ unsigned char keep[kBandMax];
-    const int nsI = nseg[I];
-    const double g = ((double)dim + 64.0) * 0x1p-23;
-    for (int j = team; j < nj; j += 16) {
-        const int J = j0 + j;
-        const int nsJ = nseg[J];
-        const double th = fmax((double)pthr[I], (double)pthr[J]);
-        bool k = false;
-        for (int pa = 0; pa < nsI * nsJ && !k; ++pa) {
-            const int ia = I * kSegs + pa / nsJ, jb = J * kSegs + pa % nsJ;
-            const float* ci = cen + (int64_t)ia * dim;
-            const float* cj = cen + (int64_t)jb * dim;
-            double d2 = 0.0, dot = 0.0;
-            for (int t = tl; t < dim; t += 16) {
-                const double x = ci[t], y = cj[t];
-                d2 += (x - y) * (x - y);
-                dot += x * y;
-            }
+// The groups of every panel in panel order, as slots I * kSegs + a (a <
+// nseg[I]), and their number.  One workgroup.
+__global__ __launch_bounds__(1024) void group_list(const int* __restrict__ nseg, int ntile,
+                                                   int* __restrict__ glist,
+                                                   int* __restrict__ gcount) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ int wsum[16];
+    __shared__ int base;
+    if (tid == 0) base = 0;
+    __syncthreads();
+    for (int c0 = 0; c0 < ntile; c0 += 1024) {
+        const int I = c0 + tid;
+        const int v = I < ntile ? nseg[I] : 0;
+        int x = v;                                   // inclusive scan within the wave
 #pragma unroll
-            for (int off = 8; off > 0; off >>= 1) {
-                d2 += __shfl_xor(d2, off, 16);
-                dot += __shfl_xor(dot, off, 16);
-            }
-            const double RI = pst[4 * ia], NI = pst[4 * ia + 1], DI = pst[4 * ia + 2],
-                         CI = pst[4 * ia + 3];
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63) wsum[w] = x;
+        __syncthreads();
+        int pre = base;
+        for (int q = 0; q < w; ++q) pre += wsum[q];
+        pre += x - v;
+        for (int q = 0; q < v; ++q) glist[pre + q] = I * kSegs + q;
+        __syncthreads();
+        if (tid == 0)
+            for (int q = 0; q < 16; ++q) base += wsum[q];
+        __syncthreads();
+    }
+    if (tid == 0) *gcount = base;
+}
+
+// Every pair of groups (ga in panel I, gb in panel J > I) at once: the centres'
+// squared distance (l2) or dot product (ip) in double, as a 64 x 64 block of
+// the groups' Gram per workgroup (LDS tiles of 16 coordinates, 4 x 4 pairs a
+// thread), then the pair's bound (above), rounded down to float, and the
+// tile's bound tlb[I ntile + J] (fkey order) as the least over its pairs.  A
+// NaN bound stores -inf, which keeps the tile.
+constexpr int kGB = 64, kGK = 16;
+
+__global__ __launch_bounds__(256) void group_bounds(const float* __restrict__ cen,
+                                                    const float* __restrict__ pst,
+                                                    const int* __restrict__ glist, int G,
+                                                    int ntile, int dim, int metric,
+                                                    unsigned* __restrict__ tlb) {
+    const int bi = blockIdx.y, bj = blockIdx.x;
+    if (bj < bi) return;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    __shared__ double sa[kGK][kGB + 1];
+    __shared__ double sb[kGK][kGB + 1];
+    __shared__ int slot_a[kGB], slot_b[kGB];
+    if (tid < kGB) {
+        const int ga = bi * kGB + tid, gb = bj * kGB + tid;
+        slot_a[tid] = ga < G ? glist[ga] : -1;
+        slot_b[tid] = gb < G ? glist[gb] : -1;
+    }
+    __syncthreads();
+    const bool l2 = metric == SWANN_METRIC_L2;
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    for (int k0 = 0; k0 < dim; k0 += kGK) {
+        // 64 groups x 16 coordinates a side: 4 elements a thread each
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = e * 256 + tid;
+            const int gr = idx >> 4, kk = idx & 15;
+            const int k = k0 + kk;
+            const int sa_ = slot_a[gr], sb_ = slot_b[gr];
+            sa[kk][gr] = (sa_ >= 0 && k < dim) ? (double)cen[(int64_t)sa_ * dim + k] : 0.0;
+            sb[kk][gr] = (sb_ >= 0 && k < dim) ? (double)cen[(int64_t)sb_ * dim + k] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kGK; ++kk) {
+            double x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = sa[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = sb[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (l2) {
+                        const double d = x[i] - y[j];
+                        acc[i][j] = __builtin_fma(d, d, acc[i][j]);
+                    } else {
+                        acc[i][j] = __builtin_fma(x[i], y[j], acc[i][j]);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+    const double g = ((double)dim + 64.0) * 0x1p-23;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ia = slot_a[ty * 4 + i];
+        if (ia < 0) continue;
+        const int I = ia / kSegs;
+        const double RI = pst[4 * ia], NI = pst[4 * ia + 1], DI = pst[4 * ia + 2],
+                     CI = pst[4 * ia + 3];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int jb = slot_b[tx * 4 + j];
+            if (jb < 0) continue;
+            const int J = jb / kSegs;
+            if (J <= I) continue;
             const double RJ = pst[4 * jb], NJ = pst[4 * jb + 1], DJ = pst[4 * jb + 2],
                          CJ = pst[4 * jb + 3];
             double lb;
-            if (metric == SWANN_METRIC_L2) {
-                const double gap = sqrt(d2) * (1.0 - 1e-9) - RI - RJ;
+            if (l2) {
+                const double gap = sqrt(acc[i][j]) * (1.0 - 1e-9) - RI - RJ;
                 lb = (gap > 0.0 ? gap * gap : 0.0) - DI - DJ - 2.0 * g * NI * NJ -
                      0x1p-21 * 1.1 * (NI + NJ) * (NI + NJ);
             } else {
-                lb = 1.0 - (dot + 1e-9 * CI * CJ + RI * CJ + RJ * CI + RI * RJ) - g * NI * NJ -
-                     0x1p-22 * (1.0 + NI * NJ);
+                lb = 1.0 - (acc[i][j] + 1e-9 * CI * CJ + RI * CJ + RJ * CI + RI * RJ) -
+                     g * NI * NJ - 0x1p-22 * (1.0 + NI * NJ);
             }
-            k = !(lb > th);                      // a NaN keeps the tile
+            float f;
+            if (lb != lb) {
+                f = -INFINITY;
+            } else {
+                f = (float)lb;
+                if ((double)f > lb) f = nextafterf(f, -INFINITY);
+            }
+            atomicMin(&tlb[(int64_t)I * ntile + J], fkey(f));
         }
-        if (tl == 0) keep[j] = k;
     }
-    __syncthreads();
-    if (tid < 64) {
-        int base = 0;
-        for (int jc = 0; jc < nj; jc += 64) {
-            const int j = jc + tid;
-            const bool k = j < nj && keep[j];
-            const uint64_t m = __ballot(k);
-            if (k) tlist[(int64_t)I * kBandMax + base + __popcll(m & ((1ull << tid) - 1ull))] = j0 + j;
-            base += __popcll(m);
+}
+
+__global__ void fill_u32(unsigned* p, int64_t n, unsigned v) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// One wave per panel I of a band launch [b0, b1): the column tiles J it must
+// still score, ascending, into tlist[I * kBandMax ..], their count into
+// tcnt[I], and the launch's total into *tsum.  A tile is kept unless its
+// bound exceeds both panels' largest thresholds (a NaN threshold keeps it).
+__global__ __launch_bounds__(64) void tile_keep(const unsigned* __restrict__ tlb,
+                                                const float* __restrict__ pthr, int ntile,
+                                                int b0, int b1, int* __restrict__ tlist,
+                                                int* __restrict__ tcnt,
+                                                unsigned long long* __restrict__ tsum) {
+    const int I = blockIdx.x, lane = threadIdx.x;
+    const int j0 = I + b0, j1 = I + b1 < ntile ? I + b1 : ntile;
+    const int nj = j1 - j0;
+    const float thI = pthr[I];
+    int base = 0;
+    for (int jc = 0; jc < nj; jc += 64) {
+        const int j = jc + lane;
+        bool k = false;
+        if (j < nj) {
+            const int J = j0 + j;
+            const float th = fmaxf(thI, pthr[J]);
+            k = J == I || !(funkey(tlb[(int64_t)I * ntile + J]) > th);
         }
-        if (tid == 0) {
-            tcnt[I] = base;
-            atomicAdd(tsum, (unsigned long long)base);
-        }
+        const uint64_t m = __ballot(k);
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        if (k) tlist[(int64_t)I * kBandMax + base + __popcll(m & below)] = j0 + j;
+        base += __popcll(m);
+    }
+    if (lane == 0) {
+        tcnt[I] = base;
+        atomicAdd(tsum, (unsigned long long)base);
     }
 }
 
 __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
                                                 int32_t* __restrict__ bcnt, int* ovf,
-                                                int64_t n, const float* __restrict__ seed) {
+                                                int64_t n, const float* __restrict__ seed,
+                                                int* __restrict__ mcnt) {
     const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (r < n) {
         gthr[r] = seed ? seed[r] : INFINITY;
         bcnt[r * 2] = 0;
         bcnt[r * 2 + 1] = 0;
+        mcnt[r] = 0;
     }
     if (r == 0) *ovf = 0;
 }
@@ -1806,11 +1973,13 @@ inline int64_t repair_bytes(int cap) {
 
 
 // The pruned ordered sweep's scratch: panel centres and statistics, the
-// panels' largest thresholds, the launch's tile lists and counts, a counter.
+// panels' largest thresholds, the launch's tile lists and counts, a counter,
+// the list of groups and every tile's bound (ntile^2 floats: 61 MB at 1M rows).
 inline int64_t prune_bytes(int64_t n, int dim) {
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     return al256(ntile * kSegs * (int64_t)dim * 4) + al256(ntile * kSegs * 16) +
-           al256(ntile * 4) * 2 + al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256;
+           al256(ntile * 4) * 2 + al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256 +
+           al256(ntile * kSegs * 4) + 256 + al256(ntile * ntile * 4);
 }
 
 // 256 x 256 tiles the last sweep on this thread scored (the bands' tiles, less
@@ -1904,20 +2073,20 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             // a row.
             float* gthr = (float*)extra; extra += al256(n * 4);
             int* ovf = (int*)extra; extra += 256;
+            int* mcnt = (int*)extra; extra += al256(n * 4);
             MfmaSweepArgs s = a;
             s.splits = 2;
             s.sym = 1;
             s.gthr = gthr;
             s.ovf = ovf;
+            s.mcnt = mcnt;
             s.fcap = cap;
             {                                       // option sweep_sym_fcap: force overflow
                 const int f = option(kOptSweepSymFcap);
                 if (f >= 1 && f < cap) s.fcap = f;
             }
-            // the pruned ordered sweep's panel data (set when it runs)
-            const float* pcen = nullptr;
-            const float* ppst = nullptr;
-            const int* pnsg = nullptr;
+            // the pruned ordered sweep's tile bounds and lists (set when it runs)
+            const unsigned* tlb = nullptr;
             float* pthr = nullptr;
             int* tlist = nullptr;
             int* tcnt = nullptr;
@@ -1935,9 +2104,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     if (prune) {
                         hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
                                            (const float*)gthr, n, pthr);
-                        hipLaunchKernelGGL(tile_keep, dim3(grid), dim3(256), 0, st, pcen, ppst,
-                                           pnsg, (const float*)pthr, (int)ntile, dim, metric,
-                                           (int)sa.b0, (int)sa.b1, tlist, tcnt, tsum);
+                        hipLaunchKernelGGL(tile_keep, dim3(grid), dim3(64), 0, st, tlb,
+                                           (const float*)pthr, (int)ntile, (int)sa.b0,
+                                           (int)sa.b1, tlist, tcnt, tsum);
                         sa.tlist = tlist;
                         sa.tcnt = tcnt;
                     } else {
@@ -1954,7 +2123,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     }
                     hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                                        bkey, bid, bcnt, gthr, ovf, n, cap, sa.fcap, C, seed,
-                                       flag);
+                                       flag, mcnt);
                     const int rc = launch_status("sweep (mfma, symmetric)");
                     if (rc) return rc;
                     b0 = sa.b1;
@@ -2087,7 +2256,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                 hipLaunchKernelGGL(gather_rows, dim3(nrb), dim3(256), 0, st, hi, n, dim, perm, xn,
                                    scaled ? scale : nullptr, hp, xnp, scp);
                 hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
-                                   (const float*)nullptr);
+                                   (const float*)nullptr, mcnt);
                 if (in_order)
                     hipLaunchKernelGGL(fill_zero, dim3(nb256), dim3(256), 0, st, flag, (int)n);
                 MfmaSweepArgs pre = s;
@@ -2110,14 +2279,36 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     tlist = (int*)extra; extra += al256(ntile * kBandMax * 4);
                     tcnt = (int*)extra; extra += al256(ntile * 4);
                     tsum = (unsigned long long*)extra; extra += 256;
+                    int* glist = (int*)extra; extra += al256(ntile * kSegs * 4);
+                    int* gcnt = (int*)extra; extra += 256;
+                    unsigned* tb = (unsigned*)extra; extra += al256(ntile * ntile * 4);
                     hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)tsum, 2);
+                    // groups split at the thresholds the seed bands left
+                    hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
+                                       (const float*)gthr, n, pthr);
                     hipLaunchKernelGGL(panel_stats, dim3((unsigned)ntile), dim3(256), 0, st,
                                        (const _Float16*)hp, (const float*)scp, (const float*)xnp,
-                                       (const int*)lab, (const int*)perm, n, dim, scaled, cen, pst,
-                                       nsg);
-                    pcen = cen;
-                    ppst = pst;
-                    pnsg = nsg;
+                                       (const float*)pthr, metric, n, dim, scaled, cen, pst, nsg);
+                    // every tile's bound once, from the Gram of the groups' centres
+                    hipLaunchKernelGGL(group_list, dim3(1), dim3(1024), 0, st, (const int*)nsg,
+                                       (int)ntile, glist, gcnt);
+                    int ng = 0;
+                    if (hipMemcpyAsync(&ng, gcnt, sizeof(int), hipMemcpyDeviceToHost, st) !=
+                            hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma): reading the group count failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    SWANN_REQUIRE(ng >= ntile && ng <= ntile * kSegs,
+                                  "sweep: panel group count out of range");
+                    hipLaunchKernelGGL(fill_u32, dim3((unsigned)((ntile * ntile + 255) / 256)),
+                                       dim3(256), 0, st, tb, ntile * ntile, 0xffffffffu);
+                    const unsigned gb = (unsigned)((ng + kGB - 1) / kGB);
+                    SWANN_REQUIRE(gb <= 65535, "sweep: too many panel groups for the bound grid");
+                    hipLaunchKernelGGL(group_bounds, dim3(gb, gb), dim3(256), 0, st,
+                                       (const float*)cen, (const float*)pst, (const int*)glist, ng,
+                                       (int)ntile, dim, metric, tb);
+                    tlb = tb;
                     rc = bands(pre, kSeedBand, ntile, nullptr, flag, true);
                     if (rc) return rc;
                     s = pre;
@@ -2132,7 +2323,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             }
         plain:
             hipLaunchKernelGGL(sym_init, dim3(nb256), dim3(256), 0, st, gthr, bcnt, ovf, n,
-                               (const float*)seed);
+                               (const float*)seed, mcnt);
             {
                 const int rc = bands(s, 0, ntile, seed, flag, false);
                 if (rc) return rc;
@@ -2276,7 +2467,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
 int64_t sweep_mfma_extra_bytes(int64_t n, int dim, int x_dtype) {
     const int64_t planes = x_dtype == SWANN_DTYPE_F16 ? 0 : 1;
     const int64_t base = al256(n * 4) * 2 + planes * al256(n * (int64_t)dim * 2) +
-                         al256(n * 4) + 256;
+                         al256(n * 4) + 256 + al256(n * 4);
     // the locality order, seeds and panel repair run only in the symmetric
     // direct-load sweep past its seed bands; only a sweep that may take that
     // path reserves their scratch (a superset of the run's conditions, so the

@@ -410,18 +410,22 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(opt, metric, dtype, mode, d
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
+@pytest.mark.parametrize("k", [15, 30])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype):
-    """Clusters of 2,000 rows (about eight row panels each) in the locality
-    order: most tiles pair two clusters, and the panels' centres and radii
-    prove them empty, so the ordered sweep scores far fewer tiles than the
-    symmetric triangle -- and its lists are still those of the unpruned
-    plain sweep and the oracle's."""
+def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype, k):
+    """Clusters in the locality order: most tiles pair two clusters, and the
+    panels' centres and radii prove them empty, so the ordered sweep scores
+    far fewer tiles than the symmetric triangle -- and its lists are still
+    those of the unpruned plain sweep and the oracle's.  With 15 clusters of
+    2,000 rows each cluster spans about eight row panels; with 30 of 1,000
+    the 58 pivots leave a few clusters without a pivot of their own, whose
+    rows then share one with another cluster's, so some panels mix two
+    clusters and prune only once their rows are split into groups."""
     opt(sweep_sym=1)
     from swann_amd import _lib
-    n, d, C, k = 30000, 64, 24, 15
-    rng = np.random.default_rng(461 + metric)
+    n, d, C = 30000, 64, 24
+    rng = np.random.default_rng(461 + metric + k)
     centres = rng.standard_normal((k, d)).astype(np.float32)
     X = centres[rng.integers(0, k, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
     if metric == 0:
@@ -429,7 +433,7 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     X = np.ascontiguousarray(X.astype(np.float16) if dtype == "f16" else X)
     Xg = torch.from_numpy(X).cuda()
     m = "ip" if metric == 0 else "l2"
-    note("pruned ordered sweep", dtype, m)
+    note("pruned ordered sweep", dtype, m, k)
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
     nt = (n + 255) // 256
     tiles = int(_lib.lib().swann_sweep_tiles_scored())
@@ -438,11 +442,11 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     opt(sweep_noseed=1)
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     assert int(_lib.lib().swann_sweep_tiles_scored()) == nt * (nt + 1) // 2
-    same_lists(f"pruned vs plain {dtype} {m}", cand, cdist, c0.cpu().numpy(), d0.cpu().numpy(),
+    same_lists(f"pruned vs plain {dtype} {m} {k}", cand, cdist, c0.cpu().numpy(), d0.cpu().numpy(),
                1e-6, 1e-6)
-    oc, od = oracle_lists(X, C, metric, ("pruned", metric, dtype))
+    oc, od = oracle_lists(X, C, metric, ("pruned", metric, dtype, k))
     scale = 1.0 if metric == 0 else float(np.abs(od).max())
-    same_lists(f"pruned vs oracle {dtype} {m}", cand, cdist, oc, od, 2e-6 * scale, 2e-5)
+    same_lists(f"pruned vs oracle {dtype} {m} {k}", cand, cdist, oc, od, 2e-6 * scale, 2e-5)
     assert np.allclose(cdist.cpu().numpy(), od, rtol=2e-5, atol=2e-6 * scale)
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
