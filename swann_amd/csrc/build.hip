@@ -300,13 +300,14 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 //
 // PLANES (fp32 rows): each staged float y = x / s_r (s_r a power of two with
 // |y| < 2^15 for the whole row) is split into hi = fp16(y) and lo =
-// fp16((y - hi) * 2^11), hi in logical chunks 0-3 of the row's 128 bytes, lo
-// in 4-7; the Gram entry is s_a s_b (hi.hi + (hi.lo + lo.hi) / 2^11), three
-// 32x32x16 f16 MFMAs per 16 of K (exact products, fp32 sums) for what the
-// fp32 path does in eight 32x32x2 f32 MFMAs.  y keeps 22 of its 24
-// significant bits (the lo.lo term and lo's own rounding are below 2^-22 of
-// the element), so the Gram differs from the fp32 one by a few of its last
-// bits, like a different summation order.
+// fp16(y - hi) (y - hi is exact in fp32), hi in logical chunks 0-3 of the
+// row's 128 bytes, lo in 4-7; the Gram entry is s_a s_b (hi.hi + hi.lo +
+// lo.hi), three 32x32x16 f16 MFMAs per 16 of K into one fp32 accumulator
+// (exact products, fp32 sums) for what the fp32 path does in eight 32x32x2
+// f32 MFMAs.  y keeps 22 of its 24 significant bits (the lo.lo term and lo's
+// own rounding are below 2^-22 of the element; lo is subnormal only for
+// elements below 2^-17 of the row's largest), so the Gram differs from the
+// fp32 one by a few of its last bits, like a different summation order.
 constexpr int kStgRow = 128;                       // bytes of a row per K chunk
 typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 
@@ -336,18 +337,18 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
         on[x] = ti[x] >= 0 && ti[x] * 32 < C && tj[x] * 32 < C;
     }
     const bool busy = on[0] || on[1] || on[2];
-    f32x16v acc[3], accx[PLANES ? 3 : 1];
+    f32x16v acc[3];
 #pragma unroll
     for (int x = 0; x < 3; ++x)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[x][e] = 0.f;
-#pragma unroll
-    for (int x = 0; x < (PLANES ? 3 : 1); ++x)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) accx[x][e] = 0.f;
     const int half = lane >> 5;
-    // staging: 128 rows x 8 chunks, 4 per thread; the next K chunk's loads
-    // go out before this chunk's MFMAs, so their latency hides behind them
+    // staging: 128 rows x 8 chunks, 4 per thread; two K chunks' loads are in
+    // flight ahead of the chunk being multiplied (the kernel waits on memory
+    // latency, not on its MFMAs).  The loads are unconditional -- a lane past
+    // the candidates or the row reads element 0 of the corpus and its bit in
+    // the chunk's mask zeroes it at staging -- so that the compiler counts
+    // them exactly and each staging waits only for its own chunk.
     const int rows = (C + 31) & ~31;               // rows some tile reads
     int sid[4];
 #pragma unroll
@@ -356,50 +357,56 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
         const int id = r < C ? cid[r] : -1;
         sid[q] = r < rows && id >= 0 && id < n ? id : -1;
     }
-    uint4 nxt[4];
-    auto fetch = [&](int k0) {
+    uint4 nxa[4], nxb[4];
+    unsigned oka = 0u, okb = 0u;
+    auto fetch = [&](uint4* dst, unsigned& okm, int k0) {
+        okm = 0u;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int k = k0 + ((q * 256 + tid) & 7) * EPC;
-            nxt[q] = make_uint4(0u, 0u, 0u, 0u);
-            if (sid[q] >= 0 && k < dim)
-                nxt[q] = *reinterpret_cast<const uint4*>(X + (int64_t)sid[q] * dim + k);
+            const bool ok = sid[q] >= 0 && k < dim;
+            const int64_t off = ok ? (int64_t)sid[q] * dim + k : 0;
+            dst[q] = *reinterpret_cast<const uint4*>(X + off);
+            okm |= (ok ? 1u : 0u) << q;
         }
     };
-    fetch(0);
-    for (int k0 = 0; k0 < dim; k0 += KC) {
+    // thread t stages rows (q 256 + t) / 8 < 128 of every chunk (all of the
+    // buffer; rows past the candidates stage zeros), with its rows' scales
+    float inv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) inv[q] = PLANES ? 1.f / srow[(q * 256 + tid) >> 3] : 1.f;
+    auto stage = [&](const uint4* src, unsigned okm) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = q * 256 + tid;
             const int r = e >> 3, c = e & 7;
-            if (r < rows) {
-                if constexpr (PLANES) {
-                    // floats 4c..4c+3 of the chunk: their hi halves to byte
-                    // 8c of the hi plane (logical chunk c/2), lo to the lo plane
-                    const float inv = 1.f / srow[r];
-                    const f32x4v v = __builtin_bit_cast(f32x4v, nxt[q]);
-                    h16x4 hi, lo;
+            const uint4 raw = ((okm >> q) & 1u) ? src[q] : make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (PLANES) {
+                // floats 4c..4c+3 of the chunk: their hi halves to byte 8c of
+                // the hi plane (logical chunk c/2), lo to the lo plane
+                const f32x4v v = __builtin_bit_cast(f32x4v, raw);
+                h16x4 hi, lo;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float y = v[i] * inv;
-                        const _Float16 h = (_Float16)y;
-                        hi[i] = h;
-                        lo[i] = (_Float16)((y - (float)h) * 2048.f);
-                    }
-                    unsigned char* row = stg + r * kStgRow + ((c & 1) << 3);
-                    *reinterpret_cast<uint2*>(row + (((c >> 1) ^ pswz(r)) << 4)) =
-                        __builtin_bit_cast(uint2, hi);
-                    *reinterpret_cast<uint2*>(row + (((4 + (c >> 1)) ^ pswz(r)) << 4)) =
-                        __builtin_bit_cast(uint2, lo);
-                } else {
-                    *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = nxt[q];
+                for (int i = 0; i < 4; ++i) {
+                    const float y = v[i] * inv[q];
+                    const _Float16 h = (_Float16)y;
+                    hi[i] = h;
+                    lo[i] = (_Float16)(y - (float)h);
                 }
+                unsigned char* row = stg + r * kStgRow + ((c & 1) << 3);
+                *reinterpret_cast<uint2*>(row + (((c >> 1) ^ pswz(r)) << 4)) =
+                    __builtin_bit_cast(uint2, hi);
+                *reinterpret_cast<uint2*>(row + (((4 + (c >> 1)) ^ pswz(r)) << 4)) =
+                    __builtin_bit_cast(uint2, lo);
+            } else {
+                *reinterpret_cast<uint4*>(stg + r * kStgRow + ((c ^ pswz(r)) << 4)) = raw;
             }
         }
-        __syncthreads();
-        if (k0 + KC < dim) fetch(k0 + KC);
+    };
+    auto multiply = [&]() {
         if (PLANES && busy) {
-            // 32 of K a chunk: two 16-wide steps of hi.hi, hi.lo and lo.hi
+            // 32 of K a chunk: two 16-wide steps of hi.hi, hi.lo and lo.hi,
+            // all into one accumulator
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int chh = 2 * t + half, chl = 4 + 2 * t + half;
@@ -417,8 +424,8 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
                     const h16x8 bl = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(
                         stg + br * kStgRow + ((chl ^ pswz(br)) << 4)));
                     acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[x], 0, 0, 0);
-                    accx[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, accx[x], 0, 0, 0);
-                    accx[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, accx[x], 0, 0, 0);
+                    acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc[x], 0, 0, 0);
+                    acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc[x], 0, 0, 0);
                 }
             }
         } else if (busy) {
@@ -449,6 +456,33 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
                 }
             }
         }
+    };
+    // Every fetch is issued, also past the last chunk (then of chunk 0 again,
+    // which is never staged): with no fetch under a branch, each staging
+    // waits for its own four loads only (vmcnt(4)), not for the next chunk's.
+    // Two chunks a trip and no exit inside it, so that at the top of the loop
+    // the compiler sees buffer a's loads as the older ones on every path; an
+    // odd last chunk runs after the loop.
+    const int nch = (dim + KC - 1) / KC;
+    fetch(nxa, oka, 0);
+    fetch(nxb, okb, nch > 1 ? KC : 0);
+    int ch = 0;
+    for (; ch + 1 < nch; ch += 2) {
+        stage(nxa, oka);
+        __syncthreads();
+        fetch(nxa, oka, ch + 2 < nch ? (ch + 2) * KC : 0);
+        multiply();
+        __syncthreads();
+        stage(nxb, okb);
+        __syncthreads();
+        fetch(nxb, okb, ch + 3 < nch ? (ch + 3) * KC : 0);
+        multiply();
+        __syncthreads();
+    }
+    if (ch < nch) {
+        stage(nxa, oka);
+        __syncthreads();
+        multiply();
         __syncthreads();
     }
     if (!busy) return;
@@ -461,8 +495,7 @@ __device__ void gram_mfma_staged(const XT* __restrict__ X, int64_t n, int dim, c
             const int r = ti[x] * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
             if (r < C && cc < C) {
                 float g = acc[x][e];
-                if constexpr (PLANES)
-                    g = (srow[r] * srow[cc]) * (acc[x][e] + accx[x][e] * (1.f / 2048.f));
+                if constexpr (PLANES) g = (srow[r] * srow[cc]) * acc[x][e];
                 if (r < cc) gram[tri(r, cc)] = g;
                 else if (r == cc) vn[r] = g;
             }
