@@ -356,3 +356,47 @@ def test_c5_graph_and_search(c5):
     r, r_oracle = rec(ids), rec(oi)
     note("full-size C5 recall@10: Index.search", r, "oracle rounds", r_oracle)
     assert abs(r - r_oracle) <= 0.005
+
+
+@pytest.fixture(scope="module")
+def c3_small():
+    """A C3-shaped corpus (20,000 x 1536 fp16, rank-256 low-rank plus noise,
+    rows normalised, ip) built by Index.build on the GPU and by the oracle's
+    restatement of build.py (sweep, prune, reverse on the fp32 values of the
+    same fp16 rows), with 1,000 queries and their exact top 10."""
+    import os
+    n = 20_000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2033)
+    W = torch.randn((RANK, DIM), generator=g, device="cuda")
+    X16 = lowrank(n, W, g).half()
+    Q = lowrank(1000, W, g)
+    note("c3-shaped graph parity: GPU build")
+    ix_gpu = swann.Index.build(X16, metric="ip", degree=DEG, candidates=C)
+    note("c3-shaped graph parity: oracle build")
+    G_or = O.build_graph(X16.float().cpu().numpy(), metric=O.METRIC_IP, degree=DEG,
+                         candidates=C, alpha=1.2, nthreads=len(os.sched_getaffinity(0)))
+    ix_or = swann.Index(X16, torch.from_numpy(np.ascontiguousarray(G_or, dtype=np.int32)).cuda(),
+                        metric="ip")
+    truth = torch.topk(Q @ X16.float().T, 10, dim=1).indices.cpu().tolist()
+    return dict(ix_gpu=ix_gpu, ix_or=ix_or, G_or=G_or, Q=Q, truth=truth)
+
+
+@pytest.mark.parametrize("knobs", [(8, 12, 32, 0.02), (32, 12, 64, 0.1)])
+def test_c3_shaped_graph_built_both_ways_gives_the_same_recall(c3_small, knobs):
+    """Both builds of the C3-shaped corpus searched by Index.search with the
+    same catalogue and knobs: recall@10 against exact ground truth agrees
+    within 0.005 either way (build.py:153-171, index.py:40-45)."""
+    J, L, Bud, eps = knobs
+    ix_gpu, ix_or, Q, truth = c3_small["ix_gpu"], c3_small["ix_or"], c3_small["Q"], c3_small["truth"]
+    assert torch.equal(ix_gpu.catalogue, ix_or.catalogue)
+
+    def rec(a):
+        return float(np.mean([len(set(x) & set(y)) / 10 for x, y in zip(a.tolist(), truth)]))
+    rs = []
+    for ix in (ix_gpu, ix_or):
+        ids, _ = ix.search(Q, k=10, branches=J, queue=L, budget=Bud, stop_eps=eps, team=16)
+        rs.append(rec(ids))
+    edges = int((ix_gpu.G >= 0).sum()), int((c3_small["G_or"] >= 0).sum())
+    note("c3-shaped graph parity", knobs, "recall@10 gpu-built / oracle-built", rs, "edges", edges)
+    assert abs(rs[0] - rs[1]) <= 0.005
