@@ -1288,7 +1288,7 @@ __global__ __launch_bounds__(256) void sym_merge(float* __restrict__ bkey,
 // valid bound; this one only decides how tight.  One workgroup per panel:
 // nseg[I] groups; for group a, centre cen[(I kSegs + a) dim ..] and
 // pst[4 (I kSegs + a) ..] = R, N, D, |c|, each rounded up.
-constexpr int kSegs = 4;
+constexpr int kSegs = 8;
 constexpr float kSplit = 2.0f;
 
 __global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ hp,
@@ -1450,6 +1450,7 @@ __global__ __launch_bounds__(256) void panel_stats(const _Float16* __restrict__ 
 // The largest threshold of each panel's rows as the last merge published
 // them (+inf for a row with fewer than C so far, or a NaN).
 __global__ __launch_bounds__(256) void panel_thr(const float* __restrict__ gthr, int64_t n,
+                                                 const int* __restrict__ dense,
                                                  float* __restrict__ pthr) {
     const int64_t r = (int64_t)blockIdx.x * kBM2 + threadIdx.x;
     float v = r < n ? gthr[r] : -INFINITY;
@@ -1459,7 +1460,10 @@ __global__ __launch_bounds__(256) void panel_thr(const float* __restrict__ gthr,
     __shared__ float red[4];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    if (threadIdx.x == 0) pthr[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (threadIdx.x == 0)
+        pthr[blockIdx.x] = (dense && dense[blockIdx.x])
+                               ? -INFINITY
+                               : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 // The groups of every panel in panel order, as slots I * kSegs + a (a <
@@ -1604,15 +1608,17 @@ __global__ void fill_u32(unsigned* p, int64_t n, unsigned v) {
 // One wave per panel I of a band launch [b0, b1): the column tiles J it must
 // still score, ascending, into tlist[I * kBandMax ..], their count into
 // tcnt[I], and the launch's total into *tsum.  A tile is kept unless its
-// bound exceeds both panels' largest thresholds (a NaN threshold keeps it).
+// bound exceeds both panels' largest thresholds (a NaN threshold keeps it); a
+// dense panel's tiles wait for the dense launch (dense_keep).
 __global__ __launch_bounds__(64) void tile_keep(const unsigned* __restrict__ tlb,
+                                                const int* __restrict__ dense,
                                                 const float* __restrict__ pthr, int ntile,
                                                 int b0, int b1, int* __restrict__ tlist,
                                                 int* __restrict__ tcnt,
                                                 unsigned long long* __restrict__ tsum) {
     const int I = blockIdx.x, lane = threadIdx.x;
     const int j0 = I + b0, j1 = I + b1 < ntile ? I + b1 : ntile;
-    const int nj = j1 - j0;
+    const int nj = (dense && dense[I]) ? 0 : j1 - j0;
     const float thI = pthr[I];
     int base = 0;
     for (int jc = 0; jc < nj; jc += 64) {
@@ -1630,6 +1636,82 @@ __global__ __launch_bounds__(64) void tile_keep(const unsigned* __restrict__ tlb
     }
     if (lane == 0) {
         tcnt[I] = base;
+        atomicAdd(tsum, (unsigned long long)base);
+    }
+}
+
+// Dense panels.  A panel whose own rows still need more than kDenseTiles tiles
+// beyond the seed window after the seed bands -- its rows have neighbours in
+// few of them, but its groups bound nothing: rows of many clusters that the
+// order's pivots gathered into one run -- would score that many tiles alone
+// in its workgroup, band after band.  Its rows are instead swept again
+// one-sided after the bands (the ordered sweep's repair, which writes their
+// lists from scratch); in the bands it scores none of its tiles and keeps none
+// for its own rows (its panel threshold counts as -inf), and the tiles other
+// panels' rows need from it are scored after the bands by those panels'
+// workgroups (dense_keep), in parallel.  dense_mark lists them (dense[I] = 1,
+// dlist / *nd); dense_flag flags their rows for the repair and raises the
+// overflow count so that the repair runs.
+constexpr int kDenseTiles = 64;
+
+__global__ __launch_bounds__(256) void dense_mark(const unsigned* __restrict__ tlb,
+                                                  const float* __restrict__ pthr, int ntile,
+                                                  int win, int* __restrict__ dense,
+                                                  int* __restrict__ dlist, int* nd) {
+    const int I = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const float th = pthr[I];
+    int c = 0;
+    for (int J = tid; J < ntile; J += 256) {
+        if ((J > I ? J - I : I - J) < win) continue;
+        const int a0 = J < I ? J : I, b0 = J < I ? I : J;
+        c += !(funkey(tlb[(int64_t)a0 * ntile + b0]) > th) ? 1 : 0;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    __shared__ int red[4];
+    if (lane == 0) red[w] = c;
+    __syncthreads();
+    if (tid == 0 && red[0] + red[1] + red[2] + red[3] > kDenseTiles) {
+        dense[I] = 1;
+        dlist[atomicAdd(nd, 1)] = I;
+    }
+}
+
+__global__ __launch_bounds__(256) void dense_flag(const int* __restrict__ dlist, int64_t n,
+                                                  int* __restrict__ flag, int* ovf) {
+    const int64_t r = (int64_t)dlist[blockIdx.x] * kBM2 + threadIdx.x;
+    if (threadIdx.x == 0) atomicAdd(ovf, 1);
+    if (r < n) flag[r] = 1;
+}
+
+// The dense launch's lists: one wave per panel J (not dense), the dense
+// panels D <= J - win whose tile (D, J) J's rows still need at the thresholds
+// the bands left.  (A tile (I, D) with I < D was scored in I's band list.)
+__global__ __launch_bounds__(64) void dense_keep(const unsigned* __restrict__ tlb,
+                                                 const int* __restrict__ dense,
+                                                 const int* __restrict__ dlist, int nd,
+                                                 const float* __restrict__ pthr, int ntile,
+                                                 int win, int* __restrict__ tlist,
+                                                 int* __restrict__ tcnt,
+                                                 unsigned long long* __restrict__ tsum) {
+    const int J = blockIdx.x, lane = threadIdx.x;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const float th = pthr[J];
+    int base = 0;
+    for (int qc = 0; qc < (dense[J] ? 0 : nd); qc += 64) {
+        const int q = qc + lane;
+        bool k = false;
+        int D = 0;
+        if (q < nd) {
+            D = dlist[q];
+            k = D <= J - win && !(funkey(tlb[(int64_t)D * ntile + J]) > th);
+        }
+        const uint64_t m = __ballot(k);
+        if (k) tlist[(int64_t)J * kBandMax + base + __popcll(m & below)] = D;
+        base += __popcll(m);
+    }
+    if (lane == 0) {
+        tcnt[J] = base;
         atomicAdd(tsum, (unsigned long long)base);
     }
 }
@@ -1974,12 +2056,14 @@ inline int64_t repair_bytes(int cap) {
 
 // The pruned ordered sweep's scratch: panel centres and statistics, the
 // panels' largest thresholds, the launch's tile lists and counts, a counter,
-// the list of groups and every tile's bound (ntile^2 floats: 61 MB at 1M rows).
+// the list of groups, every tile's bound (ntile^2 floats: 61 MB at 1M rows)
+// and the dense panels.
 inline int64_t prune_bytes(int64_t n, int dim) {
     const int64_t ntile = (n + kBM2 - 1) / kBM2;
     return al256(ntile * kSegs * (int64_t)dim * 4) + al256(ntile * kSegs * 16) +
            al256(ntile * 4) * 2 + al256(ntile * kBandMax * 4) + al256(ntile * 4) + 256 +
-           al256(ntile * kSegs * 4) + 256 + al256(ntile * ntile * 4);
+           al256(ntile * kSegs * 4) + 256 + al256(ntile * ntile * 4) + al256((ntile + 1) * 4) +
+           al256(ntile * 4);
 }
 
 // 256 x 256 tiles the last sweep on this thread scored (the bands' tiles, less
@@ -2087,6 +2171,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             }
             // the pruned ordered sweep's tile bounds and lists (set when it runs)
             const unsigned* tlb = nullptr;
+            int* dns = nullptr;          // dense panels (dense_mark)
             float* pthr = nullptr;
             int* tlist = nullptr;
             int* tcnt = nullptr;
@@ -2103,10 +2188,10 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     const unsigned grid = (unsigned)(ntile - b0);
                     if (prune) {
                         hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
-                                           (const float*)gthr, n, pthr);
+                                           (const float*)gthr, n, (const int*)dns, pthr);
                         hipLaunchKernelGGL(tile_keep, dim3(grid), dim3(64), 0, st, tlb,
-                                           (const float*)pthr, (int)ntile, (int)sa.b0,
-                                           (int)sa.b1, tlist, tcnt, tsum);
+                                           (const int*)dns, (const float*)pthr, (int)ntile,
+                                           (int)sa.b0, (int)sa.b1, tlist, tcnt, tsum);
                         sa.tlist = tlist;
                         sa.tcnt = tcnt;
                     } else {
@@ -2282,10 +2367,12 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     int* glist = (int*)extra; extra += al256(ntile * kSegs * 4);
                     int* gcnt = (int*)extra; extra += 256;
                     unsigned* tb = (unsigned*)extra; extra += al256(ntile * ntile * 4);
+                    int* dn = (int*)extra; extra += al256((ntile + 1) * 4);   // dense[], count
+                    int* dl = (int*)extra; extra += al256(ntile * 4);
                     hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)tsum, 2);
                     // groups split at the thresholds the seed bands left
                     hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
-                                       (const float*)gthr, n, pthr);
+                                       (const float*)gthr, n, (const int*)nullptr, pthr);
                     hipLaunchKernelGGL(panel_stats, dim3((unsigned)ntile), dim3(256), 0, st,
                                        (const _Float16*)hp, (const float*)scp, (const float*)xnp,
                                        (const float*)pthr, metric, n, dim, scaled, cen, pst, nsg);
@@ -2309,8 +2396,62 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                                        (const float*)cen, (const float*)pst, (const int*)glist, ng,
                                        (int)ntile, dim, metric, tb);
                     tlb = tb;
+                    hipLaunchKernelGGL(fill_zero, dim3((unsigned)((ntile + 256) / 256)), dim3(256), 0,
+                                       st, dn, (int)ntile + 1);
+                    hipLaunchKernelGGL(dense_mark, dim3((unsigned)ntile), dim3(256), 0, st, tlb,
+                                       (const float*)pthr, (int)ntile, (int)kSeedBand, dn, dl,
+                                       dn + ntile);
+                    int nd = 0;
+                    if (hipMemcpyAsync(&nd, dn + ntile, sizeof(int), hipMemcpyDeviceToHost, st) !=
+                            hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma): reading the dense panel count failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    SWANN_REQUIRE(nd >= 0 && nd <= ntile, "sweep: dense panel count out of range");
+                    // more dense panels than a tile list holds: the bands take them as
+                    // they are (slower, the same lists)
+                    if (nd > 0 && nd <= kBandMax) {
+                        hipLaunchKernelGGL(dense_flag, dim3((unsigned)nd), dim3(kBM2), 0, st,
+                                           (const int*)dl, n, flag, ovf);
+                        dns = dn;
+                    }
                     rc = bands(pre, kSeedBand, ntile, nullptr, flag, true);
                     if (rc) return rc;
+                    if (dns) {
+                        // the dense launch: tiles (D, J) scored by J's workgroups
+                        hipLaunchKernelGGL(panel_thr, dim3((unsigned)ntile), dim3(256), 0, st,
+                                           (const float*)gthr, n, (const int*)dns, pthr);
+                        int ndl = 0;
+                        if (hipMemcpyAsync(&ndl, dn + ntile, sizeof(int), hipMemcpyDeviceToHost,
+                                           st) != hipSuccess ||
+                            hipStreamSynchronize(st) != hipSuccess) {
+                            set_error("sweep (mfma): reading the dense panel count failed");
+                            return SWANN_E_LAUNCH;
+                        }
+                        hipLaunchKernelGGL(dense_keep, dim3((unsigned)ntile), dim3(64), 0, st, tlb,
+                                           (const int*)dns, (const int*)dl, ndl,
+                                           (const float*)pthr, (int)ntile, (int)kSeedBand, tlist,
+                                           tcnt, tsum);
+                        MfmaSweepArgs dd = pre;
+                        dd.b0 = 0;
+                        dd.b1 = ntile;
+                        dd.tlist = tlist;
+                        dd.tcnt = tcnt;
+                        const unsigned gd = (unsigned)ntile;
+                        if (scaled) {
+                            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(gd), dim3(1024), 0, st, dd);
+                            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 1, 16>), dim3(gd), dim3(1024), 0, st, dd);
+                        } else {
+                            if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 0, 16>), dim3(gd), dim3(1024), 0, st, dd);
+                            else hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_L2, 0, 16>), dim3(gd), dim3(1024), 0, st, dd);
+                        }
+                        hipLaunchKernelGGL(sym_merge, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
+                                           bkey, bid, bcnt, gthr, ovf, n, cap, dd.fcap, C,
+                                           (const float*)nullptr, flag, mcnt);
+                        rc = launch_status("sweep (mfma, dense panels)");
+                        if (rc) return rc;
+                    }
                     s = pre;
                     seed = nullptr;
                     ordered = perm;

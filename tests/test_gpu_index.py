@@ -410,7 +410,7 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(opt, metric, dtype, mode, d
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
-@pytest.mark.parametrize("k", [15, 30])
+@pytest.mark.parametrize("k", [15, 30, "noise"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype, k):
@@ -421,13 +421,19 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     2,000 rows each cluster spans about eight row panels; with 30 of 1,000
     the 58 pivots leave a few clusters without a pivot of their own, whose
     rows then share one with another cluster's, so some panels mix two
-    clusters and prune only once their rows are split into groups."""
+    clusters and prune only once their rows are split into groups.  With
+    "noise", 15 clusters hold 28,500 rows and 1,500 are scattered far from all
+    of them: their panels bound nothing, so they are left to the one-sided
+    repair of dense panels, which must give the same lists."""
     opt(sweep_sym=1)
     from swann_amd import _lib
     n, d, C = 30000, 64, 24
-    rng = np.random.default_rng(461 + metric + k)
-    centres = rng.standard_normal((k, d)).astype(np.float32)
-    X = centres[rng.integers(0, k, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
+    rng = np.random.default_rng(461 + metric + (k if k != "noise" else 99))
+    kc = 15 if k == "noise" else k
+    centres = rng.standard_normal((kc, d)).astype(np.float32)
+    X = centres[rng.integers(0, kc, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
+    if k == "noise":
+        X[rng.choice(n, 1500, replace=False)] = 3.0 * rng.standard_normal((1500, d)).astype(np.float32)
     if metric == 0:
         X /= np.linalg.norm(X, axis=1, keepdims=True)
     X = np.ascontiguousarray(X.astype(np.float16) if dtype == "f16" else X)
@@ -438,7 +444,8 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     nt = (n + 255) // 256
     tiles = int(_lib.lib().swann_sweep_tiles_scored())
     note("pruned ordered sweep tiles scored", tiles, "of", nt * (nt + 1) // 2)
-    assert 0 < tiles < 0.6 * nt * (nt + 1) // 2
+    if k != "noise":
+        assert 0 < tiles < 0.6 * nt * (nt + 1) // 2
     opt(sweep_noseed=1)
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     assert int(_lib.lib().swann_sweep_tiles_scored()) == nt * (nt + 1) // 2
