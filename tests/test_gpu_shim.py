@@ -1,5 +1,6 @@
-"""The reference-side binding INTEGRATION.md shows a maintainer -- a ctypes
-`ext()` replacing the reference's JIT extension (swann/_engine.py:42-63) --
+"""The reference-side binding documented for a reference maintainer (the
+ctypes `ext()` block of the repository's integration notes, replacing the
+reference's JIT extension, swann/_engine.py:42-63) --
 executed as written (only the library's path is filled in) and driven with the
 reference's own calling convention: state tensors allocated by the caller,
 empty tensors for disabled features (swann/_engine.py:251-306).  Its results
