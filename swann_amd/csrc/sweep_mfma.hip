@@ -2409,9 +2409,11 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         return SWANN_E_LAUNCH;
                     }
                     SWANN_REQUIRE(nd >= 0 && nd <= ntile, "sweep: dense panel count out of range");
-                    // more dense panels than a tile list holds: the bands take them as
-                    // they are (slower, the same lists)
-                    if (nd > 0 && nd <= kBandMax) {
+                    // many dense panels (rows that cluster nowhere, spread over most
+                    // panels): repairing them would cost more than the bands scoring their
+                    // tiles as they are, which then keep about every tile (the plain
+                    // sweep's cost, the same lists); also when a tile list cannot hold them
+                    if (nd > 0 && nd <= kBandMax && (int64_t)nd * 8 <= ntile) {
                         hipLaunchKernelGGL(dense_flag, dim3((unsigned)nd), dim3(kBM2), 0, st,
                                            (const int*)dl, n, flag, ovf);
                         dns = dn;
