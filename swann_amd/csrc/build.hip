@@ -1001,6 +1001,9 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ X
         if (c >= 0 && c < n) {
             const float* xc = X + (int64_t)c * dim;
             if (v4) {
+                // unrolled so that four loads are in flight ahead of their
+                // FMAs; the FMAs keep their order, so s is the same to the bit
+#pragma unroll 4
                 for (int t = tl * 4; t < dim; t += 64) {
                     const float4 a = *reinterpret_cast<const float4*>(xc + t);
                     const float4 b = *reinterpret_cast<const float4*>(xu + t);
