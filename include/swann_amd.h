@@ -258,6 +258,14 @@ int swann_build_sweep(const void* X, int x_dtype, int64_t n, int dim, int metric
  * executed-FLOP figure of the bench (2 * 256 * 256 * dim FLOP a tile). */
 int64_t swann_sweep_tiles_scored(void);
 
+/* Row panels of 256 rows the last swann_build_sweep on this thread handled as
+ * dense: panels of the locality-ordered sweep whose rows lie near too many
+ * other panels to prune, whose tiles the other panels' workgroups score after
+ * the bands and whose rows are then repaired one-sided; 0 when none was, -1
+ * before any sweep.  No counterpart in the reference: a diagnostic for tests
+ * and tuning. */
+int64_t swann_sweep_dense_panels(void);
+
 /* Prune (build.py:46-91): keep candidate i of node u unless an already kept
  * w satisfies alpha * d(w, i) <= d(u, i); rows of `deg` ids, -1 padded.
  * C <= 128, deg <= 128.  deg_per_node [n] (or NULL) caps node u at

@@ -43,6 +43,7 @@ PROTOTYPES = {
     "swann_sweep_workspace_size": (I64, [I64, I, I, I]),
     "swann_build_sweep": (I, [P, I, I64, I, I, I, P, P, P, P]),
     "swann_sweep_tiles_scored": (I64, []),
+    "swann_sweep_dense_panels": (I64, []),
     "swann_prune_workspace_size": (I64, [I64, I, I]),
     "swann_build_prune": (I, [P, I, I64, I, I, P, P, I, I, F, P, P, P, P, P]),
     "swann_reverse_workspace_size": (I64, [I64, I, I]),

@@ -2070,6 +2070,11 @@ inline int64_t prune_bytes(int64_t n, int dim) {
 // those the pruned ordered sweep proved empty, plus any repair), -1 before.
 thread_local int64_t g_tiles_scored = -1;
 
+// Row panels the last sweep on this thread handled as dense (tiles scored by
+// the other panels' workgroups after the bands, rows repaired one-sided), -1
+// before any sweep.
+thread_local int64_t g_dense_panels = -1;
+
 // Tiles of one band launch [b0, b1) over ntile panels: panel I has
 // min(b1, ntile - I) - b0 of them while that is positive.
 inline int64_t band_tiles(int64_t ntile, int64_t b0, int64_t b1) {
@@ -2104,6 +2109,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                    hipStream_t st, int* used, const int32_t** perm_out) {
     *perm_out = nullptr;
     g_tiles_scored = 0;
+    g_dense_panels = 0;
     const int64_t ntile_all = (n + kBM2 - 1) / kBM2;
     float* xn = (float*)extra; extra += al256(n * 4);
     float* scale = (float*)extra; extra += al256(n * 4);
@@ -2417,6 +2423,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         hipLaunchKernelGGL(dense_flag, dim3((unsigned)nd), dim3(kBM2), 0, st,
                                            (const int*)dl, n, flag, ovf);
                         dns = dn;
+                        g_dense_panels = nd;
                     }
                     rc = bands(pre, kSeedBand, ntile, nullptr, flag, true);
                     if (rc) return rc;
@@ -2644,3 +2651,4 @@ int sweep_mfma_cap(int C) {
 }  // namespace swann
 
 extern "C" int64_t swann_sweep_tiles_scored(void) { return swann::g_tiles_scored; }
+extern "C" int64_t swann_sweep_dense_panels(void) { return swann::g_dense_panels; }

@@ -410,7 +410,7 @@ def test_mfma_sweep_seeded_thresholds_keep_the_lists(opt, metric, dtype, mode, d
     assert not (cand.cpu().numpy() == np.arange(n)[:, None]).any()
 
 
-@pytest.mark.parametrize("k", [15, 30, "noise"])
+@pytest.mark.parametrize("k", [15, 30, "noise", "noise10"])
 @pytest.mark.parametrize("metric", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype, k):
@@ -422,18 +422,23 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     the 58 pivots leave a few clusters without a pivot of their own, whose
     rows then share one with another cluster's, so some panels mix two
     clusters and prune only once their rows are split into groups.  With
-    "noise", 15 clusters hold 28,500 rows and 1,500 are scattered far from all
-    of them: their panels bound nothing, so they are left to the one-sided
-    repair of dense panels, which must give the same lists."""
+    "noise10", 15 clusters and 10 rows far from all of them: under l2 the few
+    panels holding those bound nothing and go dense (their tiles scored by the
+    other panels after the bands, their rows repaired one-sided; under ip the
+    normalised outliers are mere directions and some clustered ip panels go
+    dense instead); with "noise", 1,500 such rows spread over most panels,
+    too many to repair, and the bands keep those panels' tiles as they are.
+    Every variant must give the plain sweep's lists."""
     opt(sweep_sym=1)
     from swann_amd import _lib
     n, d, C = 30000, 64, 24
-    rng = np.random.default_rng(461 + metric + (k if k != "noise" else 99))
-    kc = 15 if k == "noise" else k
+    noisy = {"noise": 1500, "noise10": 10}.get(k, 0)
+    rng = np.random.default_rng(461 + metric + (k if not noisy else 99 + noisy))
+    kc = 15 if noisy else k
     centres = rng.standard_normal((kc, d)).astype(np.float32)
     X = centres[rng.integers(0, kc, n)] + 0.3 * rng.standard_normal((n, d)).astype(np.float32)
-    if k == "noise":
-        X[rng.choice(n, 1500, replace=False)] = 3.0 * rng.standard_normal((1500, d)).astype(np.float32)
+    if noisy:
+        X[rng.choice(n, noisy, replace=False)] = 3.0 * rng.standard_normal((noisy, d)).astype(np.float32)
     if metric == 0:
         X /= np.linalg.norm(X, axis=1, keepdims=True)
     X = np.ascontiguousarray(X.astype(np.float16) if dtype == "f16" else X)
@@ -443,9 +448,14 @@ def test_ordered_sweep_prunes_empty_tiles_and_keeps_the_lists(opt, metric, dtype
     cand, cdist = B.knn_candidates(Xg, C, metric=m)
     nt = (n + 255) // 256
     tiles = int(_lib.lib().swann_sweep_tiles_scored())
-    note("pruned ordered sweep tiles scored", tiles, "of", nt * (nt + 1) // 2)
+    dense = int(_lib.lib().swann_sweep_dense_panels())
+    note("pruned ordered sweep tiles scored", tiles, "of", nt * (nt + 1) // 2, "dense", dense)
     if k != "noise":
         assert 0 < tiles < 0.6 * nt * (nt + 1) // 2
+    if k == "noise10" and metric == 1:
+        assert 0 < dense <= 10          # the outliers' panels, scored after the bands
+    if k == "noise":
+        assert dense == 0               # too many to repair: left to the bands
     opt(sweep_noseed=1)
     c0, d0 = B.knn_candidates(Xg, C, metric=m)
     assert int(_lib.lib().swann_sweep_tiles_scored()) == nt * (nt + 1) // 2
