@@ -6,10 +6,12 @@
 // (distance, index).  The reference folds slices of 8192 columns into a
 // running best; the result is the exact top-E either way.
 //
-// Small batches would leave most of the chip idle: a batch of 8 against a
-// 4096-entry catalogue is 64 GEMM tiles.  There the K dimension is split so
-// the grid has >= 1024 workgroups, partial dot products go to the workspace,
-// and a finishing pass sums them in split order and applies the formula.
+// Batches of up to 8 queries read the catalogue once in a wave-per-rows
+// product (dist_gemv).  Larger batches that would still leave most of the
+// chip idle (64 queries against a 4096-entry catalogue are 64 GEMM tiles)
+// split the K dimension so the grid has >= 1024 workgroups: partial dot
+// products go to the workspace, and a finishing pass sums them in split
+// order and applies the formula.
 // The top-E keeps a row of up to 16384 distances in the registers of 1024
 // threads and finds the E-th smallest by a 4-pass radix select over the
 // distances' order-preserving 32-bit keys (LDS histograms), then sorts only
@@ -40,9 +42,26 @@ int split_for(int64_t tiles) {
     return (int)(s < kMaxSplit ? s : kMaxSplit);
 }
 
-__device__ __forceinline__ bool lt(float da, int ia, float db, int ib) {
-    return (da < db) || (da == db && ia < ib);
+// Order-preserving key of a distance: -0 folded onto +0, so equal distances
+// have equal keys; every NaN takes the largest key, so it ranks after every
+// number (as torch.topk ranks NaN) and the order is total.
+__device__ __forceinline__ unsigned dkey(float d) {
+    if (d != d) return 0xFFFFFFFFu;
+    const unsigned u = __float_as_uint(d + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// (distance, index) order: on numbers the plain comparison; a NaN after
+// every number, NaNs by index.  Total, so a sorting network run on it keeps
+// every element once and sorts the padding (pad_d(), INT32_MAX) last.
+__device__ __forceinline__ bool lt(float da, int ia, float db, int ib) {
+    const unsigned ka = dkey(da), kb = dkey(db);
+    return ka < kb || (ka == kb && ia < ib);
+}
+
+// The distance of a padding entry: a NaN, which with index INT32_MAX ranks
+// after every real entry.
+__device__ __forceinline__ float pad_d() { return __int_as_float(0x7fffffff); }
 
 // Squared norms of rows (only the L2 metric needs them).
 __global__ __launch_bounds__(256) void row_norms(const float* __restrict__ A, int64_t n, int dim,
@@ -117,6 +136,130 @@ __global__ __launch_bounds__(256) void dist_gemm(const float* __restrict__ A,
     }
 }
 
+// Small batches (nq <= kGvMaxQ): D[m, p] for every query m against catalogue
+// rows p, the catalogue read once.  A wave takes kGvRows consecutive rows
+// (one: a 4096-row catalogue is 4096 waves, with eight 16-byte loads of the
+// row in flight a lane); lane l sums the 4-float blocks l, l + 64, ... of
+// each row against each query, which the workgroup stages in LDS
+// kGvLds / NQ dimensions at a time; then the wave folds each sum.  For l2 the
+// row's |v|^2 is summed on the way.  The 64 x 64 tiles of dist_gemm would
+// spend 63 of 64 products on padding at batch 1 and read the catalogue
+// through 16 split-K passes.  (Measured at 4096 x 4096 with the top-E: 1
+// row and 8 waves a workgroup beat 2 or 4 rows a wave and 4 waves.)
+constexpr int kGvRows = 1, kGvWaves = 8, kGvMaxQ = 8;
+constexpr int kGvLds = 8192;                  // staged query floats (32 KB)
+
+template <int NQ>
+__global__ __launch_bounds__(kGvWaves * 64) void dist_gemv(const float* __restrict__ Q,
+                                                           const float* __restrict__ V, int nq,
+                                                           int64_t P, int dim, int metric,
+                                                           const float* __restrict__ qn,
+                                                           float* __restrict__ Dm) {
+    constexpr int KC = kGvLds / NQ;           // dimensions staged a pass
+    __shared__ __align__(16) float qs[kGvLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t p0 = ((int64_t)blockIdx.x * kGvWaves + wave) * kGvRows;
+    const bool vec = (dim & 3) == 0 && ((uintptr_t)V & 15) == 0;
+    const bool qvec = (dim & 3) == 0 && ((uintptr_t)Q & 15) == 0;
+    float acc[kGvRows][NQ], vv[kGvRows];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r) {
+        vv[r] = 0.f;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) acc[r][m] = 0.f;
+    }
+    // rows past P read row P - 1 (their sums are never written)
+    const float* vr[kGvRows];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r) vr[r] = V + (p0 + r < P ? p0 + r : P - 1) * (int64_t)dim;
+    for (int k0 = 0; k0 < dim; k0 += KC) {
+        const int kc = dim - k0 < KC ? dim - k0 : KC;
+        __syncthreads();                      // the last pass's reads of qs are done
+        if (qvec) {
+            // 16-byte loads, four in flight a thread
+            const int nv = NQ * (kc >> 2);
+#pragma unroll 4
+            for (int i = tid; i < nv; i += kGvWaves * 64) {
+                const int m = i / (kc >> 2), t = (i - m * (kc >> 2)) << 2;
+                const float4 v = m < nq ? *reinterpret_cast<const float4*>(Q + (int64_t)m * dim + k0 + t)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(&qs[m * KC + t]) = v;
+            }
+        } else {
+            for (int i = tid; i < NQ * kc; i += kGvWaves * 64) {
+                const int m = i / kc, t = i - m * kc;
+                qs[m * KC + t] = m < nq ? Q[(int64_t)m * dim + k0 + t] : 0.f;
+            }
+        }
+        __syncthreads();
+        if (vec) {
+#pragma unroll 8
+            for (int t = lane * 4; t < kc; t += 256) {
+                float4 x[kGvRows];
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r)
+                    x[r] = *reinterpret_cast<const float4*>(vr[r] + k0 + t);
+#pragma unroll
+                for (int m = 0; m < NQ; ++m) {
+                    const float4 q = *reinterpret_cast<const float4*>(&qs[m * KC + t]);
+#pragma unroll
+                    for (int r = 0; r < kGvRows; ++r) {
+                        float s = acc[r][m];
+                        s = __builtin_fmaf(x[r].x, q.x, s);
+                        s = __builtin_fmaf(x[r].y, q.y, s);
+                        s = __builtin_fmaf(x[r].z, q.z, s);
+                        acc[r][m] = __builtin_fmaf(x[r].w, q.w, s);
+                    }
+                }
+                if (metric == SWANN_METRIC_L2) {
+#pragma unroll
+                    for (int r = 0; r < kGvRows; ++r) {
+                        float s = vv[r];
+                        s = __builtin_fmaf(x[r].x, x[r].x, s);
+                        s = __builtin_fmaf(x[r].y, x[r].y, s);
+                        s = __builtin_fmaf(x[r].z, x[r].z, s);
+                        vv[r] = __builtin_fmaf(x[r].w, x[r].w, s);
+                    }
+                }
+            }
+        } else {
+            for (int t = lane; t < kc; t += 64) {
+                float x[kGvRows];
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) x[r] = vr[r][k0 + t];
+#pragma unroll
+                for (int m = 0; m < NQ; ++m) {
+                    const float q = qs[m * KC + t];
+#pragma unroll
+                    for (int r = 0; r < kGvRows; ++r) acc[r][m] = __builtin_fmaf(x[r], q, acc[r][m]);
+                }
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) vv[r] = __builtin_fmaf(x[r], x[r], vv[r]);
+            }
+        }
+    }
+    // fold every sum over the wave (each lane ends with every total); lane
+    // r * NQ + m writes D[m, p0 + r]
+    float out = 0.f;
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r) {
+        float n2 = vv[r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) n2 += __shfl_xor(n2, off, 64);
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            float s = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+            if (lane == r * NQ + m)
+                out = metric == SWANN_METRIC_IP ? 1.0f - s
+                                                : (n2 - 2.0f * s) + (m < nq ? qn[m] : 0.f);
+        }
+    }
+    const int r = lane / NQ, m = lane - r * NQ;
+    if (lane < kGvRows * NQ && m < nq && p0 + r < P) Dm[(int64_t)m * P + p0 + r] = out;
+}
+
 // Sum the S partial dot products in split order, then the distance formula.
 __global__ __launch_bounds__(256) void split_finish(const float* __restrict__ part, int S,
                                                     int64_t M, int64_t N, int metric,
@@ -129,13 +272,6 @@ __global__ __launch_bounds__(256) void split_finish(const float* __restrict__ pa
     for (int z = 1; z < S; ++z) s += part[(int64_t)z * M * N + i];
     const int64_t m = i / N, nn = i - m * N;
     Dm[i] = metric == SWANN_METRIC_IP ? 1.0f - s : (bn[nn] - 2.0f * s) + an[m];
-}
-
-// Order-preserving key of a distance (-0 folded onto +0, so equal distances
-// have equal keys); larger keys sort later.
-__device__ __forceinline__ unsigned dkey(float d) {
-    const unsigned u = __float_as_uint(d + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 // Row top-E for rows of N <= kRadBlock*kRadPer: radix select of the E-th key,
@@ -152,11 +288,14 @@ __global__ __launch_bounds__(kRadBlock) void row_topk_radix(const float* __restr
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t r = blockIdx.x;
     const float* row = Dm + r * N;
+    // slots i < nper hold keys (column tid + i * kRadBlock); the loops below
+    // visit only those, and skip the padding columns c >= N
+    const int nper = (int)((N + kRadBlock - 1) / kRadBlock);
     unsigned key[kRadPer];
 #pragma unroll
     for (int i = 0; i < kRadPer; ++i) {
         const int64_t c = tid + (int64_t)i * kRadBlock;
-        key[i] = c < N ? dkey(row[c]) : 0xFFFFFFFFu;
+        key[i] = (i < nper && c < N) ? dkey(row[c]) : 0xFFFFFFFFu;
     }
     // ---- the E-th smallest key, 8 bits at a time from the top ----
     unsigned prefix = 0u, pmask = 0u;
@@ -165,9 +304,29 @@ __global__ __launch_bounds__(kRadBlock) void row_topk_radix(const float* __restr
         const int shift = 24 - 8 * pass;
         if (tid < 256) hist[tid] = 0u;
         __syncthreads();
+        // Distances that share their leading bits (all of them, in the
+        // first pass over a row of similar distances) fall into a few bins:
+        // lanes of a wave that share the first two bins add with one atomic
+        // each, the rest one by one.
 #pragma unroll
-        for (int i = 0; i < kRadPer; ++i)
-            if ((key[i] & pmask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255u], 1u);
+        for (int i = 0; i < kRadPer; ++i) {
+            if (i >= nper) break;
+            const unsigned bin = (key[i] >> shift) & 255u;
+            bool pend = tid + i * kRadBlock < N && (key[i] & pmask) == prefix;
+#pragma unroll
+            for (int peel = 0; peel < 2; ++peel) {
+                const uint64_t act = __ballot(pend);
+                if (act == 0) break;
+                const unsigned b0 = __builtin_amdgcn_readlane(bin, __builtin_ctzll(act));
+                const uint64_t same = __ballot(pend && bin == b0);
+                if (pend && bin == b0) {
+                    if (lane == __builtin_ctzll(same))
+                        atomicAdd(&hist[b0], (unsigned)__builtin_popcountll(same));
+                    pend = false;
+                }
+            }
+            if (pend) atomicAdd(&hist[bin], 1u);
+        }
         __syncthreads();
         if (wave == 0) {
             unsigned h[4], run = 0u;
@@ -200,6 +359,7 @@ __global__ __launch_bounds__(kRadBlock) void row_topk_radix(const float* __restr
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kRadPer; ++i) {
+        if (i >= nper) break;
         if (key[i] < T) {
             const int pos = atomicAdd(&s_nsel, 1);
             const int c = tid + i * kRadBlock;
@@ -209,7 +369,7 @@ __global__ __launch_bounds__(kRadBlock) void row_topk_radix(const float* __restr
     __syncthreads();
     const int nless = s_nsel;           // == E - need
     // ties at T in index order (c = tid + i*kRadBlock: i-major, then tid)
-    for (int i = 0; i < kRadPer; ++i) {
+    for (int i = 0; i < nper; ++i) {
         // padding slots (c >= N) carry the largest key and the largest
         // indices: never taken, even when a NaN distance ties them
         const bool eq = key[i] == T && tid + i * kRadBlock < N;
@@ -233,9 +393,37 @@ __global__ __launch_bounds__(kRadBlock) void row_topk_radix(const float* __restr
         if (s_ebase >= need) break;     // uniform: every later tie ranks >= need
     }
     // ---- sort the E survivors by (d, index) ----
+    if (E <= 64) {
+        // one wave, in registers: a bitonic network over 64 lanes (lanes
+        // past E hold the padding entry and sort last), no barriers
+        __syncthreads();
+        if (wave != 0) return;
+        float d = lane < E ? sd[lane] : pad_d();
+        int id = lane < E ? si[lane] : INT32_MAX;
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const float d2 = __shfl_xor(d, stride, 64);
+                const int id2 = __shfl_xor(id, stride, 64);
+                // both lanes of a pair decide the same swap, from the lower
+                // lane's element (so a pair the order cannot rank, NaN
+                // against NaN, is swapped or kept whole, never duplicated)
+                const bool up = (lane & size) == 0;
+                const bool sw = (lane & stride) == 0 ? up != lt(d, id, d2, id2)
+                                                     : up != lt(d2, id2, d, id);
+                if (sw) { d = d2; id = id2; }
+            }
+        }
+        if (lane < E) {
+            oi[r * E + lane] = id;
+            if (od) od[r * E + lane] = d;
+        }
+        return;
+    }
     int n = 1;
     while (n < E) n <<= 1;
-    for (int i = E + tid; i < n; i += kRadBlock) { sd[i] = INFINITY; si[i] = INT32_MAX; }
+    for (int i = E + tid; i < n; i += kRadBlock) { sd[i] = pad_d(); si[i] = INT32_MAX; }
     __syncthreads();
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -295,7 +483,7 @@ __global__ __launch_bounds__(kTopBlock) void row_topk(const float* __restrict__ 
         for (int i = keep + threadIdx.x; i < n; i += kTopBlock) {
             const int64_t c = c0 + (i - keep);
             const bool real = i < fill;
-            sd[i] = real ? row[c] : INFINITY;
+            sd[i] = real ? row[c] : pad_d();
             si[i] = real ? (int)c : INT32_MAX;
         }
         __syncthreads();
@@ -359,30 +547,26 @@ int scratch_address(void** out) {
 }
 }  // namespace
 
-static int select_run(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int E,
-                      int metric, int32_t* out_idx, float* out_dist, void* workspace,
-                      void* stream) {
-    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
-                  "metric must be 0 (ip) or 1 (l2)");
-    SWANN_REQUIRE(nq >= 0 && P >= 1 && dim >= 1, "select: need nq >= 0, P >= 1, dim >= 1");
-    SWANN_REQUIRE(E >= 1 && E <= kTopBuf / 2, "select: E must be in 1..%d", kTopBuf / 2);
-    SWANN_REQUIRE(E <= P, "select: E (%d) exceeds the catalogue size (%lld)", E, (long long)P);
-    SWANN_REQUIRE(nq <= INT32_MAX && (P + kTN - 1) / kTN <= INT32_MAX &&
-                      (nq + kTM - 1) / kTM <= 65535,
-                  "select: batch of %lld queries too large for one call", (long long)nq);
-    if (nq == 0) return SWANN_OK;
-    SWANN_REQUIRE(Q && Vp && out_idx && workspace, "select: a required pointer is NULL");
-    hipStream_t st = (hipStream_t)stream;
-    char* ws = (char*)workspace;
-    float* Dm = (float*)ws;
-    float* qn = (float*)(ws + ((nq * P * 4 + 255) / 256) * 256);
-    float* vn = (float*)((char*)qn + ((nq * 4 + 255) / 256) * 256);
-    if (metric == SWANN_METRIC_L2) {
-        hipLaunchKernelGGL(row_norms, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st, Q, nq, dim,
-                           qn);
+// The distance matrix of a small batch: one pass over the catalogue.
+static int gemv_run(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int metric,
+                    const float* qn, float* Dm, hipStream_t st) {
+    const dim3 g((unsigned)((P + kGvRows * kGvWaves - 1) / (kGvRows * kGvWaves)));
+    const dim3 b(kGvWaves * 64);
+    const int q = (int)nq;
+    if (nq == 1) hipLaunchKernelGGL(dist_gemv<1>, g, b, 0, st, Q, Vp, q, P, dim, metric, qn, Dm);
+    else if (nq == 2) hipLaunchKernelGGL(dist_gemv<2>, g, b, 0, st, Q, Vp, q, P, dim, metric, qn, Dm);
+    else if (nq <= 4) hipLaunchKernelGGL(dist_gemv<4>, g, b, 0, st, Q, Vp, q, P, dim, metric, qn, Dm);
+    else hipLaunchKernelGGL(dist_gemv<8>, g, b, 0, st, Q, Vp, q, P, dim, metric, qn, Dm);
+    return launch_status("select gemv");
+}
+
+// The distance matrix of a larger batch: 64 x 64 tiles, K split when the
+// tiles alone would not fill the chip.
+static int gemm_run(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int metric,
+                    const float* qn, float* vn, float* Dm, hipStream_t st) {
+    if (metric == SWANN_METRIC_L2)
         hipLaunchKernelGGL(row_norms, dim3((unsigned)((P + 3) / 4)), dim3(256), 0, st, Vp, P, dim,
                            vn);
-    }
     const int64_t tiles = ((P + kTN - 1) / kTN) * ((nq + kTM - 1) / kTM);
     int S = split_for(tiles);
     int kper = dim;
@@ -402,7 +586,32 @@ static int select_run(const float* Q, int64_t nq, int dim, const float* Vp, int6
         hipLaunchKernelGGL(dist_gemm, grid, dim3(256), 0, st, Q, Vp, nq, P, dim, metric, qn, vn,
                            Dm, dim);
     }
-    int rc = launch_status("select gemm");
+    return launch_status("select gemm");
+}
+
+static int select_run(const float* Q, int64_t nq, int dim, const float* Vp, int64_t P, int E,
+                      int metric, int32_t* out_idx, float* out_dist, void* workspace,
+                      void* stream) {
+    SWANN_REQUIRE(metric == SWANN_METRIC_IP || metric == SWANN_METRIC_L2,
+                  "metric must be 0 (ip) or 1 (l2)");
+    SWANN_REQUIRE(nq >= 0 && P >= 1 && dim >= 1, "select: need nq >= 0, P >= 1, dim >= 1");
+    SWANN_REQUIRE(E >= 1 && E <= kTopBuf / 2, "select: E must be in 1..%d", kTopBuf / 2);
+    SWANN_REQUIRE(E <= P, "select: E (%d) exceeds the catalogue size (%lld)", E, (long long)P);
+    SWANN_REQUIRE(nq <= INT32_MAX && (P + kTN - 1) / kTN <= INT32_MAX &&
+                      (nq + kTM - 1) / kTM <= 65535,
+                  "select: batch of %lld queries too large for one call", (long long)nq);
+    if (nq == 0) return SWANN_OK;
+    SWANN_REQUIRE(Q && Vp && out_idx && workspace, "select: a required pointer is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    float* Dm = (float*)ws;
+    float* qn = (float*)(ws + ((nq * P * 4 + 255) / 256) * 256);
+    float* vn = (float*)((char*)qn + ((nq * 4 + 255) / 256) * 256);
+    if (metric == SWANN_METRIC_L2)
+        hipLaunchKernelGGL(row_norms, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st, Q, nq, dim,
+                           qn);
+    const int rc = nq <= kGvMaxQ ? gemv_run(Q, nq, dim, Vp, P, metric, qn, Dm, st)
+                                 : gemm_run(Q, nq, dim, Vp, P, metric, qn, vn, Dm, st);
     if (rc) return rc;
     if (P <= (int64_t)kRadBlock * kRadPer && E <= kRadMaxE)
         hipLaunchKernelGGL(row_topk_radix, dim3((unsigned)nq), dim3(kRadBlock), 0, st, Dm, P, E,

@@ -604,23 +604,34 @@ def test_index_capture_matches_eager_search():
         cs.run(Q[:3])
 
 
-@pytest.mark.parametrize("nq", [1, 3, 8, 64, 300])
+@pytest.mark.parametrize("nq", [1, 2, 3, 5, 8, 64, 300])
 @pytest.mark.parametrize("metric", [0, 1])
 def test_select_small_and_large_batches_match_oracle(nq, metric):
-    """Selection at every batch shape: split-K partials for small grids, the
-    radix top-E for rows up to 16384 and the chunked bitonic beyond; ties
-    (duplicated catalogue rows) resolve to the lower index, as the oracle's
-    (d, index) order."""
+    """Selection at every batch shape: the one-pass product for batches of up
+    to 8 (16-byte loads, and element loads at d = 70), split-K partials for
+    small grids, the radix top-E for rows up to 16384 and the chunked bitonic
+    beyond; ties (duplicated catalogue rows) resolve to the lower index, as the oracle's
+    (d, index) order.  With two or more queries, query 1 is NaN throughout:
+    its distances cannot be ranked, so its E entries come in no stated order,
+    but they are E distinct catalogue rows (both survivor sorts swap pairs
+    whole), and the other queries' lists are unaffected."""
     rng = np.random.default_rng(100 + nq)
-    for P, d, E in ((4096, 256, 32), (5000, 72, 128), (20000, 64, 40)):
+    for P, d, E in ((4096, 256, 32), (5000, 72, 128), (20000, 64, 40), (3000, 70, 16)):
         V = rng.standard_normal((P, d)).astype(np.float32)
         V[P // 2:P // 2 + 50] = V[:50]                     # exact duplicates -> ties
         Q = rng.standard_normal((nq, d)).astype(np.float32)
         Q[0] = V[7]
+        if nq >= 2:
+            Q[1] = np.nan
         idx = S.select_nearest(torch.from_numpy(Q).cuda(), torch.from_numpy(V).cuda(), E,
                                metric=metric).cpu().numpy()
-        want, _ = O.select_nearest(Q, V, E, metric, nthreads=8)
         assert idx.shape == (nq, E)
+        assert ((idx >= 0) & (idx < P)).all()
+        assert (np.sort(idx, 1)[:, 1:] != np.sort(idx, 1)[:, :-1]).all()   # distinct
+        if nq >= 2:
+            keep = np.arange(nq) != 1
+            Q, idx = Q[keep], idx[keep]
+        want, _ = O.select_nearest(Q, V, E, metric, nthreads=8)
         Q64, V64 = Q.astype(np.float64), V.astype(np.float64)
 
         def dist(e):
@@ -630,7 +641,6 @@ def test_select_small_and_large_batches_match_oracle(nq, metric):
         wd = dist(want)
         same_lists(f"select {nq} {metric} {P} {d} {E}", idx, dist(idx), want, wd,
                    2e-6 * float(np.abs(wd).max()), 2e-5)
-        assert (np.sort(idx, 1)[:, 1:] != np.sort(idx, 1)[:, :-1]).all()   # distinct
         if metric == 1:
             # q = V[7], which has an exact duplicate at P//2 + 7: a tie at the
             # top, resolved to the lower index
