@@ -93,6 +93,31 @@ def test_batch_beyond_65535_is_served():
     assert (ids[:, 0] == np.repeat(np.arange(700), 100)).mean() > 0.95
 
 
+@pytest.mark.parametrize("branches", [40, 100])
+def test_nan_query_finds_nothing_and_leaves_the_batch_alone(branches):
+    """A query that is NaN throughout: its catalogue distances cannot be
+    ranked, yet its seeds are distinct catalogue rows (the selection's sorts
+    rank NaN after every number, and a branch count that is not a power of
+    two pads them), each seed scores NaN and is dropped, so its answer is
+    empty, (-1, +inf); the other queries' answers stay valid, with their
+    recall."""
+    X, Q = corpus(n=4000, nq=64)
+    index = swann.Index.build(X, degree=32, candidates=48)
+    truth = exact_topk(X, Q, 10)
+    base = recall(index.search(Q, k=10, branches=branches)[0], truth, 10)
+    Qn = Q.copy()
+    Qn[5] = np.nan
+    ids, dist = index.search(Qn, k=10, branches=branches)
+    note("nan query", branches, "recall without/with", base)
+    assert (ids[5] == -1).all() and np.isinf(dist[5]).all()
+    keep = np.arange(len(Q)) != 5
+    assert ((ids[keep] >= 0) & (ids[keep] < len(X))).all()
+    assert np.isfinite(dist[keep]).all()
+    r = recall(ids[keep], truth[keep], 10)
+    note("nan query", branches, base, r)
+    assert r > 0.85 and abs(r - base) <= 0.05
+
+
 def test_unknown_option_is_a_type_error():
     X, Q = corpus(n=1000)
     index = swann.Index.build(X, degree=16, candidates=32)
