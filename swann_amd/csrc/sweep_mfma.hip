@@ -903,8 +903,23 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
     for (int j = 0; j < BJ; ++j) bro[j] = (wn * CW + j * 32 + (lane & 31)) * kRowBytes;
 
     // wave-uniform (the list entry is the same for every lane): the direct
-    // loads take the tile's base address in scalar registers
-    auto tile_at = [&](int k) { return tls ? __builtin_amdgcn_readfirstlane(tls[k]) : ct0 + k; };
+    // loads take the tile's base address in scalar registers.
+    // A full band of a symmetric launch (column tiles ct0 .. ct0 + bw - 1,
+    // one of each residue mod bw) is taken in residue order: step k scores
+    // the tile J == k (mod bw).  The workgroups an XCD runs together hold
+    // consecutive panels (sym_panel), so at every step they read one column
+    // panel, or two where the residue wraps, and all but the first find its
+    // lines in L2; in the order ct0 + k, neighbours read the same panel one
+    // tile apart, long after L2 has dropped it.  The lists do not depend on
+    // the order.
+    const int bw = a.sym ? (int)(a.b1 - a.b0) : 0;
+    const bool rot = a.sym && !tls && bw > 1 && ntl == bw;
+    const int cmod = rot ? ct0 % bw : 0;
+    auto tile_at = [&](int k) {
+        if (tls) return __builtin_amdgcn_readfirstlane(tls[k]);
+        if (rot) return ct0 + (k >= cmod ? k - cmod : k - cmod + bw);
+        return ct0 + k;
+    };
     int kt_c = 0, kt_f = 0, ki_c = 0, ki_f = 0;
     int cb_c = ntl > 0 ? tile_at(0) * kBN2 : 0, cb_f = cb_c;
     auto adv = [&](int& kt, int& ki, int& cb) {
