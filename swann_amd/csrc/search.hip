@@ -563,8 +563,11 @@ struct AdvArgs {
     int remap;                   // xcd_remap the blocks (a query's branches on one XCD)
 };
 
-template <int TEAM, typename XT, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
+// The advance of one branch a workgroup.  CODES: the sign-code pre-filter
+// runs (a.codes set); a template parameter, so that the plain search's kernel
+// carries none of the filter's registers.
+template <int TEAM, typename XT, int BLOCK, bool CODES>
+__device__ __forceinline__ void advance_body(const AdvArgs& a) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NT = BLOCK / TEAM;
     const int tid = threadIdx.x, team = tid / TEAM, tl = tid % TEAM;
@@ -582,7 +585,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     // the query's bit planes for the code estimate (code_planes words)
     const int nw32 = (a.dim + 31) >> 5;
     uint32_t* cpl = reinterpret_cast<uint32_t*>(sq + dimp);
-    int* qa_id = reinterpret_cast<int*>(cpl + (a.codes ? nw32 * kPlanes : 0));
+    int* qa_id = reinterpret_cast<int*>(cpl + (CODES ? nw32 * kPlanes : 0));
     float* qa_d = reinterpret_cast<float*>(qa_id + L);
     int* qb_id = reinterpret_cast<int*>(qa_d + L);
     float* qb_d = reinterpret_cast<float*>(qb_id + L);
@@ -631,7 +634,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
     if (tid == 0) { s_best_k = FLT_MAX; s_stall = 0; s_crowd_run = 0; }
     __syncthreads();
 
-    if (a.codes && wave == 0) {
+    if (CODES && wave == 0) {
         // <q, mu> and sum(q), once per call, in a fixed order that does not
         // depend on BLOCK: lane l sums t = l, l + 64, ..., then the wave folds
         // with off = 32 .. 1.  (The reference sums through shared-memory
@@ -693,7 +696,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             s_cdelta = (dl == dl && dl < INFINITY && cs == cs && cs < INFINITY) ? dl : INFINITY;
         }
     }
-    if (a.codes) __syncthreads();
+    if (CODES) __syncthreads();
 
     int r_evals = 0, r_fail = 0, r_hits = 0, r_claim = 0;
     const bool early = (a.stop_eps >= 0.f);
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
             if (taken) ++cov;
             else { c_id[nidx] = v; c_d[nidx] = d; c_l[nidx] = plin; }
         };
-        if (!a.codes) {
+        if (!CODES) {
             for (int w = team; w < nw; w += NT) {
                 const int v = w_v[w];
                 const float d = team_dist_m<TEAM, XT>(sq, X + (int64_t)v * a.dim, a.dim, tl,
@@ -985,6 +988,16 @@ __global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
         a.expd[qb + i] = qa_e[i]; a.lin[qb + i] = qa_l[i];
     }
     if (tid < kNctr) ctr[tid] = s_ctr[tid];
+}
+
+template <int TEAM, typename XT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void advance_kernel(AdvArgs a) {
+    advance_body<TEAM, XT, BLOCK, false>(a);
+}
+
+template <int TEAM, typename XT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void advance_codes_kernel(AdvArgs a) {
+    advance_body<TEAM, XT, BLOCK, true>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1196,16 +1209,24 @@ bool rows_vec_ok(const void* X, int dim, int x_dtype) {
 // Workgroups of one advance_kernel instance a CU holds at once (registers
 // and LDS), from the runtime's occupancy query; 0 if the query fails.
 template <int TEAM, typename XT>
-int advance_occupancy(int block, size_t lds) {
+int advance_occupancy(int block, size_t lds, bool codes) {
     int v = 0;
     hipError_t e;
     if (block == 64)
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 64>, 64, lds);
+        e = codes ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_codes_kernel<TEAM, XT, 64>, 64, lds)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_kernel<TEAM, XT, 64>, 64, lds);
     else if (block == 256)
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 256>, 256, lds);
+        e = codes ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_codes_kernel<TEAM, XT, 256>, 256, lds)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_kernel<TEAM, XT, 256>, 256, lds);
     else
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, advance_kernel<TEAM, XT, 1024>, 1024,
-                                                         lds);
+        e = codes ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_codes_kernel<TEAM, XT, 1024>, 1024, lds)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &v, advance_kernel<TEAM, XT, 1024>, 1024, lds);
     return e == hipSuccess ? v : 0;
 }
 
@@ -1217,7 +1238,7 @@ int advance_occupancy(int block, size_t lds) {
 // fell from 0.79 to 0.72 and 0.53), so the blocks keep their dispatch order
 // instead, which spreads a query's branches over the XCDs; the table's and
 // bound's atomics are agent scope and stay coherent across XCDs.
-bool remap_branches(int J, int team, int x_dtype, int block, size_t lds) {
+bool remap_branches(int J, int team, int x_dtype, int block, size_t lds, bool codes) {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
@@ -1227,16 +1248,16 @@ bool remap_branches(int J, int team, int x_dtype, int block, size_t lds) {
     int per_cu = 0;
     const bool f32 = x_dtype == SWANN_DTYPE_F32;
     switch (team) {
-        case 4: per_cu = f32 ? advance_occupancy<4, float>(block, lds)
-                             : advance_occupancy<4, _Float16>(block, lds); break;
-        case 8: per_cu = f32 ? advance_occupancy<8, float>(block, lds)
-                             : advance_occupancy<8, _Float16>(block, lds); break;
-        case 16: per_cu = f32 ? advance_occupancy<16, float>(block, lds)
-                              : advance_occupancy<16, _Float16>(block, lds); break;
-        case 32: per_cu = f32 ? advance_occupancy<32, float>(block, lds)
-                              : advance_occupancy<32, _Float16>(block, lds); break;
-        default: per_cu = f32 ? advance_occupancy<64, float>(block, lds)
-                              : advance_occupancy<64, _Float16>(block, lds); break;
+        case 4: per_cu = f32 ? advance_occupancy<4, float>(block, lds, codes)
+                             : advance_occupancy<4, _Float16>(block, lds, codes); break;
+        case 8: per_cu = f32 ? advance_occupancy<8, float>(block, lds, codes)
+                             : advance_occupancy<8, _Float16>(block, lds, codes); break;
+        case 16: per_cu = f32 ? advance_occupancy<16, float>(block, lds, codes)
+                              : advance_occupancy<16, _Float16>(block, lds, codes); break;
+        case 32: per_cu = f32 ? advance_occupancy<32, float>(block, lds, codes)
+                              : advance_occupancy<32, _Float16>(block, lds, codes); break;
+        default: per_cu = f32 ? advance_occupancy<64, float>(block, lds, codes)
+                              : advance_occupancy<64, _Float16>(block, lds, codes); break;
     }
     if (per_cu <= 0) (void)hipGetLastError();
     // Grouped only while a query's branches take at most a quarter of the
@@ -1382,9 +1403,13 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
               code_margin};
     const int block = search_block_for(nb);
     const size_t lds = advance_lds(dim, D, L, codes != nullptr);
-    a.remap = remap_branches(J, team_size, x_dtype, block, lds) ? 1 : 0;
-    SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
-                   lds, (hipStream_t)stream, a);
+    a.remap = remap_branches(J, team_size, x_dtype, block, lds, codes != nullptr) ? 1 : 0;
+    if (codes)
+        SWANN_DISPATCH(advance_codes_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
+                       lds, (hipStream_t)stream, a);
+    else
+        SWANN_DISPATCH(advance_kernel, team_size, x_dtype, block, dim3((unsigned)nb),
+                       lds, (hipStream_t)stream, a);
     return launch_status("advance");
 }
 
