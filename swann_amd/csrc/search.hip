@@ -249,17 +249,23 @@ constexpr int kPlaneOff = 1 << (kPlanes - 1);
 
 // Sum of k_i over the set bits of a lane's words (w = tl, tl + TEAM, ...)
 // folded over the team: exact integer arithmetic, the total in lane 0.
+// `head` holds the lane's first chunk (code_fetch(code, tl, nw32, ...)).
 template <int TEAM>
 __device__ __forceinline__ int team_code_k(const uint32_t* __restrict__ cpl,
-                                           const int32_t* __restrict__ code, int nw32, int dim,
-                                           int tl) {
+                                           const int32_t* __restrict__ code,
+                                           const unsigned* head, int nw32, int dim, int tl) {
     uint32_t cnt[kPlanes];
 #pragma unroll
     for (int b = 0; b < kPlanes; ++b) cnt[b] = 0u;
     uint32_t nb = 0u;
     for (int w0 = tl; w0 < nw32; w0 += kCodeWords * TEAM) {
         unsigned wb[kCodeWords];
-        code_fetch<TEAM>(code, w0, nw32, wb);
+        if (w0 == tl) {
+#pragma unroll
+            for (int j = 0; j < kCodeWords; ++j) wb[j] = head[j];
+        } else {
+            code_fetch<TEAM>(code, w0, nw32, wb);
+        }
 #pragma unroll
         for (int j = 0; j < kCodeWords; ++j) {
             const int w = w0 + j * TEAM;
@@ -846,16 +852,35 @@ __device__ __forceinline__ void advance_body(const AdvArgs& a) {
                 atomicAdd(&s_ctr[3], 1);
                 c_id[nidx] = v; c_d[nidx] = FLT_MAX; c_l[nidx] = plin;
             };
+            // An item's estimate waits on two loads, its code words and its
+            // scale; the next item's are issued before this one's estimate,
+            // so a team waits for them once an item, not twice, and behind
+            // the current item's arithmetic.
+            unsigned nxt[kCodeWords];
+            float nal = 0.f;
+            if (rad != FLT_MAX && team < nw) {
+                const int v0 = w_v[team];
+                code_fetch<TEAM>(a.codes + (int64_t)v0 * a.cwords, tl, nw32, nxt);
+                nal = a.calpha[v0];
+            }
             for (int w = team; w < nw; w += NT) {
                 const int v = w_v[w];
                 if (rad == FLT_MAX) {            // no line yet: nothing is skipped
                     if (tl == 0) u_id[atomicAdd(&s_npass, 1)] = w;
                     continue;
                 }
-                const int kt = team_code_k<TEAM>(cpl, a.codes + (int64_t)v * a.cwords, nw32,
-                                                 a.dim, tl);
+                unsigned cur[kCodeWords];
+#pragma unroll
+                for (int j = 0; j < kCodeWords; ++j) cur[j] = nxt[j];
+                const float al = nal;
+                if (w + NT < nw) {
+                    const int vn = w_v[w + NT];
+                    code_fetch<TEAM>(a.codes + (int64_t)vn * a.cwords, tl, nw32, nxt);
+                    nal = a.calpha[vn];
+                }
+                const int kt = team_code_k<TEAM>(cpl, a.codes + (int64_t)v * a.cwords, cur,
+                                                 nw32, a.dim, tl);
                 if (tl == 0) {
-                    const float al = a.calpha[v];
                     const float sc = s_cscale * (float)kt;
                     const float dl = s_cdelta + 1e-6f * (fabsf(sc) + s_cdelta) + 1e-30f;
                     auto est = [&](float sum) { return 1.f - (al * (2.f * sum - s_qsum) + s_qmu); };
