@@ -672,6 +672,30 @@ def test_select_small_and_large_batches_match_oracle(nq, metric):
             assert idx[0, 0] == 7 and idx[0, 1] == P // 2 + 7
 
 
+@pytest.mark.parametrize("nq", [1, 5, 70])
+def test_select_tiny_catalogues_match_oracle(nq):
+    """Catalogues of 1 to 17 rows (the one-pass product's last workgroup
+    mostly past P, the top-E over rows shorter than a wave) and E up to P:
+    the same entries as the oracle, up to ties."""
+    rng = np.random.default_rng(700 + nq)
+    for P, d, E in ((1, 16, 1), (3, 20, 3), (17, 64, 5), (17, 7, 17)):
+        V = rng.standard_normal((P, d)).astype(np.float32)
+        Q = rng.standard_normal((nq, d)).astype(np.float32)
+        for metric in (0, 1):
+            idx = S.select_nearest(torch.from_numpy(Q).cuda(), torch.from_numpy(V).cuda(), E,
+                                   metric=metric).cpu().numpy()
+            want, _ = O.select_nearest(Q, V, E, metric, nthreads=8)
+            assert idx.shape == (nq, E)
+            Q64, V64 = Q.astype(np.float64), V.astype(np.float64)
+            if metric == 0:
+                dist = lambda e: 1.0 - np.einsum("qd,qkd->qk", Q64, V64[e])  # noqa: E731
+            else:
+                dist = lambda e: ((V64[e] - Q64[:, None, :]) ** 2).sum(-1)  # noqa: E731
+            wd = dist(want)
+            same_lists(f"tiny select {nq} {metric} {P} {d} {E}", idx, dist(idx), want, wd,
+                       2e-6 * max(float(np.abs(wd).max()), 1.0), 2e-5)
+
+
 @pytest.mark.parametrize("tag,metric", [("ip", 0), ("l2", 1)])
 def test_prune_per_node_degree_and_protect_match_reference(tag, metric):
     """robust_prune(deg_per_node=, protect=) and add_reverse(deg_per_node=)
