@@ -65,7 +65,7 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # claims layout (Index._claims: "bits<n>" or the table's slots); otherwise `traffic`
 # is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "bits1048576", "665b10b749f2945d"): 4.860e12,
+    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "bits1048576", "ebf85ab938dc0030"): 4.860e12,
 }
 
 

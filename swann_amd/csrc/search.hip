@@ -1186,13 +1186,15 @@ int search_block_for(int64_t nbranch) {
     // to run every layout on the same inputs)
     const int forced = option(kOptSearchBlock);
     if (forced == 64 || forced == 256 || forced == 1024) return forced;
-    // Batch work fills 256 CUs with one-wave branches.  A batch that cannot
-    // gets four waves per branch, and a grid smaller than two branches per
-    // CU (batch 1-8 at 32 branches) sixteen: an expansion's neighbours are
-    // then scored by 1024 / team teams at once instead of a few in turn, and
-    // a branch's chain of expansions -- the latency at small batch -- is
-    // shorter.
-    if (nbranch >= 4096) return 64;
+    // Batch work fills 256 CUs with one-wave branches.  A smaller batch gets
+    // four waves per branch, and a grid smaller than two branches per CU
+    // (batch 1-8 at 32 branches) sixteen: an expansion's neighbours are then
+    // scored by BLOCK / team teams at once instead of a few in turn, and a
+    // branch's chain of expansions -- the latency at small batch -- is
+    // shorter.  Four waves still beat one at 8,192 and 16,384 branches (C4,
+    // team 32: 11.8 against 12.3 ms, 23.3 against 24.4 ms, the same
+    // recall); one wave wins again at 65,536.
+    if (nbranch >= 32768) return 64;
     return nbranch >= 512 ? 256 : 1024;
 }
 
