@@ -23,6 +23,12 @@ def select_nearest(Qg, Vp, E, metric=METRIC_IP, precision="fp32", slice_P=8192, 
     (swann/_select.py:93-128).  `precision` and `slice_P` are accepted for
     interface compatibility; the GPU kernel is fp32 and unsliced."""
     del precision, slice_P
+    return select_nearest_i32(Qg, Vp, E, metric, workspace).long()
+
+
+def select_nearest_i32(Qg, Vp, E, metric=METRIC_IP, workspace=None):
+    """select_nearest's entries as the kernel writes them, int32 [n, min(E, P)]
+    (the search maps them to seeds without a widening copy)."""
     if not (Qg.is_cuda and Vp.is_cuda):
         raise RuntimeError("select_nearest: queries and catalogue must be on the GPU")
     Qg = Qg.float().contiguous()
@@ -31,14 +37,14 @@ def select_nearest(Qg, Vp, E, metric=METRIC_IP, precision="fp32", slice_P=8192, 
     E = min(int(E), P)
     out = torch.empty((n, E), dtype=torch.int32, device=Qg.device)
     if n == 0:
-        return out.long()
+        return out
     need = int(_ws_size(n, P))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=Qg.device)
     with torch.cuda.device(Qg.device):
         call("swann_select_nearest", ptr(Qg), n, Qg.shape[1], ptr(Vp), P, E, int(metric),
              ptr(out), None, ptr(workspace), stream_of(Qg.device))
-    return out.long()
+    return out
 
 
 def _ws_size(n, P):

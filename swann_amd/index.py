@@ -74,6 +74,7 @@ class Index:
             catalogue = torch.from_numpy(pick.astype(np.int64)).to(self.X.device)
         self.catalogue = catalogue.to(device=self.X.device, dtype=torch.int64)
         self._cat = S.pool_vectors(self.X, self.catalogue)
+        self._cat_ids = self.catalogue.to(torch.int32)     # seeds are int32 row ids
         self._flag = None
 
     # -- construction ----------------------------------------------------
@@ -103,8 +104,8 @@ class Index:
         """select -> seeds -> init -> advance -> top-k -> merge -> overflow,
         all stream-ordered device work with no host synchronisation (so it can
         be captured)."""
-        entries = S.select_nearest(Q, self._cat, cfg.branches, metric=self._m)
-        seeds = self.catalogue[entries].to(torch.int32)
+        entries = S.select_nearest_i32(Q, self._cat, cfg.branches, metric=self._m)
+        seeds = torch.index_select(self._cat_ids, 0, entries.view(-1)).view(entries.shape)
         bits, slots = self._claims(Q.shape[0], cfg)
         ids, dist, st = E.search(
             self.X, self.G, Q, seeds, k=k, L=cfg.queue, B=cfg.budget, metric=self._m,
