@@ -201,13 +201,17 @@ struct MfmaSweepArgs {
     const int* plist;
     int npl;
     // the pruned ordered sweep: workgroup (panel) I scores only the column
-    // tiles tlist[I * kBandMax + k], k < tcnt[I] (ascending, inside its band)
+    // tiles tlist[I * kBandMax + k], k < tcnt[I] (ascending, inside its band);
+    // a one-sided launch over listed panels (the bounded repair): panel
+    // plist[p] scores only tlist[p * tstride + k], k < tcnt[p], ascending,
+    // which its G workgroups share out in order
     const int* tlist;
     const int* tcnt;
     // symmetric sweep: each row's list-0 count as the last merge left it; a
     // launch that compacts a row's list sets it to -1, so that the next merge
     // cannot take the row for unchanged (sym_merge)
     int* mcnt;
+    int tstride;                 // the bounded repair's list stride (tiles a panel)
 };
 
 // Wave-cooperative compaction of one row's buffer to its C best (exact:
@@ -861,10 +865,21 @@ __global__ __launch_bounds__(WAVES * 64, 1) void sweep_dma_kernel(MfmaSweepArgs 
         ct0 = lid + (int)a.b0;
         ct1 = lid + a.b1 < nct ? lid + (int)a.b1 : nct;
     }
-    // with a tile list (the pruned ordered sweep) the column tiles are a
-    // subset of [ct0, ct1), in order; lid is the panel in a symmetric launch
-    const int* tls = (a.sym && a.tlist) ? a.tlist + (int64_t)lid * kBandMax : nullptr;
-    const int ntl = tls ? a.tcnt[lid] : ct1 - ct0;
+    // with a tile list the column tiles are a listed subset, in order: in a
+    // symmetric launch (the pruned ordered sweep) panel lid's, inside its
+    // band; in a one-sided launch over listed panels (the bounded repair)
+    // this workgroup's share of panel plist[lid / G]'s list
+    const int* tls = nullptr;
+    int ntl = ct1 - ct0;
+    if (a.tlist && a.sym) {
+        tls = a.tlist + (int64_t)lid * kBandMax;
+        ntl = a.tcnt[lid];
+    } else if (a.tlist && a.plist) {
+        const int p = lid / G, m = a.tcnt[p];
+        const int k0 = (int)((int64_t)m * split / G), k1 = (int)((int64_t)m * (split + 1) / G);
+        tls = a.tlist + (int64_t)p * a.tstride + k0;
+        ntl = k1 - k0;
+    }
     const int nsteps = ntl * nk;
     const _Float16* X = a.hi;
 
@@ -1731,6 +1746,170 @@ __global__ __launch_bounds__(64) void dense_keep(const unsigned* __restrict__ tl
     }
 }
 
+// The bounded repair of a repaired panel D = plist[p]: each of its rows
+// against every panel group, the bound of group_bounds with the row as a
+// group of one (radius 0; its norm, centre norm and norm deviation its own),
+// so that a tile J is swept again only when some row r of D may have a pair
+// there no farther than its threshold gthr[r] as the last merge left it (an
+// upper bound of r's C-th listed distance, +inf while r holds fewer).  A
+// tile left out holds no pair closer than its row's C-th, so the one-sided
+// sweep over the rest rebuilds D's lists exactly.
+//
+// Row stats as panel_stats takes them for a group: the row's plane values
+// v = scale * plane in double, N = |v| (1 + 1e-6), Dv = |xn - |v|^2| (1 +
+// 1e-6) + 1e-30.  rst[2 (p * 256 + i) + {0, 1}].
+__global__ __launch_bounds__(256) void repair_row_stats(const _Float16* __restrict__ hp,
+                                                        const float* __restrict__ scp,
+                                                        const float* __restrict__ xnp,
+                                                        const int* __restrict__ plist, int64_t n,
+                                                        int dim, int scaled,
+                                                        double* __restrict__ rst) {
+    const int p = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)plist[p] * kBM2;
+    for (int i = w; i < kBM2; i += 4) {
+        const int64_t r = r0 + i;
+        if (r >= n) {
+            if (lane == 0) { rst[2 * ((int64_t)p * kBM2 + i)] = 0.0; rst[2 * ((int64_t)p * kBM2 + i) + 1] = 0.0; }
+            continue;
+        }
+        const float sc = scaled ? scp[r] : 1.f;
+        double v2 = 0.0;
+        for (int t = lane; t < dim; t += 64) {
+            const double v = (double)(sc * (float)hp[r * dim + t]);
+            v2 += v * v;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v2 += __shfl_xor(v2, off, 64);
+        if (lane == 0) {
+            const double up = 1.0 + 1e-6;
+            rst[2 * ((int64_t)p * kBM2 + i)] = sqrt(v2) * up;
+            rst[2 * ((int64_t)p * kBM2 + i) + 1] = fabs((double)xnp[r] - v2) * up + 1e-30;
+        }
+    }
+}
+
+// need[p * ntile + J] = 1 when some row of D = plist[p] may need tile J.
+// Grid (groups / 64, 4 row quarters of D, np): 64 rows x 64 groups a
+// workgroup, their distances (l2) or products (ip) in double as in
+// group_bounds.
+__global__ __launch_bounds__(256) void repair_need(const _Float16* __restrict__ hp,
+                                                   const float* __restrict__ scp,
+                                                   const float* __restrict__ cen,
+                                                   const float* __restrict__ pst,
+                                                   const int* __restrict__ glist, int G,
+                                                   const float* __restrict__ gthr,
+                                                   const int* __restrict__ plist,
+                                                   const double* __restrict__ rst, int64_t n,
+                                                   int ntile, int dim, int metric, int scaled,
+                                                   int* __restrict__ need) {
+    const int bj = blockIdx.x, rq = blockIdx.y, p = blockIdx.z;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int64_t r0 = (int64_t)plist[p] * kBM2 + rq * kGB;
+    __shared__ double sa[kGK][kGB + 1];
+    __shared__ double sb[kGK][kGB + 1];
+    __shared__ int slot_b[kGB];
+    __shared__ float rsc[kGB];
+    if (tid < kGB) {
+        const int gb = bj * kGB + tid;
+        slot_b[tid] = gb < G ? glist[gb] : -1;
+        const int64_t r = r0 + tid;
+        rsc[tid] = r < n ? (scaled ? scp[r] : 1.f) : 0.f;
+    }
+    __syncthreads();
+    const bool l2 = metric == SWANN_METRIC_L2;
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    for (int k0 = 0; k0 < dim; k0 += kGK) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = e * 256 + tid;
+            const int gr = idx >> 4, kk = idx & 15;
+            const int k = k0 + kk;
+            const int64_t r = r0 + gr;
+            const int sb_ = slot_b[gr];
+            sa[kk][gr] = (r < n && k < dim) ? (double)(rsc[gr] * (float)hp[r * dim + k]) : 0.0;
+            sb[kk][gr] = (sb_ >= 0 && k < dim) ? (double)cen[(int64_t)sb_ * dim + k] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kGK; ++kk) {
+            double x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = sa[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = sb[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (l2) {
+                        const double d = x[i] - y[j];
+                        acc[i][j] = __builtin_fma(d, d, acc[i][j]);
+                    } else {
+                        acc[i][j] = __builtin_fma(x[i], y[j], acc[i][j]);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+    const double g = ((double)dim + 64.0) * 0x1p-23;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rl = rq * kGB + ty * 4 + i;
+        const int64_t r = (int64_t)plist[p] * kBM2 + rl;
+        if (r >= n) continue;
+        const double NI = rst[2 * ((int64_t)p * kBM2 + rl)];
+        const double DI = rst[2 * ((int64_t)p * kBM2 + rl) + 1];
+        const double th = (double)gthr[r];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int jb = slot_b[tx * 4 + j];
+            if (jb < 0) continue;
+            const double RJ = pst[4 * jb], NJ = pst[4 * jb + 1], DJ = pst[4 * jb + 2],
+                         CJ = pst[4 * jb + 3];
+            double lb;
+            if (l2) {
+                const double gap = sqrt(acc[i][j]) * (1.0 - 1e-9) - RJ;
+                lb = (gap > 0.0 ? gap * gap : 0.0) - DI - DJ - 2.0 * g * NI * NJ -
+                     0x1p-21 * 1.1 * (NI + NJ) * (NI + NJ);
+            } else {
+                lb = 1.0 - (acc[i][j] + 1e-9 * NI * CJ + RJ * NI) - g * NI * NJ -
+                     0x1p-22 * (1.0 + NI * NJ);
+            }
+            // a NaN bound or threshold keeps the tile
+            if (!(lb > th)) need[(int64_t)p * ntile + jb / kSegs] = 1;
+        }
+    }
+}
+
+// The bounded repair's lists: for repaired panel D = plist[p], D itself and
+// the tiles need marks, ascending, in tlist[p * ntile ..]; their number in
+// tcnt[p], the total added to *tsum.  One wave a panel.
+__global__ __launch_bounds__(64) void repair_list(const int* __restrict__ need,
+                                                  const int* __restrict__ plist, int ntile,
+                                                  int* __restrict__ tlist,
+                                                  int* __restrict__ tcnt,
+                                                  unsigned long long* __restrict__ tsum) {
+    const int p = blockIdx.x, lane = threadIdx.x;
+    const int D = plist[p];
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int base = 0;
+    for (int J0 = 0; J0 < ntile; J0 += 64) {
+        const int J = J0 + lane;
+        const bool k = J < ntile && (J == D || need[(int64_t)p * ntile + J] != 0);
+        const uint64_t m = __ballot(k);
+        if (k) tlist[(int64_t)p * ntile + base + __popcll(m & below)] = J;
+        base += __popcll(m);
+    }
+    if (lane == 0) {
+        tcnt[p] = base;
+        atomicAdd(tsum, (unsigned long long)base);
+    }
+}
+
 __global__ __launch_bounds__(256) void sym_init(float* __restrict__ gthr,
                                                 int32_t* __restrict__ bcnt, int* ovf,
                                                 int64_t n, const float* __restrict__ seed,
@@ -2197,6 +2376,14 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
             int* tlist = nullptr;
             int* tcnt = nullptr;
             unsigned long long* tsum = nullptr;
+            // the ordered plane and its groups, kept for the bounded repair
+            const _Float16* rhp = nullptr;
+            const float* rscp = nullptr;
+            const float* rcen = nullptr;
+            const float* rpst = nullptr;
+            const float* rxnp = nullptr;
+            const int* rglist = nullptr;
+            int rng = 0;
             int64_t host_tiles = 0;      // tiles of the launches not pruned
             // the launches of bands [b0, bend), each followed by a merge;
             // with `prune`, each launch scores only the tiles tile_keep keeps
@@ -2417,6 +2604,13 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                                        (const float*)cen, (const float*)pst, (const int*)glist, ng,
                                        (int)ntile, dim, metric, tb);
                     tlb = tb;
+                    rhp = hp;
+                    rscp = scp;
+                    rxnp = xnp;
+                    rcen = cen;
+                    rpst = pst;
+                    rglist = glist;
+                    rng = ng;
                     hipLaunchKernelGGL(fill_zero, dim3((unsigned)((ntile + 256) / 256)), dim3(256), 0,
                                        st, dn, (int)ntile + 1);
                     hipLaunchKernelGGL(dense_mark, dim3((unsigned)ntile), dim3(256), 0, st, tlb,
@@ -2529,6 +2723,46 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     return SWANN_E_LAUNCH;
                 }
                 SWANN_REQUIRE(np >= 1 && np <= ntile, "sweep: repair panel count out of range");
+                // With the pruned sweep's groups, a repaired panel sweeps only
+                // the tiles some row of it can still need, each row against
+                // every group at its own threshold (repair_need).  The marks,
+                // the rows' stats and the lists take the bands' list space.
+                const int* rlist = nullptr;
+                const int* rlcnt = nullptr;
+                int64_t rtiles = (int64_t)np * ntile;
+                const int64_t rspace = 2 * (int64_t)np * ntile + 4 * (int64_t)np * kBM2;
+                if (tlb && rcen && rng > 0 && rspace <= ntile * kBandMax) {
+                    int* rneed = tlist + (int64_t)np * ntile;
+                    double* rst = (double*)(tlist + 2 * (int64_t)np * ntile);
+                    hipLaunchKernelGGL(fill_u32, dim3((unsigned)((np * ntile + 255) / 256)),
+                                       dim3(256), 0, st, (unsigned*)rneed, (int64_t)np * ntile, 0u);
+                    hipLaunchKernelGGL(repair_row_stats, dim3((unsigned)np), dim3(256), 0, st, rhp,
+                                       rscp, rxnp, (const int*)plist, n, dim, scaled, rst);
+                    hipLaunchKernelGGL(repair_need,
+                                       dim3((unsigned)((rng + kGB - 1) / kGB), kBM2 / kGB,
+                                            (unsigned)np),
+                                       dim3(256), 0, st, rhp, rscp, rcen, rpst, rglist, rng,
+                                       (const float*)gthr, (const int*)plist,
+                                       (const double*)rst, n, (int)ntile, dim, metric, scaled,
+                                       rneed);
+                    hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, (int*)tsum, 2);
+                    hipLaunchKernelGGL(repair_list, dim3((unsigned)np), dim3(64), 0, st,
+                                       (const int*)rneed, (const int*)plist, (int)ntile, tlist,
+                                       tcnt, tsum);
+                    unsigned long long rt = 0;
+                    if (hipMemcpyAsync(&rt, tsum, sizeof(rt), hipMemcpyDeviceToHost, st) !=
+                            hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess) {
+                        set_error("sweep (mfma, symmetric): reading the repair tile count failed");
+                        return SWANN_E_LAUNCH;
+                    }
+                    SWANN_REQUIRE(rt >= (unsigned long long)np &&
+                                      rt <= (unsigned long long)np * (unsigned long long)ntile,
+                                  "sweep: repair tile count out of range");
+                    rtiles = (int64_t)rt;
+                    rlist = tlist;
+                    rlcnt = tcnt;
+                }
                 // panels repaired one at a time, 16 ways (option sweep_repair_max)
                 const int rmax = option(kOptSweepRepairMax);
                 if (np <= rmax && C * kRepairSplits <= kRepairSort) {
@@ -2539,7 +2773,7 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         set_error("sweep (mfma, symmetric): reading the repair panels failed");
                         return SWANN_E_LAUNCH;
                     }
-                    g_tiles_scored += (int64_t)np * ntile;
+                    g_tiles_scored += rtiles;
                     for (int i = 0; i < np; ++i) {
                         SWANN_REQUIRE(ph[i] >= 0 && ph[i] < ntile, "sweep: repair panel out of range");
                         // the one-sided sweep of panel ph[i] into the scratch:
@@ -2552,6 +2786,9 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                         rep.splits = kRepairSplits;
                         rep.plist = plist + i;
                         rep.npl = 1;
+                        rep.tlist = rlist ? rlist + (int64_t)i * ntile : nullptr;
+                        rep.tcnt = rlist ? rlcnt + i : nullptr;
+                        rep.tstride = (int)ntile;
                         rep.bkey = rkey - rb * kRepairSplits * cap;
                         rep.bid = rid - rb * kRepairSplits * cap;
                         rep.bcnt = rcnt - rb * kRepairSplits;
@@ -2574,12 +2811,15 @@ int sweep_mfma_run(const void* X, int x_dtype, int64_t n, int dim, int metric, i
                     *perm_out = ordered;
                     return SWANN_OK;
                 }
-                g_tiles_scored += (int64_t)np * ntile;
+                g_tiles_scored += rtiles;
                 MfmaSweepArgs rep = s;
                 rep.sym = 0;
                 rep.splits = 2;
                 rep.plist = plist;
                 rep.npl = np;
+                rep.tlist = rlist;
+                rep.tcnt = rlcnt;
+                rep.tstride = (int)ntile;
                 const unsigned rg = (unsigned)(np * 2);
                 if (scaled) {
                     if (ip) hipLaunchKernelGGL((sweep_dma_kernel<SWANN_METRIC_IP, 1, 16>), dim3(rg), dim3(1024), 0, st, rep);
