@@ -65,7 +65,7 @@ MFMA_F16_PEAK = 2.5e15              # dense fp16/bf16 MFMA, MI355X
 # claims layout (Index._claims: "bits<n>" or the table's slots); otherwise `traffic`
 # is reported as null.
 PMC_TRAFFIC = {
-    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "bits1048576", "ebf85ab938dc0030"): 4.860e12,
+    ("c3", 1_000_000, 10_000, 64, 44, 64, 0.3, "bits1048576", "86f5d362e82538e5"): 4.860e12,
 }
 
 
@@ -270,8 +270,9 @@ class Searcher:
                                      ix._claims(self.Q.shape[0], knobs))
         if record:
             ev[0].record()
-        ent = S.select_nearest(self.Q, ix._cat, cfg["branches"], metric=ix._m, workspace=self.ws)
-        seeds = ix.catalogue[ent].to(torch.int32)
+        ent = S.select_nearest_i32(self.Q, ix._cat, cfg["branches"], metric=ix._m,
+                                   workspace=self.ws)
+        seeds = torch.index_select(ix._cat_ids, 0, ent.view(-1)).view(ent.shape)
         if record:
             ev[1].record()
         st = E.init_states(ix.X, self.Q, seeds, L=cfg["queue"], B=cfg["budget"], D=ix.G.shape[1],
@@ -284,8 +285,7 @@ class Searcher:
         E.advance(ix.X, ix.G, self.Q, st, cfg["budget"], codes=self.codes)
         if record:
             ev[3].record()
-        bi, bd = E.branch_topk(st, self.k)
-        ids, dist = E.merge_branches(bi, bd, self.k)
+        ids, dist = E.merge_state(st, self.k)
         if record:
             ev[4].record()
         return ids, dist, st

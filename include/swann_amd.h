@@ -13,6 +13,7 @@
  *   swann_init_states      swann/csrc/local_search.cu:741-776  (pybind init_states)
  *   swann_advance          swann/csrc/local_search.cu:778-841  (pybind advance)
  *   swann_merge_branches   swann/csrc/local_search.cu:925-947  (pybind merge_branches)
+ *   swann_merge_branches_strided  swann/_engine.py:340-374  (branch_topk, then merge_branches)
  *   swann_select_nearest   swann/_select.py:93-128             (select_nearest)
  *   swann_build_sweep      swann/build.py:28-43                (knn_candidates)
  *   swann_build_prune      swann/build.py:46-91                (robust_prune)
@@ -202,6 +203,14 @@ int swann_enforce_min_in(int32_t* G, int64_t n, int W, const int32_t* cand, int 
  * are (-1, +inf).  Any V*kk (no shared-memory limit). */
 int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk,
                          int k, int32_t* out_ids, float* out_dist, void* stream);
+
+/* swann_merge_branches over the first kk slots of rows of ld >= kk slots:
+ * bids/bdist [Q, V, ld], e.g. a search state's sorted queues, read in place
+ * of the [Q, V, kk] copy that branch_topk makes (_engine.py:340-355).  Same
+ * output; ld == kk is swann_merge_branches itself. */
+int swann_merge_branches_strided(const int32_t* bids, const float* bdist, int64_t Q, int V,
+                                 int kk, int64_t ld, int k, int32_t* out_ids, float* out_dist,
+                                 void* stream);
 
 /* Sum of counters[..., 2] (visited-table overflows) over nbranch branches,
  * written to *out (device or host-pinned memory) without a host sync. */

@@ -347,6 +347,29 @@ def merge_branches(ids: torch.Tensor, dist: torch.Tensor, k: int, fused: bool = 
     return oi, od
 
 
+def merge_state(state: SearchState, k: int):
+    """branch_topk then merge_branches in one launch (swann/_engine.py:340-374):
+    the merge reads each branch's first min(k, L) slots straight from the
+    state's sorted queues, so no [Q, J, kk] copy is made.  Same output as
+    merge_branches(*branch_topk(state, k), k)."""
+    Q, J, L = state.ids.shape
+    kk = min(k, L)
+    if not (1 <= k <= J * kk):
+        raise RuntimeError(f"merge_state: k must be in 1..{J * kk}, got {k}")
+    if not (state.ids.is_cuda and state.dist.is_cuda and state.ids.dtype == torch.int32
+            and state.dist.dtype == torch.float32 and tuple(state.dist.shape) == (Q, J, L)):
+        raise RuntimeError("merge_state: the queues must be cuda int32 ids and float32 "
+                           "distances of one shape [Q, J, L]")
+    if not (state.ids.is_contiguous() and state.dist.is_contiguous()):
+        raise RuntimeError("merge_state: the state's queues must be contiguous")
+    oi = torch.empty((Q, k), dtype=torch.int32, device=state.ids.device)
+    od = torch.empty((Q, k), dtype=torch.float32, device=state.ids.device)
+    with torch.cuda.device(state.ids.device):
+        call("swann_merge_branches_strided", ptr(state.ids), ptr(state.dist), Q, J, kk, L,
+             int(k), ptr(oi), ptr(od), stream_of(state.ids.device))
+    return oi, od
+
+
 def _live_branches(state: SearchState) -> torch.Tensor:
     """Flattened indices q*J + j (int32, on the state's device) of the branches
     that still have an unexpanded candidate and budget left."""
@@ -390,8 +413,7 @@ def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
         advance(X, G, Qv, st, B, codes=codes)
     if _OVERFLOW_GUARD if check is None else check:
         st.check()
-    bi, bd = branch_topk(st, k)
-    ids, dist = merge_branches(bi, bd, k)
+    ids, dist = merge_state(st, k)
     return ids, dist, st
 
 

@@ -34,6 +34,7 @@ PROTOTYPES = {
                           I, I, I, I, I, I, F, I, P, P, I, P, I, I, F, P, I64,
                           P, I, P, P, F, P]),
     "swann_merge_branches": (I, [P, P, I64, I, I, I, P, P, P]),
+    "swann_merge_branches_strided": (I, [P, P, I64, I, I, I64, I, P, P, P]),
     "swann_overflow_async": (I, [P, I64, P, P]),
     "swann_select_workspace_size": (I64, [I64, I64]),
     "swann_select_nearest": (I, [P, I64, I, P, I64, I, I, P, P, P, P]),

@@ -1074,21 +1074,38 @@ __device__ __forceinline__ bool merge_visit(uint64_t m, int& prev_id, int& w, ui
     return true;
 }
 
+// Branch results sit in rows of `ld` slots, `kk` of them used: entry i of a
+// query (i < V*kk) is branch i / kk, slot i % kk.  A thread walks its entries
+// t, t + S, t + 2S, ... by carrying (branch, slot) and adding (S / kk, S % kk).
+struct MergeWalk {
+    int64_t v, j;
+    __device__ MergeWalk(int64_t i, int kk) : v(i / kk), j(i % kk) {}
+    __device__ __forceinline__ int64_t at(int64_t ld) const { return v * ld + j; }
+    __device__ __forceinline__ void step(int64_t sv, int sj, int kk) {
+        v += sv;
+        j += sj;
+        if (j >= kk) { j -= kk; ++v; }
+    }
+};
+
 // n <= 64*R: one wave per query, R keys per lane in registers.
 template <int R>
 __global__ __launch_bounds__(64) void merge_wave_kernel(const int32_t* __restrict__ bids,
                                                         const float* __restrict__ bdist,
                                                         int32_t* __restrict__ oi,
                                                         float* __restrict__ od, int64_t q0,
-                                                        int n, int k) {
+                                                        int n, int kk, int64_t ld, int k) {
     const int64_t q = q0 + blockIdx.x;
     const int lane = threadIdx.x;
-    const int64_t base = q * (int64_t)n;
+    const int64_t base = q * (int64_t)(n / kk) * ld;
     uint64_t key[R];
+    MergeWalk at(lane, kk);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int i = lane + 64 * r;
-        key[r] = i < n ? merge_key(bids[base + i], bdist[base + i]) : ~0ull;
+        const int64_t a = base + at.at(ld);
+        key[r] = i < n ? merge_key(bids[a], bdist[a]) : ~0ull;
+        at.step(64 / kk, 64 % kk, kk);
     }
     const int64_t row = q * (int64_t)k;
     uint64_t lo = 0;
@@ -1108,19 +1125,22 @@ __global__ __launch_bounds__(64) void merge_wave_kernel(const int32_t* __restric
 // minima meet in LDS, double-buffered so one barrier per step suffices.
 __global__ __launch_bounds__(kMergeBlockThreads) void merge_block_kernel(
     const int32_t* __restrict__ bids, const float* __restrict__ bdist, int32_t* __restrict__ oi,
-    float* __restrict__ od, int64_t q0, int64_t n, int k) {
+    float* __restrict__ od, int64_t q0, int64_t n, int kk, int64_t ld, int k) {
     constexpr int kWaves = kMergeBlockThreads / 64;
     __shared__ uint64_t part[2][kWaves];
     const int64_t q = q0 + blockIdx.x;
-    const int64_t base = q * n;
+    const int64_t base = q * (n / kk) * ld;
     const int64_t row = q * (int64_t)k;
     uint64_t lo = 0;
     int prev_id = -1, w = 0;
     for (int64_t step = 0; step < n && w < k; ++step) {
         uint64_t m = ~0ull;
+        MergeWalk at(threadIdx.x, kk);
         for (int64_t i = threadIdx.x; i < n; i += kMergeBlockThreads) {
-            const uint64_t x = merge_key(bids[base + i], bdist[base + i]);
+            const int64_t a = base + at.at(ld);
+            const uint64_t x = merge_key(bids[a], bdist[a]);
             m = x >= lo ? umin64(m, x) : m;
+            at.step(kMergeBlockThreads / kk, kMergeBlockThreads % kk, kk);
         }
         m = wave_min_u64(m);
         if ((threadIdx.x & 63) == 0) part[step & 1][threadIdx.x >> 6] = m;
@@ -1440,10 +1460,12 @@ int swann_advance(const void* X, int x_dtype, int64_t n, int dim, const int32_t*
     return launch_status("advance");
 }
 
-int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk, int k,
-                         int32_t* out_ids, float* out_dist, void* stream) {
+int swann_merge_branches_strided(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk,
+                                 int64_t ld, int k, int32_t* out_ids, float* out_dist,
+                                 void* stream) {
     clear_error();
     SWANN_REQUIRE(V >= 1 && kk >= 1, "expected (Q, V, kk) branch results with V, kk >= 1");
+    SWANN_REQUIRE(ld >= kk, "row stride ld must be >= kk");
     const int64_t n = (int64_t)V * kk;
     SWANN_REQUIRE(k > 0 && k <= n, "k must be in 1..V*kk");
     SWANN_REQUIRE(Q >= 0, "Q out of range");
@@ -1459,30 +1481,35 @@ int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int
             const int ni = (int)n;
             if (r <= 1)
                 hipLaunchKernelGGL(merge_wave_kernel<1>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
             else if (r <= 2)
                 hipLaunchKernelGGL(merge_wave_kernel<2>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
             else if (r <= 4)
                 hipLaunchKernelGGL(merge_wave_kernel<4>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
             else if (r <= 8)
                 hipLaunchKernelGGL(merge_wave_kernel<8>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
             else if (r <= 16)
                 hipLaunchKernelGGL(merge_wave_kernel<16>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
             else
                 hipLaunchKernelGGL(merge_wave_kernel<32>, dim3(nq), dim3(64), 0, st, bids, bdist,
-                                   out_ids, out_dist, q0, ni, k);
+                                   out_ids, out_dist, q0, ni, kk, ld, k);
         } else {
             hipLaunchKernelGGL(merge_block_kernel, dim3(nq), dim3(kMergeBlockThreads), 0, st, bids,
-                               bdist, out_ids, out_dist, q0, n, k);
+                               bdist, out_ids, out_dist, q0, n, kk, ld, k);
         }
         const int rc = launch_status("merge_branches");
         if (rc) return rc;
     }
     return SWANN_OK;
+}
+
+int swann_merge_branches(const int32_t* bids, const float* bdist, int64_t Q, int V, int kk, int k,
+                         int32_t* out_ids, float* out_dist, void* stream) {
+    return swann_merge_branches_strided(bids, bdist, Q, V, kk, kk, k, out_ids, out_dist, stream);
 }
 
 int swann_overflow_async(const int32_t* counters, int64_t nbranch, int32_t* out, void* stream) {

@@ -215,6 +215,31 @@ def test_merge_dedup_matches_oracle():
         assert gd.cpu().numpy().tobytes() == wd.tobytes(), (Q, V, kk, k)
 
 
+def test_merge_reads_queues_in_place():
+    """merge_state reads the first min(k, L) slots of each branch's L-slot
+    queue where they lie; against the oracle's merge of the [Q, V, kk] copy
+    that branch_topk would make, bit for bit.  Slot counts that do and do not
+    divide a wave (64) or a workgroup (1024), both kernel shapes, k above L."""
+    from types import SimpleNamespace
+    rng = np.random.default_rng(41)
+    for Q, V, L, k in ((5, 6, 16, 10), (7, 40, 44, 10), (3, 9, 13, 7), (4, 3, 5, 12),
+                       (2, 300, 44, 10), (3, 128, 24, 100), (2, 1, 1, 1), (6, 64, 12, 10)):
+        kk = min(k, L)
+        note("merge in place", Q, V, L, k)
+        pool = max(8, V * kk // 3)
+        ids = rng.integers(-1, pool, (Q, V, L)).astype(np.int32)
+        base = rng.random(pool).astype(np.float32)
+        dist = np.where(ids >= 0, base[np.clip(ids, 0, None)], np.float32(3e38)).astype(np.float32)
+        gi, gd = to_gpu(ids, dist)
+        oi, od = E.merge_state(SimpleNamespace(ids=gi, dist=gd), k)
+        wi, wd = O.merge(np.ascontiguousarray(ids[..., :kk]),
+                         np.ascontiguousarray(dist[..., :kk]), k)
+        assert np.array_equal(oi.cpu().numpy(), wi), (Q, V, L, k)
+        assert od.cpu().numpy().tobytes() == wd.tobytes(), (Q, V, L, k)
+    with pytest.raises(RuntimeError):
+        E.merge_state(SimpleNamespace(ids=gi, dist=gd), V * L + 1)
+
+
 def test_merge_keeps_the_reference_quirks():
     """Hand cases of the (distance, id) walk with the predecessor rule of
     local_search.cu:903-910: an id seen again at a larger distance is dropped

@@ -118,6 +118,10 @@ def test_product_refuses_cpu_tensors():
         E.init_states(X, X[:2].clone(), torch.zeros((2, 1), dtype=torch.int32), D=4)
     with pytest.raises(RuntimeError):
         E.merge_branches(torch.zeros((2, 3, 4), dtype=torch.int32), torch.zeros((2, 3, 4)), 4)
+    from types import SimpleNamespace
+    with pytest.raises(RuntimeError):
+        E.merge_state(SimpleNamespace(ids=torch.zeros((2, 3, 4), dtype=torch.int32),
+                                      dist=torch.zeros((2, 3, 4))), 4)
 
 
 def test_no_oracle_in_the_product():
