@@ -398,9 +398,9 @@ def search(X, G, Qv, seeds, k=10, L=16, B=16, metric=METRIC_IP, team_size=32,
            policy=POLICY_BEST, stop_eps=-1.0, shared_cache=False, shared_bound=False,
            exclusive=False, stall_patience=0, crowd_frac=0.0, elide_visited=False, chunk=0,
            codes=None, check=None, cache_slots=None, claim_bits=False):
-    """init -> advance(budget) -> per-branch best-k -> merged top-k
-    (swann/_engine.py:428-447).  `check` overrides the global overflow guard:
-    True checks synchronously, False skips it."""
+    """init -> advance(budget) -> merged top-k of the branches' best k, read
+    from their queues in place (swann/_engine.py:428-447).  `check` overrides
+    the global overflow guard: True checks synchronously, False skips it."""
     st = init_states(X, Qv, seeds, L=L, B=B, D=G.shape[1], metric=metric, team_size=team_size,
                      policy=policy, stop_eps=stop_eps, kstop=k, shared_cache=shared_cache,
                      shared_bound=shared_bound, exclusive=exclusive,

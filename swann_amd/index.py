@@ -101,7 +101,7 @@ class Index:
         return self._search_device(Q, k, cfg)
 
     def _search_device(self, Q: torch.Tensor, k: int, cfg: SearchConfig):
-        """select -> seeds -> init -> advance -> top-k -> merge -> overflow,
+        """select -> seeds -> init -> advance -> merge -> overflow,
         all stream-ordered device work with no host synchronisation (so it can
         be captured)."""
         entries = S.select_nearest_i32(Q, self._cat, cfg.branches, metric=self._m)
@@ -220,7 +220,7 @@ class CapturedSearch:
     (`torch.cuda.CUDAGraph`) and replayed.
 
     Every kernel of the search (selection GEMM and top-k, seed gather, branch
-    init, advance, per-branch top-k, merge, overflow count) is one node; the
+    init, advance, merge of the branches' best k, overflow count) is one node; the
     state, table, workspace and outputs live in the graph's private memory
     pool and are reused by every replay.  The overflow guard is not applied:
     `overflow` is a device scalar the caller may read when it likes.  Nothing
